@@ -1,0 +1,369 @@
+/*
+ * vestra_hip.h -- C ABI of the MI355X (gfx950) fused ViT-block operations.
+ *
+ * This is the drop-in boundary for the Depth-Anything-3 ViT block's fused
+ * per-token path.  It mirrors the device runtime the reference engine calls
+ * (`vestra_kernels::cuda::CudaRuntime`, used by
+ * crates/da-engine/src/vit_block.rs:136-667 and
+ * crates/da-engine/src/patch_embed.rs:139-245), so a Rust `extern "C"` binding
+ * can stand where the CUDA runtime stood.  Every entry point names the
+ * reference method it replaces.
+ *
+ * Conventions
+ *  - Plain C types only: opaque handles, pointers and sizes.  No C++ or torch
+ *    types cross this boundary.
+ *  - Every function returns an `int` status (VK_OK == 0, negative on error)
+ *    and never aborts.  The message of the last failure on the calling host
+ *    thread is returned by vk_last_error().  VK_ERR_UNSUPPORTED marks a shape
+ *    or option outside the kernels' qualified subset: a caller maps it to the
+ *    reference's `None` (fall back to the CPU path), see vit_block.rs:331-333.
+ *  - One HIP stream per runtime.  Device work is stream-ordered and
+ *    asynchronous; vk_download_*, vk_runtime_synchronize and
+ *    vk_event_elapsed_ms block.  A runtime must not be used from two host
+ *    threads at once without external locking; separate runtimes are
+ *    independent.
+ *  - Tensors are flat, contiguous, typed device buffers (f32, f16 or u8).
+ *    Creators allocate; every creator has a matching destroy.  In-place
+ *    operations take the tensor handle they modify; the reference's
+ *    "consume and return the token tensor" (vit_block.rs:489-499,563) is
+ *    "in place on the same handle" here.
+ *  - Activations are f32.  Parameter vectors (LayerNorm/QK-norm gamma and
+ *    beta, LayerScale gamma) may be f32 or f16 (GGUF F16 element layout,
+ *    crates/da-gguf/src/reader.rs:303-318); f16 is widened exactly in
+ *    registers, so results equal the f32 path on the widened values.
+ */
+#ifndef VESTRA_HIP_H
+#define VESTRA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VK_ABI_VERSION 1
+
+typedef enum vk_status {
+  VK_OK = 0,
+  VK_ERR_INVALID = -1,     /* bad handle, null pointer, size mismatch      */
+  VK_ERR_UNSUPPORTED = -2, /* outside the qualified shape/option subset   */
+  VK_ERR_HIP = -3,         /* HIP runtime error                            */
+  VK_ERR_OOM = -4          /* device allocation failed                      */
+} vk_status;
+
+typedef enum vk_dtype { VK_F32 = 0, VK_F16 = 1, VK_U8 = 2 } vk_dtype;
+
+typedef struct vk_runtime vk_runtime;
+typedef struct vk_tensor vk_tensor;
+typedef struct vk_linear vk_linear;
+typedef struct vk_event vk_event;
+typedef struct vk_graph vk_graph;
+
+/* ------------------------------------------------------------------ */
+/* errors, version                                                      */
+/* ------------------------------------------------------------------ */
+
+/* Message of the last failed call on this host thread ("" if none).
+ * Replaces the payload of `CudaError::Kernel(String)`
+ * (crates/da-engine/src/patch_embed.rs:207-217). */
+const char* vk_last_error(void);
+int vk_abi_version(void);
+
+/* ------------------------------------------------------------------ */
+/* runtime                                                              */
+/* ------------------------------------------------------------------ */
+
+/* CudaRuntime::new(device) (engine.rs:284-385 enable_cuda_*). */
+int vk_runtime_create(int device, vk_runtime** out);
+int vk_runtime_destroy(vk_runtime* rt);
+/* Blocks until all work queued on the runtime's stream has finished. */
+int vk_runtime_synchronize(vk_runtime* rt);
+/* The runtime's hipStream_t, for callers that enqueue their own work. */
+void* vk_runtime_stream(vk_runtime* rt);
+/* Number of compute units of the runtime's device (0 on error). */
+int vk_runtime_cu_count(vk_runtime* rt);
+
+/* ------------------------------------------------------------------ */
+/* tensors and transfers                                                */
+/* ------------------------------------------------------------------ */
+
+/* Uninitialised device tensor of `len` elements. */
+int vk_tensor_alloc(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** out);
+/* Non-owning view of caller-owned device memory (destroy frees the handle
+ * only). */
+int vk_tensor_wrap(vk_runtime* rt, vk_dtype dtype, void* device_ptr, size_t len,
+                   vk_tensor** out);
+int vk_tensor_destroy(vk_tensor* t);
+size_t vk_tensor_len(const vk_tensor* t);
+int vk_tensor_dtype(const vk_tensor* t);
+void* vk_tensor_device_ptr(const vk_tensor* t);
+
+/* CudaRuntime::upload_f32 (vit_block.rs:161-184, 335). Synchronous. */
+int vk_upload_f32(vk_runtime* rt, const float* host, size_t len, vk_tensor** out);
+int vk_upload_f16(vk_runtime* rt, const uint16_t* host, size_t len, vk_tensor** out);
+int vk_upload_u8(vk_runtime* rt, const uint8_t* host, size_t len, vk_tensor** out);
+/* Host -> existing tensor (len must equal the tensor length). Synchronous. */
+int vk_write_f32(vk_runtime* rt, vk_tensor* t, const float* host, size_t len);
+int vk_write_u8(vk_runtime* rt, vk_tensor* t, const uint8_t* host, size_t len);
+/* CudaRuntime::download_f32 (vit_block.rs:370, 659-662). Blocks. */
+int vk_download_f32(vk_runtime* rt, const vk_tensor* t, float* host, size_t len);
+/* CudaRuntime::copy_f32 (backbone.rs:991-1027). New tensor. */
+int vk_copy_f32(vk_runtime* rt, const vk_tensor* src, vk_tensor** out);
+/* CudaRuntime::copy_segment_f32: new tensor = src[offset .. offset+len]. */
+int vk_copy_segment_f32(vk_runtime* rt, const vk_tensor* src, size_t offset,
+                        size_t len, vk_tensor** out);
+/* CudaRuntime::copy_segment_into_f32: dst[dst_off..+len] = src[src_off..+len]. */
+int vk_copy_segment_into_f32(vk_runtime* rt, vk_tensor* dst, size_t dst_offset,
+                             const vk_tensor* src, size_t src_offset, size_t len);
+/* CudaRuntime::overwrite_prefix_f32 (vit_block.rs:452-478): tokens[0..len] =
+ * prefix[0..len] -- the camera-token slot write. */
+int vk_overwrite_prefix_f32(vk_runtime* rt, vk_tensor* tokens,
+                            const vk_tensor* prefix, size_t len);
+
+/* ------------------------------------------------------------------ */
+/* fused per-token operations                                            */
+/* ------------------------------------------------------------------ */
+
+/* CudaRuntime::layernorm_f32_cpu_order(x, gamma, beta, rows, cols, eps)
+ * (vit_block.rs:528-537, 567-576, 627-636): row LayerNorm, biased two-pass
+ * variance, y = (x-mean)*inv*gamma + beta.  Returns a new tensor.  The
+ * reduction is a wave-level tree (not the CPU's sequential order); results
+ * match the CPU within rtol 1e-5.  cols % 4 == 0, cols <= 8192. */
+int vk_layernorm_f32(vk_runtime* rt, const vk_tensor* x, const vk_tensor* gamma,
+                     const vk_tensor* beta, size_t rows, size_t cols, float eps,
+                     vk_tensor** out);
+/* Same into an existing tensor (out may equal x: in place, as
+ * scalar::layernorm in vit_block.rs:712). */
+int vk_layernorm_into_f32(vk_runtime* rt, const vk_tensor* x,
+                          const vk_tensor* gamma, const vk_tensor* beta,
+                          size_t rows, size_t cols, float eps, vk_tensor* out);
+
+/* CudaRuntime::gelu_f32_in_place (vit_block.rs:578, 642): exact-erf GELU
+ * 0.5*x*(1+erf(x/sqrt2)) with the erf of the reference's scalar kernel
+ * (Abramowitz-Stegun 7.1.26, docs/plans/2026-07-18-rust-engine-v1.md:870-876). */
+int vk_gelu_f32_inplace(vk_runtime* rt, vk_tensor* x);
+/* Same with the device library's erff in place of A&S 7.1.26. */
+int vk_gelu_erf_f32_inplace(vk_runtime* rt, vk_tensor* x);
+
+/* CudaRuntime::add_f32_in_place (vit_block.rs:564, 580, 660): dst += src. */
+int vk_add_f32_inplace(vk_runtime* rt, vk_tensor* dst, const vk_tensor* src);
+/* scalar::layerscale (vit_block.rs:755-759; graph.rs:58-66): x[r,c] *= g[c]. */
+int vk_layerscale_f32_inplace(vk_runtime* rt, vk_tensor* x, const vk_tensor* gamma,
+                              size_t rows, size_t cols);
+/* LayerScale + residual, fused: x += gamma (.) y, as t = y*gamma; x = x + t
+ * (two roundings; the reference's LS-folded projection epilogue
+ * vit_block.rs:214-222,303-313 followed by add_f32_in_place).  gamma NULL
+ * means an unscaled residual add (presence gating, vit_block.rs:740-748). */
+int vk_layerscale_residual_f32(vk_runtime* rt, vk_tensor* x, const vk_tensor* y,
+                               const vk_tensor* gamma, size_t rows, size_t cols);
+/* LayerScale + residual followed by the next LayerNorm in one pass:
+ * x += gamma (.) y; ln_out = LayerNorm(x).  Equal to
+ * vk_layerscale_residual_f32 then vk_layernorm_into_f32 (the block's
+ * add_residual -> LN2 step, vit_block.rs:1090-1106; and the LS2 residual ->
+ * next block's LN1).  No reference counterpart as one call. */
+int vk_layerscale_residual_layernorm_f32(vk_runtime* rt, vk_tensor* x,
+                                         const vk_tensor* y,
+                                         const vk_tensor* ls_gamma,
+                                         const vk_tensor* ln_gamma,
+                                         const vk_tensor* ln_beta, size_t rows,
+                                         size_t cols, float eps,
+                                         vk_tensor* ln_out);
+
+/* CudaRuntime::qk_norm_rope_f32_da3_base(q, k, q_gamma, q_beta, k_gamma,
+ * k_beta, positions, heads, rows, freq, eps) (vit_block.rs:343-357, 543-557):
+ * in place on head-major q and k [heads, rows, 64]: LayerNorm over each
+ * (head, token) row of 64 with eps (QK_NORM_EPS = 1e-5, vit_block.rs:686),
+ * then 2D RoPE with positions [rows*2] (y, x) f32 on the device.  head_dim is
+ * 64 (the reference's da3_base qualification). */
+int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                        const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                        const vk_tensor* k_gamma, const vk_tensor* k_beta,
+                        const vk_tensor* positions, size_t heads, size_t rows,
+                        float freq, float eps);
+
+/* Layouts of q/k for the grid form below. */
+typedef enum vk_qk_layout {
+  /* [heads, view_count * tokens_per_view, head_dim]: one head-major sequence,
+   * the flattened multi-view layout of global layers (backbone.rs:770-796). */
+  VK_QK_HEADS_OUTER = 0,
+  /* [view_count, heads, tokens_per_view, head_dim]: one head-major block per
+   * view, i.e. view_count independent local-layer calls in one launch. */
+  VK_QK_VIEWS_OUTER = 1
+} vk_qk_layout;
+
+/* Q/K-norm + RoPE with positions computed on the device from the patch grid
+ * (vit_block.rs:841-881 / 512-526): per view, tokens < n_special get (0,0);
+ * patch p gets (p/gw+1, p%gw+1), or (1,1) for every patch when `global` is
+ * non-zero.  rows = view_count * (n_special + gh*gw).  Replaces the host
+ * position build + upload of run_tail_device (vit_block.rs:512-526, 542).
+ * q_gamma/q_beta/k_gamma/k_beta NULL skips the LayerNorm (qk-norm gating,
+ * vit_block.rs:835-838); head_dim == 64. */
+int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                             const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                             const vk_tensor* k_gamma, const vk_tensor* k_beta,
+                             size_t heads, size_t head_dim, size_t n_special,
+                             size_t gh, size_t gw, size_t view_count,
+                             int global, vk_qk_layout layout, float freq,
+                             float eps);
+
+/* Device positions tensor [rows*2] f32, as built on the host at
+ * vit_block.rs:512-526 (for callers of vk_qk_norm_rope_f32). */
+int vk_rope_positions_f32(vk_runtime* rt, size_t n_special, size_t gh,
+                          size_t gw, size_t view_count, int global,
+                          vk_tensor** out);
+
+/* ------------------------------------------------------------------ */
+/* patch embedding                                                      */
+/* ------------------------------------------------------------------ */
+
+/* CudaRuntime::patchify_nchw_f32(img, h, w, patch, channels)
+ * (patch_embed.rs:221-223): NCHW f32 -> patch rows [gh*gw, channels*p*p],
+ * column c*p*p + ky*p + kx. */
+int vk_patchify_nchw_f32(vk_runtime* rt, const vk_tensor* img, size_t h,
+                         size_t w, size_t patch, size_t channels,
+                         vk_tensor** out);
+
+/* CudaRuntime::prepare_linear_f32(in, out, W[in x out], bias, ls_gamma)
+ * (vit_block.rs:214-222, 303-313; patch_embed.rs:176-189): caches the
+ * weights on the device.  ls_gamma may be NULL.  Host pointers, synchronous. */
+int vk_linear_prepare_f32(vk_runtime* rt, size_t in_features,
+                          size_t out_features, const float* weight_in_out,
+                          const float* bias, const float* ls_gamma,
+                          vk_linear** out);
+/* The same from an OIHW conv filter [out, in] (patch_embed.rs:176-181 does
+ * this transpose on the host; here the kernel reads OIHW directly). */
+int vk_linear_prepare_oihw_f32(vk_runtime* rt, size_t in_features,
+                               size_t out_features, const float* weight_out_in,
+                               const float* bias, vk_linear** out);
+int vk_linear_destroy(vk_linear* lin);
+size_t vk_linear_input_features(const vk_linear* lin);
+/* CudaLinearF32::run(x, rows): y = (x @ W + b) [* gamma], F32 MFMA with f32
+ * accumulation.  New tensor [rows, out]. */
+int vk_linear_run_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                      size_t rows, vk_tensor** out);
+
+/* CudaRuntime::prepend_cls_add_pos_f32(patches, cls, pos, n_patches, embed)
+ * (patch_embed.rs:234-240): row 0 = cls + pos[0]; row 1+p = patch_p + pos[1+p]. */
+int vk_prepend_cls_add_pos_f32(vk_runtime* rt, const vk_tensor* patches,
+                               const vk_tensor* cls, const vk_tensor* pos,
+                               size_t n_patches, size_t embed, vk_tensor** out);
+
+/* PosEmbedCache::get_or_build / interpolate_pos_embed (pos_embed.rs:122-218):
+ * bicubic (Keys a=-0.75) resize of the learned [grid*grid+1, embed] table to
+ * [1+gh*gw, embed], CLS row passed through.  Bit-identical to the scalar
+ * restatement.  New tensor; callers cache it per (gh, gw). */
+int vk_pos_embed_bicubic_f32(vk_runtime* rt, const vk_tensor* pos_embed,
+                             size_t grid, size_t embed, size_t gh, size_t gw,
+                             float interp_offset, vk_tensor** out);
+
+/* The whole per-image token preparation in one kernel: u8 HWC image ->
+ * ImageNet-style normalisation (preprocess.rs:484-500) -> 14x14 unfold ->
+ * F32 MFMA projection with the OIHW filter held by `proj` (prepared with
+ * vk_linear_prepare_oihw_f32) + bias -> + position table -> token assembly
+ * [CLS+pos0, registers (no position), patches+pos] (pos_embed.rs:254-306).
+ * registers may be NULL when n_register == 0.  out has
+ * (1 + n_register + gh*gw) * embed elements. */
+int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h,
+                      size_t w, size_t patch, const float mean[3],
+                      const float std_[3], const vk_linear* proj,
+                      const vk_tensor* cls, const vk_tensor* registers,
+                      size_t n_register, const vk_tensor* pos_table,
+                      vk_tensor* out);
+
+/* ------------------------------------------------------------------ */
+/* one ViT block's fused-op sequence                                    */
+/* ------------------------------------------------------------------ */
+
+/* Model shape and options (the ModelConfig fields the path reads,
+ * crates/da-engine/src/config.rs:145-185). */
+typedef struct vk_vit_config {
+  size_t embed_dim;     /* D: 768 ViT-B, 1024 ViT-L                 */
+  size_t num_heads;     /* H                                        */
+  size_t head_dim;      /* 64                                       */
+  size_t mlp_hidden;    /* M: 3072 / 4096                           */
+  size_t num_register;  /* n_special = 1 + num_register             */
+  float ln_eps;         /* block LayerNorm eps (1e-6 for DA3)       */
+  float qk_norm_eps;    /* QK_NORM_EPS = 1e-5                       */
+  float rope_freq;      /* 100                                      */
+  int rope_start;       /* first layer with RoPE, -1 never          */
+  int qknorm_start;     /* first layer with Q/K-norm, -1 never      */
+  int alt_start;        /* first local/global alternation layer     */
+} vk_vit_config;
+
+/* Per-layer parameters (the vit.blk.{i}.* tensors of vit_block.rs:30-50).
+ * qnorm/knorm NULL: Q/K-norm skipped; ls1/ls2 NULL: unscaled residual. */
+typedef struct vk_vit_layer {
+  const vk_tensor* norm1_gamma;
+  const vk_tensor* norm1_beta;
+  const vk_tensor* qnorm_gamma;
+  const vk_tensor* qnorm_beta;
+  const vk_tensor* knorm_gamma;
+  const vk_tensor* knorm_beta;
+  const vk_tensor* ls1;
+  const vk_tensor* norm2_gamma;
+  const vk_tensor* norm2_beta;
+  const vk_tensor* ls2;
+} vk_vit_layer;
+
+/* Device activations of one block.  The GEMM/attention products between the
+ * fused operations (q, k, attn_proj, hidden, mlp_out) are produced by the
+ * caller's projections; this sequence owns the per-token work around them. */
+typedef struct vk_vit_activations {
+  vk_tensor* tokens;          /* [rows, D] residual stream, in/out        */
+  vk_tensor* ln1;             /* [rows, D] LN1 output                      */
+  vk_tensor* q;               /* [H, rows, 64] or per-view blocks          */
+  vk_tensor* k;
+  const vk_tensor* attn_proj; /* [rows, D] attention output projection     */
+  vk_tensor* ln2;             /* [rows, D] LN2 output                      */
+  vk_tensor* hidden;          /* [rows, M] FC1 output, GELU in place       */
+  const vk_tensor* mlp_out;   /* [rows, D] FC2 output                      */
+} vk_vit_activations;
+
+#define VK_BLOCK_FUSE_LS_LN 1u      /* fuse LS1+res with LN2              */
+#define VK_BLOCK_SKIP_LN1 2u        /* LN1 already produced (by the previous
+                                       block's fused LS2+res+LN1)          */
+#define VK_BLOCK_FUSE_NEXT_LN1 4u   /* finish with LS2+res fused with the next
+                                       block's LN1 (next_layer required)   */
+
+/* One DA3 ViT block's fused per-token operations, in the reference order of
+ * run_tail_device (vit_block.rs:489-582) and vit_block_with_views
+ * (vit_block.rs:1019-1139):
+ *   [camera overwrite at alt_start] -> LN1 -> Q/K-norm + RoPE (gated by
+ *   qknorm_start / rope_start; positions per view, global layers (1,1)) ->
+ *   tokens += ls1 (.) attn_proj -> LN2 -> GELU(hidden) ->
+ *   tokens += ls2 (.) mlp_out [-> next block's LN1].
+ * Every view of a multi-view batch is processed in one launch per operation
+ * (rows = view_count * tokens_per_view, view-major); q/k use
+ * VK_QK_HEADS_OUTER for global layers and VK_QK_VIEWS_OUTER for local ones.
+ * camera: [2*D] (reference view slot 0, source views slot 1,
+ * backbone.rs:746-768) or NULL when alt_start < 0. */
+int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
+                           size_t layer_idx, const vk_vit_layer* layer,
+                           const vk_vit_layer* next_layer,
+                           const vk_vit_activations* act, size_t gh, size_t gw,
+                           size_t view_count, const vk_tensor* camera,
+                           unsigned flags);
+
+/* ------------------------------------------------------------------ */
+/* timing and graphs                                                    */
+/* ------------------------------------------------------------------ */
+
+int vk_event_create(vk_runtime* rt, vk_event** out);
+int vk_event_destroy(vk_event* ev);
+/* Records on the runtime's stream. */
+int vk_event_record(vk_runtime* rt, vk_event* ev);
+/* Blocks until `stop` completes; milliseconds between the two events. */
+int vk_event_elapsed_ms(vk_event* start, vk_event* stop, float* ms);
+
+/* Stream capture of everything the runtime enqueues between begin and end
+ * into a HIP graph, replayed with vk_graph_launch. */
+int vk_graph_begin_capture(vk_runtime* rt);
+int vk_graph_end_capture(vk_runtime* rt, vk_graph** out);
+int vk_graph_launch(vk_runtime* rt, vk_graph* g);
+int vk_graph_destroy(vk_graph* g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VESTRA_HIP_H */

@@ -1,0 +1,315 @@
+"""The oracle: numpy front end of the scalar CPU restatement (vestra_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  This package is the checker that the HIP library
+is compared against.  It is imported by tests/, by __graft_entry__.smoke() to
+check one small GPU invocation, and by bench.py's cpu_baseline leg (which
+times it as the reported CPU baseline).  The product path never imports it.
+
+Each wrapper names the reference function it restates; the C source cites
+file:line for every formula.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvestra_oracle.so")
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        build()
+    return C.CDLL(LIB_PATH)
+
+
+lib = _load()
+
+_vp, _sz, _i, _f = C.c_void_p, C.c_size_t, C.c_int, C.c_float
+_SIGS = {
+    "ora_set_threads": ([_i], None),
+    "ora_get_threads": ([], _i),
+    "ora_f16_to_f32": ([C.c_uint16], _f),
+    "ora_f16_to_f32_array": ([_vp, _vp, _sz], None),
+    "ora_layernorm_f32": ([_vp, _vp, _sz, _sz, _vp, _vp, _f], None),
+    "ora_layernorm_w16": ([_vp, _vp, _sz, _sz, _vp, _vp, _f], None),
+    "ora_erf_as7126": ([_f], _f),
+    "ora_gelu_f32": ([_vp, _sz], None),
+    "ora_gelu_erff_f32": ([_vp, _sz], None),
+    "ora_layerscale_f32": ([_vp, _sz, _sz, _vp], None),
+    "ora_add_f32": ([_vp, _vp, _sz], None),
+    "ora_layerscale_residual_f32": ([_vp, _vp, _vp, _sz, _sz], None),
+    "ora_layerscale_residual_w16": ([_vp, _vp, _vp, _sz, _sz], None),
+    "ora_rope_positions": ([_vp, _sz, _sz, _sz, _sz, _i], None),
+    "ora_rope_inv_freq": ([_vp, _sz, _f], None),
+    "ora_rope2d_f32": ([_vp, _sz, _sz, _sz, _vp, _f], None),
+    "ora_qk_norm_rope_f32": ([_vp] * 7 + [_sz, _sz, _sz, _f, _f], None),
+    "ora_qk_norm_rope_w16": ([_vp] * 7 + [_sz, _sz, _sz, _f, _f], None),
+    "ora_normalize_u8_hwc": ([_vp, _vp, _sz, _sz, _vp, _vp], None),
+    "ora_patchify_nchw": ([_vp, _vp, _sz, _sz, _sz, _sz], None),
+    "ora_linear_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz], None),
+    "ora_patch_project_oihw": ([_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp], None),
+    "ora_pos_embed_bicubic": ([_vp, _sz, _sz, _sz, _sz, _f, _vp], None),
+    "ora_assemble_tokens": ([_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp], None),
+    "ora_patch_embed_u8": ([_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _sz, _vp,
+                            _vp], None),
+    "ora_overwrite_prefix_f32": ([_vp, _vp, _sz], None),
+}
+for _n, (_a, _r) in _SIGS.items():
+    _fn = getattr(lib, _n)
+    _fn.argtypes = _a
+    _fn.restype = _r
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a: np.ndarray):
+    # data_as keeps a reference to the array alive as long as the pointer
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def set_threads(n: int) -> None:
+    lib.ora_set_threads(int(n))
+
+
+def f16_bits(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float16).view(np.uint16)
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib.ora_f16_to_f32_array(_p(b), _p(out), b.size)
+    return out
+
+
+def layernorm(x, gamma, beta, eps: float) -> np.ndarray:
+    """scalar::layernorm over the last axis (vit_block.rs:696-714)."""
+    x = _f32(x)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    out = np.empty_like(x)
+    if np.asarray(gamma).dtype == np.float16:
+        g, b = f16_bits(gamma), f16_bits(beta)
+        lib.ora_layernorm_w16(_p(x), _p(out), rows, cols, _p(g), _p(b), eps)
+    else:
+        g, b = _f32(gamma), _f32(beta)
+        lib.ora_layernorm_f32(_p(x), _p(out), rows, cols, _p(g), _p(b), eps)
+    return out
+
+
+def gelu(x) -> np.ndarray:
+    """Kernels::gelu with A&S 7.1.26 erf (plans:865-876), returns a copy."""
+    y = _f32(x).copy()
+    lib.ora_gelu_f32(_p(y), y.size)
+    return y
+
+
+def gelu_erff(x) -> np.ndarray:
+    y = _f32(x).copy()
+    lib.ora_gelu_erff_f32(_p(y), y.size)
+    return y
+
+
+def erf_as7126(x: float) -> float:
+    return float(lib.ora_erf_as7126(float(x)))
+
+
+def layerscale(x, gamma) -> np.ndarray:
+    y = _f32(x).copy()
+    cols = y.shape[-1]
+    lib.ora_layerscale_f32(_p(y), y.size // cols, cols, _p(_f32(gamma)))
+    return y
+
+
+def add(dst, src) -> np.ndarray:
+    d = _f32(dst).copy()
+    s = _f32(src)
+    lib.ora_add_f32(_p(d), _p(s), d.size)
+    return d
+
+
+def layerscale_residual(x, y, gamma) -> np.ndarray:
+    """x + y*gamma with two roundings (vit_block.rs:755-758 then add_residual)."""
+    out = _f32(x).copy()
+    yv = _f32(y)
+    cols = out.shape[-1]
+    if gamma is None:
+        lib.ora_add_f32(_p(out), _p(yv), out.size)
+    elif np.asarray(gamma).dtype == np.float16:
+        lib.ora_layerscale_residual_w16(_p(out), _p(yv), _p(f16_bits(gamma)), out.size // cols, cols)
+    else:
+        lib.ora_layerscale_residual_f32(_p(out), _p(yv), _p(_f32(gamma)), out.size // cols, cols)
+    return out
+
+
+def rope_positions(n_special: int, gh: int, gw: int, view_count: int, global_layer: bool) -> np.ndarray:
+    """Position builder of vit_block.rs:841-881, [rows, 2] f32 (y, x)."""
+    rows = (n_special + gh * gw) * view_count
+    out = np.empty((rows, 2), np.float32)
+    lib.ora_rope_positions(_p(out), n_special, gh, gw, view_count, 1 if global_layer else 0)
+    return out
+
+
+def rope_inv_freq(head_dim: int, base: float = 100.0) -> np.ndarray:
+    out = np.empty(head_dim // 4, np.float32)
+    lib.ora_rope_inv_freq(_p(out), head_dim, base)
+    return out
+
+
+def rope2d(x, heads: int, n: int, head_dim: int, pos_yx, base: float = 100.0) -> np.ndarray:
+    """vestra_kernels::rope2d on [heads, n, head_dim] (returns a copy)."""
+    y = _f32(x).copy()
+    pos = np.ascontiguousarray(pos_yx, dtype=np.int64)
+    lib.ora_rope2d_f32(_p(y), heads, n, head_dim, _p(pos), base)
+    return y
+
+
+def qk_norm_rope(q, k, qg, qb, kg, kb, pos_yx, heads: int, n: int, head_dim: int = 64,
+                 base: float = 100.0, eps: float = 1e-5):
+    """qk_norm_rope_f32_da3_base (vit_block.rs:911-924), returns (q, k) copies."""
+    qo, ko = _f32(q).copy(), _f32(k).copy()
+    pos = _f32(pos_yx)
+    if np.asarray(qg).dtype == np.float16:
+        args = [f16_bits(a) for a in (qg, qb, kg, kb)]
+        lib.ora_qk_norm_rope_w16(_p(qo), _p(ko), *[_p(a) for a in args], _p(pos), heads, n,
+                                 head_dim, base, eps)
+    else:
+        args = [_f32(a) for a in (qg, qb, kg, kb)]
+        lib.ora_qk_norm_rope_f32(_p(qo), _p(ko), *[_p(a) for a in args], _p(pos), heads, n,
+                                 head_dim, base, eps)
+    return qo, ko
+
+
+def normalize_u8_hwc(img, mean, std) -> np.ndarray:
+    img = np.ascontiguousarray(img, dtype=np.uint8)
+    h, w, _ = img.shape
+    out = np.empty((3, h, w), np.float32)
+    m, s = _f32(mean), _f32(std)
+    lib.ora_normalize_u8_hwc(_p(img), _p(out), h, w, _p(m), _p(s))
+    return out
+
+
+def patchify_nchw(img, patch: int) -> np.ndarray:
+    img = _f32(img)
+    c, h, w = img.shape
+    out = np.empty(((h // patch) * (w // patch), c * patch * patch), np.float32)
+    lib.ora_patchify_nchw(_p(img), _p(out), h, w, patch, c)
+    return out
+
+
+def linear(x, w_kn, bias) -> np.ndarray:
+    """run_linear without LayerScale: x @ W[k, n] + b, sequential k."""
+    x, w = _f32(x), _f32(w_kn)
+    m, k = x.shape
+    n = w.shape[1]
+    out = np.empty((m, n), np.float32)
+    lib.ora_linear_f32(_p(x), _p(w), _p(_f32(bias)) if bias is not None else None, _p(out), m, k, n)
+    return out
+
+
+def patch_project_oihw(img_chw, patch: int, w_oihw, bias) -> np.ndarray:
+    img = _f32(img_chw)
+    _, h, w = img.shape
+    wt = _f32(w_oihw)
+    embed = wt.shape[0]
+    out = np.empty(((h // patch) * (w // patch), embed), np.float32)
+    lib.ora_patch_project_oihw(_p(img), h, w, patch, _p(wt), _p(_f32(bias)), embed, _p(out))
+    return out
+
+
+def pos_embed_bicubic(pos_embed, grid: int, embed: int, gh: int, gw: int,
+                      interp_offset: float = 0.1) -> np.ndarray:
+    """interpolate_pos_embed (pos_embed.rs:122-169)."""
+    src = _f32(pos_embed)
+    out = np.empty((1 + gh * gw, embed), np.float32)
+    lib.ora_pos_embed_bicubic(_p(src), grid, embed, gh, gw, interp_offset, _p(out))
+    return out
+
+
+def assemble_tokens(patch_tokens, gh: int, gw: int, cls, registers, pos_table) -> np.ndarray:
+    pt = _f32(patch_tokens)
+    embed = pt.shape[-1]
+    nreg = 0 if registers is None else int(np.asarray(registers).size // embed)
+    regs = None if registers is None else _f32(registers)
+    out = np.empty((1 + nreg + gh * gw, embed), np.float32)
+    lib.ora_assemble_tokens(_p(pt), gh, gw, embed, _p(_f32(cls)), _p(regs), nreg,
+                            _p(_f32(pos_table)), _p(out))
+    return out
+
+
+def patch_embed_u8(img_hwc, patch: int, mean, std, w_oihw, bias, cls, registers,
+                   pos_table) -> np.ndarray:
+    img = np.ascontiguousarray(img_hwc, dtype=np.uint8)
+    h, w, _ = img.shape
+    wt = _f32(w_oihw)
+    embed = wt.shape[0]
+    nreg = 0 if registers is None else int(np.asarray(registers).size // embed)
+    regs = None if registers is None else _f32(registers)
+    out = np.empty((1 + nreg + (h // patch) * (w // patch), embed), np.float32)
+    lib.ora_patch_embed_u8(_p(img), h, w, patch, _p(_f32(mean)), _p(_f32(std)), _p(wt),
+                           _p(_f32(bias)), embed, _p(_f32(cls)), _p(regs), nreg,
+                           _p(_f32(pos_table)), _p(out))
+    return out
+
+
+def block_fused_ops(tokens, q, k, attn_proj, hidden, mlp_out, layer: dict, cfg: dict,
+                    layer_idx: int, gh: int, gw: int, view_count: int, camera=None):
+    """One block's fused per-token sequence (vit_block.rs:1019-1139 order), on copies.
+
+    layer: dict of numpy parameter vectors (norm1_gamma, ..., ls2; absent or
+    None entries follow the reference's presence gating).  q/k layout: one
+    head-major sequence for global layers, per-view head-major blocks for local
+    ones.  Returns dict(tokens, ln1, q, k, ln2, hidden).
+    """
+    D = cfg["embed_dim"]
+    H = cfg["num_heads"]
+    hd = cfg["head_dim"]
+    n_special = 1 + cfg["num_register"]
+    tpv = n_special + gh * gw
+    rows = tpv * view_count
+    alt = cfg["alt_start"]
+    glob = alt >= 0 and layer_idx >= alt and layer_idx % 2 == 1
+    x = _f32(tokens).reshape(rows, D).copy()
+    if alt >= 0 and layer_idx == alt:
+        cam = _f32(camera).reshape(-1)
+        for v in range(view_count):
+            slot = 1 if v > 0 else 0
+            x[v * tpv] = cam[slot * D:(slot + 1) * D]
+    ln1 = layernorm(x, layer["norm1_gamma"], layer["norm1_beta"], cfg["ln_eps"])
+    qo = _f32(q).copy()
+    ko = _f32(k).copy()
+    use_qkn = cfg["qknorm_start"] >= 0 and layer_idx >= cfg["qknorm_start"] and \
+        layer.get("qnorm_gamma") is not None
+    use_rope = cfg["rope_start"] >= 0 and layer_idx >= cfg["rope_start"]
+    if use_rope or use_qkn:
+        pos = rope_positions(n_special, gh, gw, view_count, glob)
+        if glob:
+            blocks = [(qo.reshape(H, rows, hd), ko.reshape(H, rows, hd), pos)]
+        else:
+            qv = qo.reshape(view_count, H, tpv, hd)
+            kv = ko.reshape(view_count, H, tpv, hd)
+            blocks = [(qv[v], kv[v], pos[v * tpv:(v + 1) * tpv]) for v in range(view_count)]
+        for qb_, kb_, p in blocks:
+            n = qb_.shape[1]
+            if use_qkn:
+                qb_[...] = layernorm(qb_, layer["qnorm_gamma"], layer["qnorm_beta"], cfg["qk_norm_eps"])
+                kb_[...] = layernorm(kb_, layer["knorm_gamma"], layer["knorm_beta"], cfg["qk_norm_eps"])
+            if use_rope:
+                pi = p.astype(np.int64)
+                qb_[...] = rope2d(qb_, H, n, hd, pi, cfg["rope_freq"]).reshape(qb_.shape)
+                kb_[...] = rope2d(kb_, H, n, hd, pi, cfg["rope_freq"]).reshape(kb_.shape)
+    x = layerscale_residual(x, _f32(attn_proj).reshape(rows, D), layer.get("ls1"))
+    ln2 = layernorm(x, layer["norm2_gamma"], layer["norm2_beta"], cfg["ln_eps"])
+    hid = gelu(hidden)
+    x = layerscale_residual(x, _f32(mlp_out).reshape(rows, D), layer.get("ls2"))
+    return {"tokens": x, "ln1": ln1, "q": qo, "k": ko, "ln2": ln2, "hidden": hid}

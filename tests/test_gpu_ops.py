@@ -1,0 +1,259 @@
+"""GPU parity of the fused per-token operations against the oracle.
+
+Every test calls the HIP kernels through the C ABI (vestra_hip ->
+libvestra_hip.so) on seeded inputs and compares with the scalar CPU oracle:
+  * bit-exact where the operation order is the same (LayerScale+residual,
+    residual add, LayerScale, RoPE positions, bicubic table, patchify,
+    token assembly, RoPE of already-normalised rows);
+  * |got - ref| <= atol + rtol*|ref| with rtol 1e-5 / atol 1e-6 for F32
+    where the GPU reduces in a different order (LayerNorm mean/variance) or
+    uses the device exp / erf, and rtol 2e-3 / atol 2e-3 for F16-stored
+    parameters with F32 accumulation.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import F32_ATOL, F32_RTOL, W16_ATOL, W16_RTOL, assert_parity
+
+pytestmark = pytest.mark.gpu
+
+vh = pytest.importorskip("vestra_hip")
+
+
+def normals(rng, *shape, scale=1.0, shift=0.0):
+    return (shift + scale * rng.standard_normal(shape)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("rows,cols", [(5, 8), (1, 768), (866, 768), (865, 768),
+                                       (10392, 768), (3458, 1024), (37, 64), (3, 1300)])
+def test_layernorm_matches_oracle(rt, rng, rows, cols):
+    x = normals(rng, rows, cols)
+    g = normals(rng, cols, scale=0.02, shift=1.0)
+    b = normals(rng, cols, scale=0.02)
+    out = rt.layernorm_f32_cpu_order(rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b),
+                                     rows, cols, 1e-6).numpy()
+    assert_parity(out, oracle.layernorm(x, g, b, 1e-6), F32_ATOL, F32_RTOL, f"ln {rows}x{cols}")
+
+
+def test_layernorm_in_place_and_f16_params(rt, rng):
+    rows, cols = 3458, 1024
+    x = normals(rng, rows, cols)
+    g = normals(rng, cols, scale=0.02, shift=1.0).astype(np.float16)
+    b = normals(rng, cols, scale=0.02).astype(np.float16)
+    t = rt.upload_f32(x)
+    rt.layernorm_into_f32(t, rt.upload_f16(g), rt.upload_f16(b), rows, cols, 1e-6, t)
+    ref = oracle.layernorm(x, g, b, 1e-6)
+    assert_parity(t.numpy(), ref, F32_ATOL, F32_RTOL, "ln in place f16 params")
+    assert_parity(t.numpy(), ref, W16_ATOL, W16_RTOL, "ln f16 bar")
+
+
+def test_layernorm_rejects_bad_shapes(rt, rng):
+    x = rt.upload_f32(normals(rng, 4, 6))
+    g = rt.upload_f32(np.ones(6, np.float32))
+    with pytest.raises(vh.UnsupportedShape):
+        rt.layernorm_f32_cpu_order(x, g, g, 4, 6, 1e-6)   # cols % 4 != 0
+    with pytest.raises(vh.VestraError) as e:
+        rt.layernorm_f32_cpu_order(x, g, g, 5, 6, 1e-6)   # size mismatch
+    assert e.value.code == vh.VK_ERR_INVALID and "rows*cols" in e.value.message
+
+
+def test_layernorm_empty_rows(rt):
+    g = rt.upload_f32(np.ones(8, np.float32))
+    out = rt.layernorm_f32_cpu_order(rt.alloc_f32(0), g, g, 0, 8, 1e-6)
+    assert len(out) == 0
+
+
+# ---------------------------------------------------------------- GELU
+@pytest.mark.parametrize("n", [866 * 3072, 1, 2, 3, 5, 4099, 3458 * 4096])
+def test_gelu_matches_oracle(rt, rng, n):
+    x = normals(rng, n)
+    if n > 8:
+        x[:8] = [0.0, -0.0, 10.0, -10.0, 1e-30, -5.5, 30.0, -30.0]
+    t = rt.upload_f32(x)
+    rt.gelu_f32_in_place(t)
+    assert_parity(t.numpy(), oracle.gelu(x), F32_ATOL, F32_RTOL, f"gelu n={n}")
+
+
+def test_gelu_erf_variant_matches_oracle(rt, rng):
+    x = normals(rng, 866 * 3072, scale=2.0)
+    t = rt.upload_f32(x)
+    rt.gelu_erf_f32_in_place(t)
+    assert_parity(t.numpy(), oracle.gelu_erff(x), F32_ATOL, F32_RTOL, "gelu erff")
+
+
+def test_gelu_empty(rt):
+    t = rt.alloc_f32(0)
+    rt.gelu_f32_in_place(t)
+
+
+# ---------------------------------------------------------------- LayerScale / residual
+@pytest.mark.parametrize("rows,cols", [(866, 768), (10392, 768), (3458, 1024), (3, 4), (7, 12)])
+def test_layerscale_residual_bit_exact(rt, rng, rows, cols):
+    x = normals(rng, rows, cols)
+    y = normals(rng, rows, cols)
+    g = rng.uniform(0, 0.1, cols).astype(np.float32)
+    t = rt.upload_f32(x)
+    rt.layerscale_residual_f32(t, rt.upload_f32(y), rt.upload_f32(g), rows, cols)
+    assert np.array_equal(t.numpy().reshape(rows, cols), oracle.layerscale_residual(x, y, g))
+
+
+def test_layerscale_residual_f16_gamma_and_absent_gamma(rt, rng):
+    rows, cols = 3458, 1024
+    x, y = normals(rng, rows, cols), normals(rng, rows, cols)
+    g16 = rng.uniform(0, 0.1, cols).astype(np.float16)
+    t = rt.upload_f32(x)
+    rt.layerscale_residual_f32(t, rt.upload_f32(y), rt.upload_f16(g16), rows, cols)
+    assert np.array_equal(t.numpy().reshape(rows, cols), oracle.layerscale_residual(x, y, g16))
+    t2 = rt.upload_f32(x)
+    rt.layerscale_residual_f32(t2, rt.upload_f32(y), None, rows, cols)
+    assert np.array_equal(t2.numpy().reshape(rows, cols), oracle.add(x, y))
+
+
+def test_add_and_layerscale_bit_exact(rt, rng):
+    x, y = normals(rng, 1001), normals(rng, 1001)   # odd length: scalar tail
+    t = rt.upload_f32(x)
+    rt.add_f32_in_place(t, rt.upload_f32(y))
+    assert np.array_equal(t.numpy(), oracle.add(x, y))
+    x2 = normals(rng, 6, 8)
+    g = normals(rng, 8)
+    t2 = rt.upload_f32(x2)
+    rt.layerscale_f32_in_place(t2, rt.upload_f32(g), 6, 8)
+    assert np.array_equal(t2.numpy().reshape(6, 8), oracle.layerscale(x2, g))
+
+
+def test_add_rejects_aliasing_and_mismatch(rt, rng):
+    t = rt.upload_f32(normals(rng, 16))
+    with pytest.raises(vh.VestraError):
+        rt.add_f32_in_place(t, t)
+    with pytest.raises(vh.VestraError):
+        rt.add_f32_in_place(t, rt.upload_f32(normals(rng, 15)))
+
+
+@pytest.mark.parametrize("with_ls", [True, False])
+def test_fused_layerscale_residual_layernorm(rt, rng, with_ls):
+    rows, cols = 10392, 768
+    x, y = normals(rng, rows, cols), normals(rng, rows, cols)
+    ls = rng.uniform(0, 0.1, cols).astype(np.float32)
+    g = normals(rng, cols, scale=0.02, shift=1.0)
+    b = normals(rng, cols, scale=0.02)
+    tx = rt.upload_f32(x)
+    out = rt.alloc_f32(rows * cols)
+    rt.layerscale_residual_layernorm_f32(tx, rt.upload_f32(y), rt.upload_f32(ls) if with_ls else None,
+                                         rt.upload_f32(g), rt.upload_f32(b), rows, cols, 1e-6, out)
+    x_ref = oracle.layerscale_residual(x, y, ls if with_ls else None)
+    assert np.array_equal(tx.numpy().reshape(rows, cols), x_ref)
+    assert_parity(out.numpy(), oracle.layernorm(x_ref, g, b, 1e-6), F32_ATOL, F32_RTOL,
+                  "ls+res+ln")
+
+
+# ---------------------------------------------------------------- Q/K norm + RoPE
+def qk_params(rng, dtype=np.float32):
+    return [normals(rng, 64, scale=0.02, shift=1.0 if i % 2 == 0 else 0.0).astype(dtype)
+            for i in range(4)]
+
+
+@pytest.mark.parametrize("n_special,gh,gw,glob", [(2, 24, 36, False), (1, 24, 36, False),
+                                                  (2, 24, 36, True), (1, 2, 2, False),
+                                                  (2, 48, 72, False)])
+def test_qk_norm_rope_reference_form(rt, rng, n_special, gh, gw, glob):
+    heads = 12
+    n = n_special + gh * gw
+    q, k = normals(rng, heads, n, 64), normals(rng, heads, n, 64)
+    qg, qb, kg, kb = qk_params(rng)
+    pos = oracle.rope_positions(n_special, gh, gw, 1, glob)
+    tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+    rt.qk_norm_rope_f32_da3_base(tq, tk, rt.upload_f32(qg), rt.upload_f32(qb),
+                                 rt.upload_f32(kg), rt.upload_f32(kb), rt.upload_f32(pos),
+                                 heads, n, 100.0, 1e-5)
+    rq, rk = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n)
+    assert_parity(tq.numpy(), rq, F32_ATOL, F32_RTOL, "q")
+    assert_parity(tk.numpy(), rk, F32_ATOL, F32_RTOL, "k")
+
+
+def test_rope_alone_is_bit_exact(rt, rng):
+    # without the LayerNorm the rotation itself has no reduction: the GPU
+    # must equal the oracle bit for bit (shared cos/sin rounding, no FMA)
+    heads, n_special, gh, gw = 12, 2, 24, 36
+    n = n_special + gh * gw
+    q, k = normals(rng, heads, n, 64), normals(rng, heads, n, 64)
+    tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+    rt.qk_norm_rope_grid_f32(tq, tk, None, None, None, None, heads, 64, n_special, gh, gw, 1,
+                             False, vh.VK_QK_HEADS_OUTER)
+    pos = oracle.rope_positions(n_special, gh, gw, 1, False).astype(np.int64)
+    assert np.array_equal(tq.numpy().reshape(heads, n, 64), oracle.rope2d(q, heads, n, 64, pos))
+    assert np.array_equal(tk.numpy().reshape(heads, n, 64), oracle.rope2d(k, heads, n, 64, pos))
+
+
+def test_rope_positions_beyond_the_table(rt, rng):
+    heads, n = 2, 6
+    q, k = normals(rng, heads, n, 64), normals(rng, heads, n, 64)
+    pos = np.array([[0, 0], [1, 1], [1023, 5], [1024, 1100], [2000, 7], [5, 4096]], np.float32)
+    tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+    rt.qk_norm_rope_f32_da3_base(tq, tk, None, None, None, None, rt.upload_f32(pos), heads, n)
+    ref = oracle.rope2d(q, heads, n, 64, pos.astype(np.int64))
+    assert_parity(tq.numpy(), ref, F32_ATOL, F32_RTOL, "rope large positions")
+
+
+@pytest.mark.parametrize("glob", [False, True])
+def test_qk_grid_multi_view_layouts(rt, rng, glob):
+    heads, n_special, gh, gw, views = 12, 2, 24, 36, 3
+    tpv = n_special + gh * gw
+    rows = tpv * views
+    q, k = normals(rng, rows * heads * 64), normals(rng, rows * heads * 64)
+    qg, qb, kg, kb = qk_params(rng)
+    layout = vh.VK_QK_HEADS_OUTER if glob else vh.VK_QK_VIEWS_OUTER
+    tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+    rt.qk_norm_rope_grid_f32(tq, tk, *[rt.upload_f32(a) for a in (qg, qb, kg, kb)], heads, 64,
+                             n_special, gh, gw, views, glob, layout)
+    pos = oracle.rope_positions(n_special, gh, gw, views, glob)
+    if glob:
+        rq, rk = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, rows)
+    else:
+        rq, rk = q.reshape(views, heads, tpv, 64).copy(), k.reshape(views, heads, tpv, 64).copy()
+        for v in range(views):
+            rq[v], rk[v] = [a.reshape(heads, tpv, 64) for a in oracle.qk_norm_rope(
+                rq[v], rk[v], qg, qb, kg, kb, pos[v * tpv:(v + 1) * tpv], heads, tpv)]
+    assert_parity(tq.numpy(), rq, F32_ATOL, F32_RTOL, "q multi-view")
+    assert_parity(tk.numpy(), rk, F32_ATOL, F32_RTOL, "k multi-view")
+
+
+def test_qk_single_view_layouts_agree(rt, rng):
+    heads, n_special, gh, gw = 12, 2, 6, 9
+    n = n_special + gh * gw
+    q, k = normals(rng, heads * n * 64), normals(rng, heads * n * 64)
+    params = [rt.upload_f32(a) for a in qk_params(rng)]
+    outs = []
+    for layout in (vh.VK_QK_HEADS_OUTER, vh.VK_QK_VIEWS_OUTER):
+        tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+        rt.qk_norm_rope_grid_f32(tq, tk, *params, heads, 64, n_special, gh, gw, 1, False, layout)
+        outs.append((tq.numpy(), tk.numpy()))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_qk_f16_params_vit_l(rt, rng):
+    heads, n_special, gh, gw = 16, 2, 48, 72
+    n = n_special + gh * gw
+    q, k = normals(rng, heads, n, 64), normals(rng, heads, n, 64)
+    qg, qb, kg, kb = qk_params(rng, np.float16)
+    tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+    rt.qk_norm_rope_grid_f32(tq, tk, *[rt.upload_f16(a) for a in (qg, qb, kg, kb)], heads, 64,
+                             n_special, gh, gw, 1, False, vh.VK_QK_HEADS_OUTER)
+    pos = oracle.rope_positions(n_special, gh, gw, 1, False)
+    rq, rk = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n)
+    assert_parity(tq.numpy(), rq, F32_ATOL, F32_RTOL, "q f16 params")
+    assert_parity(tk.numpy(), rk, F32_ATOL, F32_RTOL, "k f16 params")
+
+
+def test_qk_rejects_unqualified_head_dim(rt, rng):
+    t1, t2 = rt.upload_f32(normals(rng, 2 * 5 * 32)), rt.upload_f32(normals(rng, 2 * 5 * 32))
+    with pytest.raises(vh.UnsupportedShape):
+        rt.qk_norm_rope_grid_f32(t1, t2, None, None, None, None, 2, 32, 1, 2, 2, 1, False,
+                                 vh.VK_QK_HEADS_OUTER)
+
+
+def test_rope_positions_bit_exact(rt):
+    for args in ((2, 24, 36, 12, False), (2, 24, 36, 12, True), (1, 3, 5, 2, False)):
+        got = rt.rope_positions_f32(*args).numpy().reshape(-1, 2)
+        assert np.array_equal(got, oracle.rope_positions(*args))

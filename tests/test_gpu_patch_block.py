@@ -1,0 +1,298 @@
+"""GPU parity of patch embedding, the runtime surface and the block sequence.
+
+Patch projection runs on F32 MFMA with a different accumulation order than
+the oracle's sequential sum, so it is compared within rtol 1e-5 / atol 1e-6
+(F32 weights) or rtol 2e-3 / atol 2e-3 (F16-stored weights); everything
+without a reduction (patchify, bicubic table, token assembly, copies) is
+bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import F32_ATOL, F32_RTOL, assert_parity
+
+pytestmark = pytest.mark.gpu
+
+vh = pytest.importorskip("vestra_hip")
+
+MEAN = [0.485, 0.456, 0.406]
+STD = [0.229, 0.224, 0.225]
+
+
+def normals(rng, *shape, scale=1.0, shift=0.0):
+    return (shift + scale * rng.standard_normal(shape)).astype(np.float32)
+
+
+def assert_dot_parity(got, ref, scale, k, label):
+    """Parity for K-long f32 dot products accumulated in different orders
+    (sequential in the oracle, MFMA on the GPU): rtol 1e-5 / atol 1e-6 plus
+    the probabilistic rounding bound of either sum, sqrt(K) * 2^-24 *
+    sum_k |a_k w_k| per output, counted twice (both sides round)."""
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    scale = np.asarray(scale, np.float64).reshape(-1)
+    bound = F32_ATOL + F32_RTOL * np.abs(ref) + 2.0 * np.sqrt(k) * 2.0 ** -24 * scale
+    err = np.abs(got - ref)
+    worst = int(np.argmax(err / bound))
+    assert np.all(err <= bound), (f"[{label}] worst@{worst} got={got[worst]!r} "
+                                  f"ref={ref[worst]!r} err={err[worst]:.3e} "
+                                  f"bound={bound[worst]:.3e}")
+
+
+# ---------------------------------------------------------------- runtime
+def test_runtime_copies(rt, rng):
+    x = normals(rng, 3 * 768)
+    t = rt.upload_f32(x)
+    assert np.array_equal(rt.copy_f32(t).numpy(), x)
+    seg = rt.copy_segment_f32(t, 768, 768)
+    assert np.array_equal(seg.numpy(), x[768:1536])
+    dst = rt.upload_f32(np.zeros(4 * 768, np.float32))
+    rt.copy_segment_into_f32(dst, 768, t, 0, 3 * 768)
+    expect = np.zeros(4 * 768, np.float32)
+    expect[768:] = x
+    assert np.array_equal(dst.numpy(), expect)
+    cam = normals(rng, 768)
+    rt.overwrite_prefix_f32(t, rt.upload_f32(cam), 768)
+    assert np.array_equal(t.numpy()[:768], cam) and np.array_equal(t.numpy()[768:], x[768:])
+    with pytest.raises(vh.VestraError) as e:
+        rt.copy_segment_f32(t, 3 * 768, 1)
+    assert "outside" in e.value.message
+
+
+def test_events_and_graph_replays(rt, rng):
+    rows, cols = 866, 768
+    x, y = normals(rng, rows, cols), normals(rng, rows, cols)
+    g = rng.uniform(0, 0.1, cols).astype(np.float32)
+    tx, ty, tg = rt.upload_f32(x), rt.upload_f32(y), rt.upload_f32(g)
+    rt.synchronize()
+    rt.begin_capture()
+    rt.layerscale_residual_f32(tx, ty, tg, rows, cols)
+    graph = rt.end_capture()
+    expect = x.copy()
+    for _ in range(3):
+        graph.launch()
+        rt.synchronize()
+        expect = oracle.layerscale_residual(expect, y, g)
+        assert np.array_equal(tx.numpy().reshape(rows, cols), expect)
+        # eager work between replays
+        rt.add_f32_in_place(tx, ty)
+        expect = oracle.add(expect, y)
+    e0, e1 = rt.event(), rt.event()
+    e0.record()
+    graph.launch()
+    e1.record()
+    assert e0.elapsed_ms(e1) >= 0.0
+
+
+# ---------------------------------------------------------------- patch embedding pieces
+def test_patchify_bit_exact(rt, rng):
+    img = normals(rng, 3, 336, 504)
+    out = rt.patchify_nchw_f32(rt.upload_f32(img), 336, 504, 14, 3).numpy()
+    assert np.array_equal(out.reshape(864, 588), oracle.patchify_nchw(img, 14))
+
+
+def test_linear_patch_kats(rt):
+    # patch_embed.rs:280-339 through the split CUDA-shaped path:
+    # patchify -> linear (OIHW filter) -> tokens.  embed padded to 4 columns.
+    img = np.zeros((3, 4, 4), np.float32)
+    img[0] = np.arange(16, dtype=np.float32).reshape(4, 4)
+    w = np.zeros((4, 3, 2, 2), np.float32)
+    w[0, 0] = 1.0
+    lin = rt.prepare_linear_oihw_f32(12, 4, w, np.zeros(4, np.float32))
+    rows = rt.patchify_nchw_f32(rt.upload_f32(img), 4, 4, 2, 3)
+    out = lin.run(rows, 4).numpy().reshape(4, 4)
+    assert out[:, 0].tolist() == [10.0, 18.0, 42.0, 50.0]
+    lin0 = rt.prepare_linear_oihw_f32(12, 4, np.zeros((4, 3, 2, 2), np.float32),
+                                      np.array([1, 2, 3, 4], np.float32))
+    out0 = lin0.run(rt.patchify_nchw_f32(rt.upload_f32(np.ones((3, 4, 4), np.float32)), 4, 4, 2,
+                                         3), 4).numpy().reshape(4, 4)
+    assert (out0 == np.array([1, 2, 3, 4], np.float32)).all()
+
+
+@pytest.mark.parametrize("m,k,n,with_ls", [(864, 588, 768, False), (865, 768, 768, True),
+                                           (5, 13, 8, False), (3456, 588, 1024, False)])
+def test_linear_matches_oracle(rt, rng, m, k, n, with_ls):
+    x = normals(rng, m, k)
+    w = normals(rng, k, n, scale=0.02)
+    b = normals(rng, n, scale=0.02)
+    ls = rng.uniform(0, 0.1, n).astype(np.float32) if with_ls else None
+    lin = rt.prepare_linear_f32(k, n, w, b, ls)
+    assert lin.input_features() == k
+    out = lin.run(rt.upload_f32(x), m).numpy().reshape(m, n)
+    ref = oracle.linear(x, w, b)
+    if with_ls:
+        ref = oracle.layerscale(ref, ls)
+    scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64)
+    if with_ls:
+        scale = scale * ls
+    assert_dot_parity(out, ref, scale, k, f"linear {m}x{k}x{n}")
+
+
+def test_pos_embed_bicubic_bit_exact(rt, rng):
+    M, E = 37, 768
+    pe = normals(rng, M * M + 1, E, scale=0.02)
+    out = rt.pos_embed_bicubic_f32(rt.upload_f32(pe), M, E, 24, 36, 0.1).numpy()
+    assert np.array_equal(out.reshape(-1, E), oracle.pos_embed_bicubic(pe, M, E, 24, 36, 0.1))
+
+
+def test_prepend_cls_add_pos_bit_exact(rt, rng):
+    np_, E = 864, 768
+    patches, cls, pos = normals(rng, np_, E), normals(rng, E), normals(rng, np_ + 1, E)
+    out = rt.prepend_cls_add_pos_f32(rt.upload_f32(patches), rt.upload_f32(cls),
+                                     rt.upload_f32(pos), np_, E).numpy()
+    assert np.array_equal(out.reshape(-1, E), oracle.assemble_tokens(patches, 24, 36, cls, None, pos))
+
+
+# ---------------------------------------------------------------- fused patch embedding
+@pytest.mark.parametrize("h,w,embed,n_register", [(336, 504, 768, 1), (336, 504, 768, 0),
+                                                  (28, 42, 16, 0), (672, 1008, 1024, 1)])
+def test_patch_embed_u8_matches_oracle(rt, rng, h, w, embed, n_register):
+    gh, gw = h // 14, w // 14
+    img = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    wt = normals(rng, embed, 3, 14, 14, scale=0.02)
+    b = normals(rng, embed, scale=0.02)
+    cls = normals(rng, embed, scale=0.02)
+    regs = normals(rng, n_register, embed, scale=0.02) if n_register else None
+    pos = normals(rng, 1 + gh * gw, embed, scale=0.02)
+    proj = rt.prepare_linear_oihw_f32(588, embed, wt, b)
+    out = rt.alloc_f32((1 + n_register + gh * gw) * embed)
+    rt.patch_embed_u8(rt.upload_u8(img), h, w, 14, MEAN, STD, proj, rt.upload_f32(cls),
+                      rt.upload_f32(regs) if regs is not None else None, n_register,
+                      rt.upload_f32(pos), out)
+    ref = oracle.patch_embed_u8(img, 14, MEAN, STD, wt, b, cls, regs, pos)
+    got = out.numpy().reshape(ref.shape)
+    # special rows involve no reduction: bit-exact
+    assert np.array_equal(got[:1 + n_register], ref[:1 + n_register])
+    a = np.abs(oracle.patchify_nchw(oracle.normalize_u8_hwc(img, MEAN, STD), 14)).astype(np.float64)
+    scale = a @ np.abs(wt.reshape(embed, -1)).astype(np.float64).T
+    assert_dot_parity(got[1 + n_register:], ref[1 + n_register:], scale, 588,
+                      f"patch_embed {h}x{w}")
+
+
+def test_patch_embed_rejects_unqualified_patch(rt, rng):
+    img = rt.upload_u8(rng.integers(0, 256, (32, 32, 3), dtype=np.uint8))
+    proj = rt.prepare_linear_oihw_f32(3 * 16 * 16, 8, normals(rng, 8, 3, 16, 16), normals(rng, 8))
+    with pytest.raises(vh.UnsupportedShape):
+        rt.patch_embed_u8(img, 32, 32, 16, MEAN, STD, proj, rt.upload_f32(normals(rng, 8)), None,
+                          0, rt.upload_f32(normals(rng, 5, 8)), rt.alloc_f32(5 * 8))
+
+
+# ---------------------------------------------------------------- block sequence
+def make_block(rt, rng, D, H, M, rows, with_ls=True, with_qkn=True):
+    host = {
+        "norm1_gamma": normals(rng, D, scale=0.02, shift=1.0),
+        "norm1_beta": normals(rng, D, scale=0.02),
+        "norm2_gamma": normals(rng, D, scale=0.02, shift=1.0),
+        "norm2_beta": normals(rng, D, scale=0.02),
+    }
+    if with_qkn:
+        host.update({"qnorm_gamma": normals(rng, 64, scale=0.02, shift=1.0),
+                     "qnorm_beta": normals(rng, 64, scale=0.02),
+                     "knorm_gamma": normals(rng, 64, scale=0.02, shift=1.0),
+                     "knorm_beta": normals(rng, 64, scale=0.02)})
+    if with_ls:
+        host["ls1"] = rng.uniform(0, 0.1, D).astype(np.float32)
+        host["ls2"] = rng.uniform(0, 0.1, D).astype(np.float32)
+    dev = {k: rt.upload_f32(v) for k, v in host.items()}
+    return host, dev
+
+
+@pytest.mark.parametrize("views,layer_idx,flags", [
+    (1, 0, 0), (1, 4, vh.VK_BLOCK_FUSE_LS_LN), (3, 5, vh.VK_BLOCK_FUSE_LS_LN),
+    (3, 6, vh.VK_BLOCK_FUSE_LS_LN), (12, 7, vh.VK_BLOCK_FUSE_LS_LN)])
+def test_block_fused_ops_matches_oracle(rt, rng, views, layer_idx, flags):
+    D, H, M, nreg, gh, gw = 768, 12, 3072, 1, 24, 36
+    tpv = 1 + nreg + gh * gw
+    rows = tpv * views
+    cfg = dict(embed_dim=D, num_heads=H, head_dim=64, mlp_hidden=M, num_register=nreg,
+               ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0, rope_start=0, qknorm_start=0,
+               alt_start=4)
+    host, dev = make_block(rt, rng, D, H, M, rows)
+    tokens = normals(rng, rows, D)
+    q, k = normals(rng, rows * D), normals(rng, rows * D)
+    attn, mlp = normals(rng, rows, D), normals(rng, rows, D)
+    hidden = normals(rng, rows, M)
+    camera = normals(rng, 2 * D, scale=0.02)
+    act_t = {"tokens": rt.upload_f32(tokens), "ln1": rt.alloc_f32(rows * D),
+             "q": rt.upload_f32(q), "k": rt.upload_f32(k), "attn_proj": rt.upload_f32(attn),
+             "ln2": rt.alloc_f32(rows * D), "hidden": rt.upload_f32(hidden),
+             "mlp_out": rt.upload_f32(mlp)}
+    rt.vit_block_fused_ops(vh.VitConfig(**cfg), layer_idx, vh.layer_struct(**dev), None,
+                           vh.activations_struct(**act_t), gh, gw, views,
+                           rt.upload_f32(camera), flags)
+    ref = oracle.block_fused_ops(tokens, q, k, attn, hidden, mlp, host, cfg, layer_idx, gh, gw,
+                                 views, camera)
+    for name in ("tokens", "ln1", "q", "k", "ln2", "hidden"):
+        assert_parity(act_t[name].numpy(), ref[name], F32_ATOL, F32_RTOL,
+                      f"block {name} views={views} layer={layer_idx}")
+
+
+def test_block_gating_matches_reference_semantics(rt, rng):
+    # vit_block.rs:1403-1453: below qknorm_start/rope_start the Q/K path is
+    # untouched; ls absent -> unscaled residual (1368-1401).
+    D, H, M, gh, gw = 768, 12, 3072, 2, 3
+    rows = 1 + gh * gw
+    cfg = dict(embed_dim=D, num_heads=H, head_dim=64, mlp_hidden=M, num_register=0,
+               ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0, rope_start=1, qknorm_start=1,
+               alt_start=-1)
+    host, dev = make_block(rt, rng, D, H, M, rows, with_ls=False)
+    tokens, q, k = normals(rng, rows, D), normals(rng, rows * D), normals(rng, rows * D)
+    attn, mlp, hidden = normals(rng, rows, D), normals(rng, rows, D), normals(rng, rows, M)
+    for layer_idx in (0, 1):
+        act_t = {"tokens": rt.upload_f32(tokens), "ln1": rt.alloc_f32(rows * D),
+                 "q": rt.upload_f32(q), "k": rt.upload_f32(k), "attn_proj": rt.upload_f32(attn),
+                 "ln2": rt.alloc_f32(rows * D), "hidden": rt.upload_f32(hidden),
+                 "mlp_out": rt.upload_f32(mlp)}
+        rt.vit_block_fused_ops(vh.VitConfig(**cfg), layer_idx, vh.layer_struct(**dev), None,
+                               vh.activations_struct(**act_t), gh, gw, 1, None, 0)
+        ref = oracle.block_fused_ops(tokens, q, k, attn, hidden, mlp, host, cfg, layer_idx, gh,
+                                     gw, 1)
+        got_q = act_t["q"].numpy()
+        if layer_idx == 0:
+            assert np.array_equal(got_q, q)
+        else:
+            assert not np.allclose(got_q, q)
+        assert_parity(got_q, ref["q"], F32_ATOL, F32_RTOL, f"gated q layer {layer_idx}")
+        assert np.array_equal(act_t["tokens"].numpy().reshape(rows, D), ref["tokens"])
+
+
+def test_block_chain_with_cross_block_fusion(rt, rng):
+    # three consecutive blocks, LS2+res fused with the next block's LN1
+    D, H, M, nreg, gh, gw, views = 768, 12, 3072, 1, 24, 36, 2
+    tpv = 1 + nreg + gh * gw
+    rows = tpv * views
+    cfg = dict(embed_dim=D, num_heads=H, head_dim=64, mlp_hidden=M, num_register=nreg,
+               ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0, rope_start=0, qknorm_start=0,
+               alt_start=4)
+    layers = [make_block(rt, rng, D, H, M, rows) for _ in range(3)]
+    tokens = normals(rng, rows, D)
+    q, k = normals(rng, rows * D), normals(rng, rows * D)
+    attn, mlp, hidden = normals(rng, rows, D), normals(rng, rows, D), normals(rng, rows, M)
+    camera = normals(rng, 2 * D, scale=0.02)
+    act_t = {"tokens": rt.upload_f32(tokens), "ln1": rt.alloc_f32(rows * D),
+             "q": rt.upload_f32(q), "k": rt.upload_f32(k), "attn_proj": rt.upload_f32(attn),
+             "ln2": rt.alloc_f32(rows * D), "hidden": rt.upload_f32(hidden),
+             "mlp_out": rt.upload_f32(mlp)}
+    act = vh.activations_struct(**act_t)
+    cam_t = rt.upload_f32(camera)
+    x, qq, kk, hh = tokens, q, k, hidden
+    for i, layer_idx in enumerate((3, 4, 5)):
+        flags = vh.VK_BLOCK_FUSE_LS_LN
+        nxt = None
+        if i > 0:
+            flags |= vh.VK_BLOCK_SKIP_LN1
+        if i < 2:
+            flags |= vh.VK_BLOCK_FUSE_NEXT_LN1
+            nxt = vh.layer_struct(**layers[i + 1][1])
+        rt.vit_block_fused_ops(vh.VitConfig(**cfg), layer_idx, vh.layer_struct(**layers[i][1]),
+                               nxt, act, gh, gw, views, cam_t, flags)
+        ref = oracle.block_fused_ops(x, qq, kk, attn, hh, mlp, layers[i][0], cfg, layer_idx, gh,
+                                     gw, views, camera)
+        x, qq, kk, hh = ref["tokens"], ref["q"], ref["k"], ref["hidden"]
+    got = act_t["tokens"].numpy()
+    assert_parity(got, x, F32_ATOL, F32_RTOL, "chained tokens")
+    assert_parity(act_t["ln1"].numpy(), ref["ln1"], F32_ATOL, F32_RTOL, "chained ln1")
+    assert_parity(act_t["ln2"].numpy(), ref["ln2"], F32_ATOL, F32_RTOL, "chained ln2")
+    assert_parity(act_t["q"].numpy(), qq, F32_ATOL, F32_RTOL, "chained q")
+    assert_parity(act_t["hidden"].numpy(), hh, F32_ATOL, F32_RTOL, "chained hidden")

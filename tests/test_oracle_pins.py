@@ -1,0 +1,361 @@
+"""Pins the oracle (CPU restatement) before it is trusted as the GPU checker.
+
+Each oracle function is checked against the reference's own known-answer data
+(tests/golden/reference_kats.json), float64 library twins (tests/golden/
+twins.npz, written by torch), float64 brute force, and invariants chosen so
+that a plausible mistake (dropped term, wrong sign or index, transposed
+operand, wrong epsilon) fails one of them.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_parity, parity_report
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def kats():
+    with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module")
+def twins():
+    return dict(np.load(os.path.join(GOLDEN, "twins.npz")))
+
+
+# ---------------------------------------------------------------- comparator
+def test_compare_semantics_match_reference(kats):
+    for case in kats["compare_semantics"]["cases"]:
+        ok, max_abs, worst = parity_report(case["got"], case["ref"], case["atol"], case["rtol"])
+        assert ok == case["ok"]
+        if "worst" in case:
+            assert worst == case["worst"]
+            assert abs(max_abs - case["max_abs"]) < 1e-9
+
+
+# ---------------------------------------------------------------- f16
+def test_f16_widening_is_exact_for_every_bit_pattern():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = oracle.f16_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+# ---------------------------------------------------------------- LayerNorm
+def test_layernorm_kat_zero_mean(kats):
+    k = kats["layernorm_kat"]
+    y = oracle.layernorm(np.array([k["x"]], np.float32), np.ones(4, np.float32),
+                         np.zeros(4, np.float32), k["eps"])
+    assert abs(float(y.mean())) < k["mean_tol"]
+
+
+def test_layernorm_matches_torch_twin_768(twins):
+    y = oracle.layernorm(twins["ln768_x"], twins["ln768_g"], twins["ln768_b"], 1e-6)
+    assert_parity(y, twins["ln768_y64"], 1e-6, 1e-5, "ln768 vs torch f64")
+
+
+def test_layernorm_matches_torch_twin_qk64(twins):
+    y = oracle.layernorm(twins["ln64_x"], twins["ln64_g"], twins["ln64_b"], 1e-5)
+    assert_parity(y, twins["ln64_y64"], 1e-6, 1e-5, "ln64 vs torch f64")
+
+
+def test_layernorm_float64_brute_force_and_wrong_variants(rng):
+    x = (rng.standard_normal((33, 1024)) * 2 + 0.3).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(1024)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(1024)).astype(np.float32)
+    y = oracle.layernorm(x, g, b, 1e-6)
+    xd = x.astype(np.float64)
+    m = xd.mean(-1, keepdims=True)
+    v = ((xd - m) ** 2).mean(-1, keepdims=True)
+    ref = (xd - m) / np.sqrt(v + 1e-6) * g + b
+    assert_parity(y, ref, 1e-6, 1e-5, "ln brute force")
+    # an unbiased variance or a gamma/beta swap must not pass
+    v_unb = ((xd - m) ** 2).sum(-1, keepdims=True) / (1024 - 1)
+    wrong = (xd - m) / np.sqrt(v_unb + 1e-6) * g + b
+    assert not parity_report(y, wrong, 1e-6, 1e-5)[0]
+    wrong2 = (xd - m) / np.sqrt(v + 1e-6) * b + g
+    assert not parity_report(y, wrong2, 1e-6, 1e-5)[0]
+
+
+def test_layernorm_sequential_sum_order():
+    # A row whose sequential f32 sum differs from its pairwise sum: the
+    # oracle must follow the reference's left-to-right order.
+    row = np.array([1e8, 1.0, -1e8, 1.0] * 16, np.float32)
+    seq = np.float32(0)
+    for v in row:
+        seq = np.float32(seq + v)
+    y = oracle.layernorm(row[None], np.ones(64, np.float32), np.zeros(64, np.float32), 1e-5)
+    mean = np.float32(seq / np.float32(64))
+    d = (row - mean).astype(np.float32)
+    sq = np.float32(0)
+    for v in d:
+        sq = np.float32(sq + np.float32(v * v))
+    inv = np.float32(1) / np.sqrt(np.float32(sq / np.float32(64)) + np.float32(1e-5))
+    expect = ((row - mean) * inv).astype(np.float32)
+    assert np.array_equal(y[0], expect)
+
+
+def test_qk_norm_eps_discriminator(rng):
+    # attention_and_layerscale_op.rs:91-196: near-constant rows make eps 1e-5
+    # and 1e-6 distinguishable.
+    heads, n, hd = 2, 2, 4
+    q = np.zeros((heads * n, hd), np.float32)
+    for r in range(heads * n):
+        q[r] = 100.0 + r + rng.uniform(-1e-3, 1e-3, hd)
+    g, b = np.ones(hd, np.float32), np.zeros(hd, np.float32)
+    y5 = oracle.layernorm(q, g, b, 1e-5)
+    y6 = oracle.layernorm(q, g, b, 1e-6)
+    assert np.max(np.abs(y5 - y6)) > 1e-8
+
+
+# ---------------------------------------------------------------- GELU
+AS_BOUND = 1.5e-7 + 6 * 2.0 ** -24
+
+
+def test_gelu_kats(kats):
+    k = kats["gelu_kat"]
+    y = oracle.gelu(np.array(k["x"], np.float32))
+    for got, exp, tol in zip(y, k["expected"], k["tol"]):
+        assert abs(float(got) - exp) < tol
+
+
+def test_erf_as7126_error_bound():
+    xs = np.linspace(-6, 6, 4001)
+    err = max(abs(oracle.erf_as7126(float(np.float32(x))) - math.erf(float(np.float32(x))))
+              for x in xs)
+    # A&S 7.1.26 bound 1.5e-7 plus f32 evaluation: the cancellation in
+    # 1 - p*t*exp(-a^2) costs up to ~6 ulp(1) = 6 * 2^-24
+    assert err < AS_BOUND
+    # a wrong coefficient is far outside that bound
+    assert err > 0
+
+
+def test_gelu_within_as7126_bound_of_exact_twin(twins):
+    x = twins["gelu_x"]
+    y = oracle.gelu(x).astype(np.float64)
+    exact = twins["gelu_y64"]
+    bound = 0.5 * np.abs(x.astype(np.float64)) * AS_BOUND + 2 * np.spacing(
+        np.abs(exact).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(y - exact) <= bound + 1e-30)
+
+
+def test_gelu_erff_variant_matches_exact_twin(twins):
+    y = oracle.gelu_erff(twins["gelu_x"])
+    assert_parity(y, twins["gelu_y64"], 1e-6, 1e-5, "gelu(erff) vs torch f64")
+
+
+# ---------------------------------------------------------------- LayerScale / residual
+def test_layerscale_op_values(kats):
+    k = kats["layerscale_op"]
+    x = np.array(k["x"], np.float32).reshape(k["rows"], k["cols"])
+    y = oracle.layerscale(x, np.array(k["gamma"], np.float32))
+    assert np.array_equal(y.reshape(-1), np.array(k["expected"], np.float32))
+
+
+def test_layerscale_residual_two_roundings(rng):
+    x = rng.standard_normal((5, 8)).astype(np.float32)
+    y = rng.standard_normal((5, 8)).astype(np.float32)
+    g = rng.uniform(0, 0.1, 8).astype(np.float32)
+    out = oracle.layerscale_residual(x, y, g)
+    expect = (x + (y * g).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(out, expect)
+    assert np.array_equal(oracle.layerscale_residual(x, y, None), (x + y).astype(np.float32))
+    # an FMA (single rounding) differs on some elements of a larger draw
+    xb = rng.standard_normal(4096).astype(np.float32)
+    yb = rng.standard_normal(4096).astype(np.float32)
+    gb = np.full(4096, np.float32(0.0731))
+    two = oracle.layerscale_residual(xb[None], yb[None], gb)[0]
+    fma = (xb.astype(np.float64) + yb.astype(np.float64) * gb.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(two, (xb + (yb * gb).astype(np.float32)).astype(np.float32))
+    assert not np.array_equal(two, fma)
+
+
+def test_layerscale_residual_w16_equals_widened(rng):
+    x = rng.standard_normal((3, 16)).astype(np.float32)
+    y = rng.standard_normal((3, 16)).astype(np.float32)
+    g16 = rng.uniform(0, 0.1, 16).astype(np.float16)
+    assert np.array_equal(oracle.layerscale_residual(x, y, g16),
+                          oracle.layerscale_residual(x, y, g16.astype(np.float32)))
+
+
+# ---------------------------------------------------------------- RoPE
+def test_rope_positions_layout():
+    # n_special 2, grid 2x3, two views: specials (0,0) per view, patches
+    # (row+1, col+1) locally, (1,1) globally (vit_block.rs:841-881).
+    loc = oracle.rope_positions(2, 2, 3, 2, False)
+    one_view = [[0, 0], [0, 0], [1, 1], [1, 2], [1, 3], [2, 1], [2, 2], [2, 3]]
+    assert loc.tolist() == one_view * 2
+    glob = oracle.rope_positions(2, 2, 3, 2, True)
+    assert glob.tolist() == ([[0, 0], [0, 0]] + [[1, 1]] * 6) * 2
+
+
+def test_rope_identity_at_origin(rng):
+    x = rng.standard_normal((2, 3, 64)).astype(np.float32)
+    pos = np.zeros((3, 2), np.int64)
+    assert np.array_equal(oracle.rope2d(x, 2, 3, 64, pos), x)
+
+
+def test_rope_preserves_pair_norms(rng):
+    x = rng.standard_normal((3, 5, 64)).astype(np.float32)
+    pos = rng.integers(0, 80, (5, 2))
+    y = oracle.rope2d(x, 3, 5, 64, pos).astype(np.float64)
+    xd = x.astype(np.float64)
+    for half in (0, 32):
+        a, b = xd[..., half:half + 16], xd[..., half + 16:half + 32]
+        a2, b2 = y[..., half:half + 16], y[..., half + 16:half + 32]
+        assert np.allclose(a * a + b * b, a2 * a2 + b2 * b2, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_relative_position_property(rng):
+    # <R(p)q, R(p')k> depends only on p - p' (per coordinate)
+    q = rng.standard_normal((1, 1, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 1, 64)).astype(np.float32)
+
+    def dot(pq, pk):
+        a = oracle.rope2d(q, 1, 1, 64, np.array([pq], np.int64)).astype(np.float64)
+        b = oracle.rope2d(k, 1, 1, 64, np.array([pk], np.int64)).astype(np.float64)
+        return float((a * b).sum())
+
+    base = dot((3, 5), (1, 2))
+    for shift in ((1, 0), (0, 4), (7, 9)):
+        s = dot((3 + shift[0], 5 + shift[1]), (1 + shift[0], 2 + shift[1]))
+        assert abs(s - base) < 1e-4 * max(1.0, abs(base))
+    assert abs(dot((4, 5), (1, 2)) - base) > 1e-3
+
+
+def test_rope_recovered_angles_and_pairing():
+    # a unit vector at element j of a half rotates inside the (j, j+16) pair by
+    # pos * base^(-2j/32): y half by the row coordinate, x half by the column.
+    py, px = 7, 3
+    for half, p in ((0, py), (32, px)):
+        for j in range(16):
+            x = np.zeros((1, 1, 64), np.float32)
+            x[0, 0, half + j] = 1.0
+            y = oracle.rope2d(x, 1, 1, 64, np.array([[py, px]], np.int64))[0, 0]
+            nz = np.flatnonzero(np.abs(y) > 1e-7)
+            assert set(nz.tolist()) <= {half + j, half + j + 16}
+            theta = math.atan2(float(y[half + j + 16]), float(y[half + j]))
+            expect = p * 100.0 ** (-2.0 * j / 32.0)
+            d = (theta - expect + math.pi) % (2 * math.pi) - math.pi
+            assert abs(d) < 2e-5 * max(1.0, expect)
+
+
+def test_rope_changes_output(kats):
+    k = kats["rope_changes_output"]
+    rng = np.random.default_rng(0x12345678)
+    x = rng.standard_normal((k["heads"], k["n"], k["head_dim"])).astype(np.float32)
+    pos = np.array(k["pos_yx"], np.int64).reshape(k["n"], 2)
+    y = oracle.rope2d(x, k["heads"], k["n"], k["head_dim"], pos, k["freq"])
+    assert np.array_equal(y[:, 0], x[:, 0])  # token at (0,0) unchanged
+    assert np.max(np.abs(y[:, 1] - x[:, 1])) > 1e-4
+
+
+def test_qk_norm_rope_is_norm_then_rope(rng):
+    heads, n = 3, 7
+    q = rng.standard_normal((heads, n, 64)).astype(np.float32)
+    k = rng.standard_normal((heads, n, 64)).astype(np.float32)
+    qg, qb, kg, kb = [(1 + 0.02 * rng.standard_normal(64)).astype(np.float32) for _ in range(4)]
+    pos = oracle.rope_positions(1, 2, 3, 1, False)
+    qo, ko = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n)
+    q_ref = oracle.rope2d(oracle.layernorm(q, qg, qb, 1e-5), heads, n, 64, pos.astype(np.int64))
+    k_ref = oracle.rope2d(oracle.layernorm(k, kg, kb, 1e-5), heads, n, 64, pos.astype(np.int64))
+    assert np.array_equal(qo, q_ref) and np.array_equal(ko, k_ref)
+    # rope-then-norm is a different function
+    wrong = oracle.layernorm(oracle.rope2d(q, heads, n, 64, pos.astype(np.int64)), qg, qb, 1e-5)
+    assert not np.allclose(qo, wrong, atol=1e-4)
+
+
+# ---------------------------------------------------------------- patch embed
+def test_patch_embed_kats(kats):
+    for name in ("patch_embed_bias_broadcast", "patch_embed_row_major"):
+        k = kats[name]
+        img = np.array(k["image_nchw"], np.float32).reshape(3, k["h"], k["w"])
+        w = np.array(k["weight_oihw"], np.float32).reshape(k["embed"], 3, k["patch"], k["patch"])
+        out = oracle.patch_project_oihw(img, k["patch"], w, np.array(k["bias"], np.float32))
+        assert out.tolist() == k["expected_tokens"], name
+
+
+def test_patch_projection_matches_conv2d_twin(twins):
+    out = oracle.patch_project_oihw(twins["conv_img"], 14, twins["conv_w"], twins["conv_b"])
+    assert_parity(out, twins["conv_y64"], 1e-6, 1e-5, "patch conv vs torch f64")
+    # the split path (patchify -> linear with W^T) is the same projection
+    rows = oracle.patchify_nchw(twins["conv_img"], 14)
+    wt = twins["conv_w"].reshape(16, -1).T.copy()
+    lin = oracle.linear(rows, wt, twins["conv_b"])
+    assert_parity(lin, twins["conv_y64"], 1e-6, 1e-5, "patchify+linear vs torch f64")
+
+
+def test_normalize_kat(kats):
+    k = kats["normalize"]
+    img = np.array(k["hwc_u8"], np.uint8).reshape(k["h"], k["w"], 3)
+    out = oracle.normalize_u8_hwc(img, k["mean"], k["std"])
+    for c in range(3):
+        for y in range(k["h"]):
+            for x in range(k["w"]):
+                v = int(img[y, x, c])
+                expect = (np.float32(v) / np.float32(255.0) - np.float32(k["mean"][c])) / np.float32(k["std"][c])
+                assert abs(float(out[c, y, x]) - float(expect)) < k["tolerance"]
+                f64 = (v / 255.0 - k["mean"][c]) / k["std"][c]
+                assert abs(float(out[c, y, x]) - f64) < 1e-5
+
+
+def test_pos_embed_kats(kats):
+    k = kats["pos_embed_tokens"]
+    pe = np.array(k["pos_embed"], np.float32)
+    table = oracle.pos_embed_bicubic(pe, k["grid"], k["embed"], k["gh"], k["gw"])
+    patches = np.zeros((k["gh"] * k["gw"], k["embed"]), np.float32)
+    toks = oracle.assemble_tokens(patches, k["gh"], k["gw"], np.array(k["cls"], np.float32), None,
+                                  table)
+    assert toks[0].tolist() == k["expected_row0"]
+    native = oracle.pos_embed_bicubic(pe, 3, 2, 3, 3)
+    assert native[0].tolist() == k["native_grid_cls_row"]
+
+
+def test_pos_embed_bicubic_matches_torch_twin(twins):
+    pe = twins["pe_src"]
+    for gh, gw in ((24, 36), (5, 7)):
+        out = oracle.pos_embed_bicubic(pe, 37, 8, gh, gw, 0.1)
+        assert np.array_equal(out[0], pe[0])
+        assert_parity(out[1:], twins[f"pe_{gh}x{gw}_y64"], 1e-6, 1e-4, f"bicubic {gh}x{gw}")
+
+
+def test_pos_embed_partition_of_unity():
+    # a constant grid resizes to the same constant (Keys weights sum to 1)
+    pe = np.full((37 * 37 + 1, 4), 0.25, np.float32)
+    out = oracle.pos_embed_bicubic(pe, 37, 4, 24, 36)
+    assert np.allclose(out, 0.25, atol=1e-6)
+
+
+def test_assemble_tokens_registers_get_no_position(rng):
+    embed, gh, gw = 8, 2, 3
+    patches = rng.standard_normal((gh * gw, embed)).astype(np.float32)
+    cls = rng.standard_normal(embed).astype(np.float32)
+    regs = rng.standard_normal((1, embed)).astype(np.float32)
+    pos = rng.standard_normal((1 + gh * gw, embed)).astype(np.float32)
+    toks = oracle.assemble_tokens(patches, gh, gw, cls, regs, pos)
+    assert np.array_equal(toks[0], cls + pos[0])
+    assert np.array_equal(toks[1], regs[0])
+    assert np.array_equal(toks[2:], patches + pos[1:])
+
+
+def test_patch_embed_u8_composes_the_three_steps(rng):
+    h, w, embed = 28, 42, 16
+    img = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    mean, std = [0.485, 0.456, 0.406], [0.229, 0.224, 0.225]
+    wt = (0.02 * rng.standard_normal((embed, 3, 14, 14))).astype(np.float32)
+    b = (0.02 * rng.standard_normal(embed)).astype(np.float32)
+    cls = rng.standard_normal(embed).astype(np.float32)
+    pos = rng.standard_normal((1 + 6, embed)).astype(np.float32)
+    full = oracle.patch_embed_u8(img, 14, mean, std, wt, b, cls, None, pos)
+    chw = oracle.normalize_u8_hwc(img, mean, std)
+    proj = oracle.patch_project_oihw(chw, 14, wt, b)
+    assert np.array_equal(full, oracle.assemble_tokens(proj, 2, 3, cls, None, pos))

@@ -1,0 +1,130 @@
+// One DA3 ViT block's fused per-token operations, enqueued on the runtime's
+// stream in the reference order (run_tail_device, vit_block.rs:489-582, and
+// vit_block_with_views, vit_block.rs:1019-1139).  The GEMMs and attention
+// between the operations are the caller's; their products arrive in
+// vk_vit_activations.
+//
+// Multi-view batches are handled MI355X-first: the residual stream of all
+// views stays in one view-major device buffer for every layer.  Per-token
+// operations are independent of view boundaries, so local and global layers
+// both run as one launch over view_count * tokens_per_view rows; only the
+// RoPE positions differ (per-view grid positions vs (1,1)) and the Q/K layout
+// (per-view head-major blocks vs one head-major sequence).  The reference's
+// flatten / split copies around global layers (backbone.rs:770-796,
+// 990-1027) do not exist here.
+#include "common.h"
+
+namespace {
+
+bool layer_uses_global(const vk_vit_config* cfg, size_t layer) {
+  return cfg->alt_start >= 0 && static_cast<long long>(layer) >= cfg->alt_start && layer % 2 == 1;
+}
+
+int check_len(const vk_tensor* t, size_t len, const char* name) {
+  VK_REQUIRE(t != nullptr, "activation %s is null", name);
+  VK_REQUIRE(t->dtype == VK_F32, "activation %s must be f32", name);
+  VK_REQUIRE(t->len == len, "activation %s holds %zu, expected %zu", name, t->len, len);
+  return VK_OK;
+}
+
+}  // namespace
+
+extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
+                                      size_t layer_idx, const vk_vit_layer* layer,
+                                      const vk_vit_layer* next_layer,
+                                      const vk_vit_activations* act, size_t gh, size_t gw,
+                                      size_t view_count, const vk_tensor* camera,
+                                      unsigned flags) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(cfg && layer && act, "null argument");
+  VK_REQUIRE(view_count > 0 && gw > 0 && gh > 0, "empty grid or view count");
+  const size_t D = cfg->embed_dim;
+  const size_t H = cfg->num_heads;
+  const size_t hd = cfg->head_dim;
+  const size_t M = cfg->mlp_hidden;
+  VK_REQUIRE(D > 0 && H > 0 && hd > 0 && M > 0, "empty model dimensions");
+  VK_REQUIRE(H * hd == D, "num_heads*head_dim (%zu) must equal embed_dim (%zu)", H * hd, D);
+  const size_t n_special = 1 + cfg->num_register;
+  const size_t tpv = n_special + gh * gw;
+  const size_t rows = tpv * view_count;
+  VK_TRY(check_len(act->tokens, rows * D, "tokens"));
+  VK_TRY(check_len(act->ln1, rows * D, "ln1"));
+  VK_TRY(check_len(act->q, rows * D, "q"));
+  VK_TRY(check_len(act->k, rows * D, "k"));
+  VK_TRY(check_len(act->attn_proj, rows * D, "attn_proj"));
+  VK_TRY(check_len(act->ln2, rows * D, "ln2"));
+  VK_TRY(check_len(act->hidden, rows * M, "hidden"));
+  VK_TRY(check_len(act->mlp_out, rows * D, "mlp_out"));
+  VK_REQUIRE(!(flags & VK_BLOCK_FUSE_NEXT_LN1) || next_layer,
+             "VK_BLOCK_FUSE_NEXT_LN1 needs next_layer");
+
+  const bool global = layer_uses_global(cfg, layer_idx);
+
+  // camera-token slot write before block alt_start (backbone.rs:446-457 for
+  // one view; 746-768 per view: slot 0 for the reference view, slot 1 for the
+  // source views).
+  bool camera_written = false;
+  if (cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start)) {
+    VK_REQUIRE(camera != nullptr, "camera token required at alt_start=%d", cfg->alt_start);
+    VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D, "camera token must hold >= %zu f32", D);
+    VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
+               "multi-view camera token must hold reference and source slots (2*%zu)", D);
+    for (size_t v = 0; v < view_count; ++v) {
+      const size_t slot = v > 0 ? 1 : 0;
+      VK_TRY(vk_copy_segment_into_f32(rt, act->tokens, v * tpv * D, camera, slot * D, D));
+    }
+    camera_written = true;
+  }
+
+  // LN1 (skipped when the previous block already produced it, unless the
+  // camera write changed the tokens since)
+  if (!(flags & VK_BLOCK_SKIP_LN1) || camera_written) {
+    VK_TRY(vk_layernorm_into_f32(rt, act->tokens, layer->norm1_gamma, layer->norm1_beta, rows, D,
+                                 cfg->ln_eps, act->ln1));
+  }
+
+  // Q/K-norm + RoPE gating (vit_block.rs:835-838)
+  const bool use_qknorm = cfg->qknorm_start >= 0 &&
+                          static_cast<long long>(layer_idx) >= cfg->qknorm_start &&
+                          layer->qnorm_gamma != nullptr;
+  const bool use_rope =
+      cfg->rope_start >= 0 && static_cast<long long>(layer_idx) >= cfg->rope_start;
+  const vk_qk_layout layout = global ? VK_QK_HEADS_OUTER : VK_QK_VIEWS_OUTER;
+  if (use_rope) {
+    VK_TRY(vk_qk_norm_rope_grid_f32(
+        rt, act->q, act->k, use_qknorm ? layer->qnorm_gamma : nullptr,
+        use_qknorm ? layer->qnorm_beta : nullptr, use_qknorm ? layer->knorm_gamma : nullptr,
+        use_qknorm ? layer->knorm_beta : nullptr, H, hd, n_special, gh, gw, view_count,
+        global ? 1 : 0, layout, cfg->rope_freq, cfg->qk_norm_eps));
+  } else if (use_qknorm) {
+    // Q/K-norm without RoPE: LayerNorm over every (head, token) row
+    VK_TRY(vk_layernorm_into_f32(rt, act->q, layer->qnorm_gamma, layer->qnorm_beta, rows * H, hd,
+                                 cfg->qk_norm_eps, act->q));
+    VK_TRY(vk_layernorm_into_f32(rt, act->k, layer->knorm_gamma, layer->knorm_beta, rows * H, hd,
+                                 cfg->qk_norm_eps, act->k));
+  }
+
+  // tokens += ls1 (.) attn_proj, then LN2
+  if (flags & VK_BLOCK_FUSE_LS_LN) {
+    VK_TRY(vk_layerscale_residual_layernorm_f32(rt, act->tokens, act->attn_proj, layer->ls1,
+                                                layer->norm2_gamma, layer->norm2_beta, rows, D,
+                                                cfg->ln_eps, act->ln2));
+  } else {
+    VK_TRY(vk_layerscale_residual_f32(rt, act->tokens, act->attn_proj, layer->ls1, rows, D));
+    VK_TRY(vk_layernorm_into_f32(rt, act->tokens, layer->norm2_gamma, layer->norm2_beta, rows, D,
+                                 cfg->ln_eps, act->ln2));
+  }
+
+  // GELU on the FC1 output
+  VK_TRY(vk_gelu_f32_inplace(rt, act->hidden));
+
+  // tokens += ls2 (.) mlp_out [, next block's LN1]
+  if (flags & VK_BLOCK_FUSE_NEXT_LN1) {
+    VK_TRY(vk_layerscale_residual_layernorm_f32(rt, act->tokens, act->mlp_out, layer->ls2,
+                                                next_layer->norm1_gamma, next_layer->norm1_beta,
+                                                rows, D, cfg->ln_eps, act->ln1));
+  } else {
+    VK_TRY(vk_layerscale_residual_f32(rt, act->tokens, act->mlp_out, layer->ls2, rows, D));
+  }
+  return VK_OK;
+}

@@ -1,0 +1,160 @@
+// Internal definitions shared by the runtime and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "vestra_hip.h"
+
+// ---------------------------------------------------------------------------
+// host-side objects behind the opaque handles
+// ---------------------------------------------------------------------------
+
+struct vk_runtime {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int cu_count = 0;
+  // cos/sin tables of the 2D rotary embedding, keyed by (frequency bits,
+  // head_dim); device pointers owned by the runtime.
+  std::map<std::pair<uint32_t, int>, float*> rope_tables;
+};
+
+struct vk_tensor {
+  vk_runtime* rt = nullptr;
+  void* ptr = nullptr;
+  size_t len = 0;
+  vk_dtype dtype = VK_F32;
+  bool owned = true;
+};
+
+struct vk_linear {
+  vk_runtime* rt = nullptr;
+  size_t in_features = 0;
+  size_t out_features = 0;
+  float* weight_kn = nullptr;  // [in, out], out contiguous
+  float* bias = nullptr;       // [out]
+  float* ls_gamma = nullptr;   // [out] or null
+};
+
+struct vk_event {
+  vk_runtime* rt = nullptr;
+  hipEvent_t ev = nullptr;
+};
+
+struct vk_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+// error plumbing
+// ---------------------------------------------------------------------------
+
+namespace vk {
+
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+int hip_fail(hipError_t e, const char* what);
+size_t dtype_size(vk_dtype d);
+// Ensures the calling thread's current device is the runtime's device.
+int bind(vk_runtime* rt);
+// Launch check: turns a failed launch into a status.
+int check_launch(const char* what);
+// Device cos/sin table for the 2D RoPE (see rope_table_layout below).
+int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out);
+
+}  // namespace vk
+
+#define VK_REQUIRE(cond, ...)                              \
+  do {                                                     \
+    if (!(cond)) return vk::set_error(VK_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define VK_UNSUPPORTED_IF(cond, ...)                       \
+  do {                                                     \
+    if (cond) return vk::set_error(VK_ERR_UNSUPPORTED, __VA_ARGS__); \
+  } while (0)
+
+#define VK_HIP(call)                                       \
+  do {                                                     \
+    hipError_t e_ = (call);                                \
+    if (e_ != hipSuccess) return vk::hip_fail(e_, #call);  \
+  } while (0)
+
+#define VK_TRY(call)                                       \
+  do {                                                     \
+    int s_ = (call);                                       \
+    if (s_ != VK_OK) return s_;                            \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// RoPE table layout (device, f32):
+//   [0, kRopeTableMax]          positions covered by the table
+//   entry p: 32 floats: cos(p*inv_freq_j) j<16, then sin(p*inv_freq_j) j<16
+//   after the last entry: inv_freq_j, j<16 (for positions outside the table)
+// ---------------------------------------------------------------------------
+namespace vk {
+constexpr int kRopeTableMax = 1023;
+constexpr int kRopeQuarter = 16;  // head_dim 64: two halves of 32, 16 pairs each
+}  // namespace vk
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+namespace vkd {
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the
+// same (bitwise identical) value.
+__device__ __forceinline__ float row16_sum(float v) {
+  int iv;
+  iv = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true);  // quad_perm 1,0,3,2
+  v = v + __builtin_bit_cast(float, iv);
+  iv = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true);  // quad_perm 2,3,0,1
+  v = v + __builtin_bit_cast(float, iv);
+  iv = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true); // row_half_mirror
+  v = v + __builtin_bit_cast(float, iv);
+  iv = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true); // row_mirror
+  v = v + __builtin_bit_cast(float, iv);
+  return v;
+}
+
+// Sum over a whole wave64; every lane receives the same value.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v = v + __shfl_xor(v, 16, 64);
+  v = v + __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Parameter vector element loads (f32 or binary16 storage).
+template <typename PT>
+struct Param;
+
+template <>
+struct Param<float> {
+  __device__ __forceinline__ static float4 load4(const float* p, size_t i4) {
+    return reinterpret_cast<const float4*>(p)[i4];
+  }
+};
+
+template <>
+struct Param<uint16_t> {
+  __device__ __forceinline__ static float4 load4(const uint16_t* p, size_t i4) {
+    const ushort4 h = reinterpret_cast<const ushort4*>(p)[i4];
+    return make_float4(f16_to_f32(h.x), f16_to_f32(h.y), f16_to_f32(h.z),
+                       f16_to_f32(h.w));
+  }
+};
+
+}  // namespace vkd

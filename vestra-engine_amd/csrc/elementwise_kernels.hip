@@ -1,0 +1,249 @@
+// Streaming element-wise kernels for gfx950: GELU (in place), residual add,
+// LayerScale, and the fused LayerScale + residual.
+//
+// All are HBM-bound streams.  Each thread moves 128-bit (float4) vectors with
+// a grid-stride loop sized to a few workgroups per CU, so every wave keeps
+// several independent 16-byte loads in flight; the (len % 4) tail is handled
+// by the first threads of the grid.  Per-column parameters (LayerScale gamma)
+// are indexed by the float4's column, valid because cols % 4 == 0.
+#include "common.h"
+
+namespace {
+
+using vkd::Param;
+
+// Abramowitz & Stegun 7.1.26 erf (|error| < 1.5e-7): the erf of the
+// reference's scalar GELU (docs/plans/2026-07-18-rust-engine-v1.md:870-876),
+// with the same operation order: t = 1/(1 + p*a);
+// y = 1 - ((((a5*t + a4)*t + a3)*t + a2)*t + a1)*t * exp(-a*a); erf = sign*y.
+__device__ __forceinline__ float erf_as7126(float x) {
+  const float s = __builtin_signbit(x) ? -1.0f : 1.0f;
+  const float a = fabsf(x);
+  const float t = 1.0f / (1.0f + 0.3275911f * a);
+  float p = 1.0614054f * t - 1.4531520f;
+  p = p * t;
+  p = p + 1.4214137f;
+  p = p * t - 0.28449674f;
+  p = p * t + 0.25482959f;
+  const float y = 1.0f - p * t * expf(-a * a);
+  return s * y;
+}
+
+template <int MODE>
+__device__ __forceinline__ float gelu1(float v) {
+  const float inv_sqrt2 = 0.70710678f;
+  const float e = (MODE == 0) ? erf_as7126(v * inv_sqrt2) : erff(v * inv_sqrt2);
+  return 0.5f * v * (1.0f + e);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void gelu_kernel(float* __restrict__ x, long long n) {
+  const long long n4 = n >> 2;
+  const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+  float4* x4 = reinterpret_cast<float4*>(x);
+  long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  // two independent vectors per iteration keep more loads in flight
+  for (; i + stride < n4; i += 2 * stride) {
+    float4 a = x4[i];
+    float4 b = x4[i + stride];
+    a.x = gelu1<MODE>(a.x); a.y = gelu1<MODE>(a.y); a.z = gelu1<MODE>(a.z); a.w = gelu1<MODE>(a.w);
+    b.x = gelu1<MODE>(b.x); b.y = gelu1<MODE>(b.y); b.z = gelu1<MODE>(b.z); b.w = gelu1<MODE>(b.w);
+    x4[i] = a;
+    x4[i + stride] = b;
+  }
+  if (i < n4) {
+    float4 a = x4[i];
+    a.x = gelu1<MODE>(a.x); a.y = gelu1<MODE>(a.y); a.z = gelu1<MODE>(a.z); a.w = gelu1<MODE>(a.w);
+    x4[i] = a;
+  }
+  const long long tail = n - (n4 << 2);
+  const long long tid = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid < tail) x[(n4 << 2) + tid] = gelu1<MODE>(x[(n4 << 2) + tid]);
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float* __restrict__ dst,
+                                                  const float* __restrict__ src, long long n) {
+  const long long n4 = n >> 2;
+  const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+  float4* d4 = reinterpret_cast<float4*>(dst);
+  const float4* s4 = reinterpret_cast<const float4*>(src);
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
+       i += stride) {
+    float4 a = d4[i];
+    const float4 b = s4[i];
+    a.x = a.x + b.x;
+    a.y = a.y + b.y;
+    a.z = a.z + b.z;
+    a.w = a.w + b.w;
+    d4[i] = a;
+  }
+  const long long tail = n - (n4 << 2);
+  const long long tid = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid < tail) dst[(n4 << 2) + tid] = dst[(n4 << 2) + tid] + src[(n4 << 2) + tid];
+}
+
+// x[r, c] *= g[c]
+template <typename PT>
+__global__ __launch_bounds__(256) void layerscale_kernel(float* __restrict__ x,
+                                                         const PT* __restrict__ g,
+                                                         long long n4, int cols4) {
+  const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+  float4* x4 = reinterpret_cast<float4*>(x);
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
+       i += stride) {
+    float4 a = x4[i];
+    const float4 gv = Param<PT>::load4(g, i % cols4);
+    a.x = a.x * gv.x;
+    a.y = a.y * gv.y;
+    a.z = a.z * gv.z;
+    a.w = a.w * gv.w;
+    x4[i] = a;
+  }
+}
+
+// x[r, c] += y[r, c] * g[c]   (t = y*g rounded, then x + t rounded)
+template <typename PT>
+__global__ __launch_bounds__(256) void layerscale_residual_kernel(
+    float* __restrict__ x, const float* __restrict__ y, const PT* __restrict__ g,
+    long long n4, int cols4) {
+  const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+  float4* x4 = reinterpret_cast<float4*>(x);
+  const float4* y4 = reinterpret_cast<const float4*>(y);
+  long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (; i + stride < n4; i += 2 * stride) {
+    float4 a = x4[i];
+    float4 a2 = x4[i + stride];
+    const float4 b = y4[i];
+    const float4 b2 = y4[i + stride];
+    const float4 gv = Param<PT>::load4(g, i % cols4);
+    const float4 gv2 = Param<PT>::load4(g, (i + stride) % cols4);
+    float t;
+    t = b.x * gv.x; a.x = a.x + t;
+    t = b.y * gv.y; a.y = a.y + t;
+    t = b.z * gv.z; a.z = a.z + t;
+    t = b.w * gv.w; a.w = a.w + t;
+    t = b2.x * gv2.x; a2.x = a2.x + t;
+    t = b2.y * gv2.y; a2.y = a2.y + t;
+    t = b2.z * gv2.z; a2.z = a2.z + t;
+    t = b2.w * gv2.w; a2.w = a2.w + t;
+    x4[i] = a;
+    x4[i + stride] = a2;
+  }
+  if (i < n4) {
+    float4 a = x4[i];
+    const float4 b = y4[i];
+    const float4 gv = Param<PT>::load4(g, i % cols4);
+    float t;
+    t = b.x * gv.x; a.x = a.x + t;
+    t = b.y * gv.y; a.y = a.y + t;
+    t = b.z * gv.z; a.z = a.z + t;
+    t = b.w * gv.w; a.w = a.w + t;
+    x4[i] = a;
+  }
+}
+
+// Grid for a stream of n4 float4 vectors: enough workgroups to give each CU
+// several resident waves, capped so each thread loops a few times.
+unsigned stream_grid(vk_runtime* rt, long long n4) {
+  const long long per_block = 256;
+  long long want = (n4 + per_block - 1) / per_block;
+  const long long cap = static_cast<long long>(rt->cu_count > 0 ? rt->cu_count : 256) * 16;
+  if (want > cap) want = cap;
+  if (want < 1) want = 1;
+  return static_cast<unsigned>(want);
+}
+
+bool param_ok(const vk_tensor* t, size_t len) {
+  return t && (t->dtype == VK_F32 || t->dtype == VK_F16) && t->len == len;
+}
+
+template <int MODE>
+int run_gelu(vk_runtime* rt, vk_tensor* x) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(x != nullptr, "null tensor");
+  VK_REQUIRE(x->dtype == VK_F32, "gelu activations must be f32");
+  if (x->len == 0) return VK_OK;
+  const long long n = static_cast<long long>(x->len);
+  const long long n4 = n >> 2;
+  unsigned grid = stream_grid(rt, (n4 + 1) / 2);
+  hipLaunchKernelGGL((gelu_kernel<MODE>), dim3(grid), dim3(256), 0, rt->stream,
+                     static_cast<float*>(x->ptr), n);
+  return vk::check_launch("gelu_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+int vk_gelu_f32_inplace(vk_runtime* rt, vk_tensor* x) { return run_gelu<0>(rt, x); }
+
+int vk_gelu_erf_f32_inplace(vk_runtime* rt, vk_tensor* x) { return run_gelu<1>(rt, x); }
+
+int vk_add_f32_inplace(vk_runtime* rt, vk_tensor* dst, const vk_tensor* src) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(dst && src, "null tensor");
+  VK_REQUIRE(dst->dtype == VK_F32 && src->dtype == VK_F32, "add operands must be f32");
+  VK_REQUIRE(dst->len == src->len, "add: length mismatch %zu vs %zu", dst->len, src->len);
+  VK_REQUIRE(dst->ptr != src->ptr || dst->len == 0, "add: dst and src must be distinct");
+  if (dst->len == 0) return VK_OK;
+  const long long n = static_cast<long long>(dst->len);
+  hipLaunchKernelGGL(add_kernel, dim3(stream_grid(rt, n >> 2)), dim3(256), 0, rt->stream,
+                     static_cast<float*>(dst->ptr), static_cast<const float*>(src->ptr), n);
+  return vk::check_launch("add_kernel");
+}
+
+int vk_layerscale_f32_inplace(vk_runtime* rt, vk_tensor* x, const vk_tensor* gamma,
+                              size_t rows, size_t cols) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(x != nullptr, "null tensor");
+  VK_REQUIRE(x->dtype == VK_F32, "layerscale activations must be f32");
+  VK_REQUIRE(x->len == rows * cols, "layerscale: x holds %zu, rows*cols=%zu", x->len,
+             rows * cols);
+  VK_REQUIRE(param_ok(gamma, cols), "layerscale: gamma must be an f32/f16 vector of cols=%zu",
+             cols);
+  VK_UNSUPPORTED_IF(cols % 4 != 0, "layerscale: cols=%zu must be a multiple of 4", cols);
+  if (rows * cols == 0) return VK_OK;
+  const long long n4 = static_cast<long long>(rows * cols / 4);
+  const int cols4 = static_cast<int>(cols / 4);
+  if (gamma->dtype == VK_F16)
+    hipLaunchKernelGGL((layerscale_kernel<uint16_t>), dim3(stream_grid(rt, n4)), dim3(256), 0,
+                       rt->stream, static_cast<float*>(x->ptr),
+                       static_cast<const uint16_t*>(gamma->ptr), n4, cols4);
+  else
+    hipLaunchKernelGGL((layerscale_kernel<float>), dim3(stream_grid(rt, n4)), dim3(256), 0,
+                       rt->stream, static_cast<float*>(x->ptr),
+                       static_cast<const float*>(gamma->ptr), n4, cols4);
+  return vk::check_launch("layerscale_kernel");
+}
+
+int vk_layerscale_residual_f32(vk_runtime* rt, vk_tensor* x, const vk_tensor* y,
+                               const vk_tensor* gamma, size_t rows, size_t cols) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(x && y, "null tensor");
+  VK_REQUIRE(x->dtype == VK_F32 && y->dtype == VK_F32, "activations must be f32");
+  VK_REQUIRE(x->len == rows * cols && y->len == rows * cols,
+             "layerscale_residual: x (%zu) / y (%zu) must hold rows*cols=%zu", x->len, y->len,
+             rows * cols);
+  VK_REQUIRE(x->ptr != y->ptr || x->len == 0, "x and y must be distinct buffers");
+  if (!gamma) return vk_add_f32_inplace(rt, x, y);
+  VK_REQUIRE(param_ok(gamma, cols), "gamma must be an f32/f16 vector of cols=%zu", cols);
+  VK_UNSUPPORTED_IF(cols % 4 != 0, "layerscale_residual: cols=%zu must be a multiple of 4",
+                    cols);
+  if (rows * cols == 0) return VK_OK;
+  const long long n4 = static_cast<long long>(rows * cols / 4);
+  const int cols4 = static_cast<int>(cols / 4);
+  const unsigned grid = stream_grid(rt, (n4 + 1) / 2);
+  if (gamma->dtype == VK_F16)
+    hipLaunchKernelGGL((layerscale_residual_kernel<uint16_t>), dim3(grid), dim3(256), 0,
+                       rt->stream, static_cast<float*>(x->ptr),
+                       static_cast<const float*>(y->ptr),
+                       static_cast<const uint16_t*>(gamma->ptr), n4, cols4);
+  else
+    hipLaunchKernelGGL((layerscale_residual_kernel<float>), dim3(grid), dim3(256), 0,
+                       rt->stream, static_cast<float*>(x->ptr),
+                       static_cast<const float*>(y->ptr), static_cast<const float*>(gamma->ptr),
+                       n4, cols4);
+  return vk::check_launch("layerscale_residual_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,607 @@
+// Row-normalisation kernels for gfx950: block LayerNorm, the fused
+// LayerScale+residual+LayerNorm, and the fused per-head Q/K LayerNorm + 2D
+// RoPE.
+//
+// Mapping to CDNA4:
+//  * LayerNorm rows (D = 768 / 1024): one wave64 per row, each lane holds
+//    D/256 float4 in registers (128-bit coalesced loads: a wave reads one
+//    contiguous KiB per instruction), mean and variance reduced with DPP row
+//    reductions plus two cross-row swizzles; the row is read from HBM once
+//    and written once.  Four rows per 256-thread workgroup.
+//  * Q/K rows (head_dim 64): 16 lanes per (head, token) row, one float4 per
+//    lane, so a row's LayerNorm reduces inside one DPP row (4 DPP steps) and
+//    the RoPE partner element (i <-> i+16 inside each 32-wide half) sits
+//    exactly 4 lanes away: one swizzle, no LDS round trip.  Q and K rows are
+//    covered by one launch.
+//  * Arithmetic per element follows the scalar reference order with every
+//    product and sum rounded (built with -ffp-contract=off); only the order
+//    of the mean/variance reductions differs (wave tree vs sequential).
+#include "common.h"
+
+namespace {
+
+using vkd::Param;
+
+// ---------------------------------------------------------------------------
+// LayerNorm over rows of `cols` floats, one wave per row.
+// NV = float4 per lane (cols <= 256 * NV).  x and y may alias.
+// ---------------------------------------------------------------------------
+template <int NV, typename PT>
+__global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
+                                                      const PT* __restrict__ gamma,
+                                                      const PT* __restrict__ beta,
+                                                      int rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wave leaves together
+  const int nvec = cols >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    if (c < nvec) {
+      v[i] = xr[c];
+      s += v[i].x;
+      s += v[i].y;
+      s += v[i].z;
+      s += v[i].w;
+    } else {
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  s = vkd::wave_sum(s);
+  const float mean = s / static_cast<float>(cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    if (c < nvec) {
+      float d;
+      d = v[i].x - mean; q += d * d;
+      d = v[i].y - mean; q += d * d;
+      d = v[i].z - mean; q += d * d;
+      d = v[i].w - mean; q += d * d;
+    }
+  }
+  q = vkd::wave_sum(q);
+  const float var = q / static_cast<float>(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+  float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    if (c < nvec) {
+      const float4 g = Param<PT>::load4(gamma, c);
+      const float4 b = Param<PT>::load4(beta, c);
+      float4 o;
+      o.x = (v[i].x - mean) * inv * g.x + b.x;
+      o.y = (v[i].y - mean) * inv * g.y + b.y;
+      o.z = (v[i].z - mean) * inv * g.z + b.z;
+      o.w = (v[i].w - mean) * inv * g.w + b.w;
+      yr[c] = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// x += ls (.) yb (t = yb*ls rounded, x = x + t rounded); ln_out = LN(x).
+// HAS_LS false: unscaled residual add.  One wave per row.
+// ---------------------------------------------------------------------------
+template <int NV, typename PT, bool HAS_LS>
+__global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
+    float* __restrict__ x, const float* __restrict__ yb, const PT* __restrict__ ls,
+    const PT* __restrict__ gamma, const PT* __restrict__ beta,
+    float* __restrict__ ln_out, int rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nvec = cols >> 2;
+  const size_t base = static_cast<size_t>(row) * cols;
+  float4* xr = reinterpret_cast<float4*>(x + base);
+  const float4* yr = reinterpret_cast<const float4*>(yb + base);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    if (c < nvec) {
+      float4 a = xr[c];
+      const float4 b = yr[c];
+      if (HAS_LS) {
+        const float4 g = Param<PT>::load4(ls, c);
+        float t;
+        t = b.x * g.x; a.x = a.x + t;
+        t = b.y * g.y; a.y = a.y + t;
+        t = b.z * g.z; a.z = a.z + t;
+        t = b.w * g.w; a.w = a.w + t;
+      } else {
+        a.x = a.x + b.x;
+        a.y = a.y + b.y;
+        a.z = a.z + b.z;
+        a.w = a.w + b.w;
+      }
+      xr[c] = a;
+      v[i] = a;
+      s += a.x;
+      s += a.y;
+      s += a.z;
+      s += a.w;
+    } else {
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  s = vkd::wave_sum(s);
+  const float mean = s / static_cast<float>(cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    if (c < nvec) {
+      float d;
+      d = v[i].x - mean; q += d * d;
+      d = v[i].y - mean; q += d * d;
+      d = v[i].z - mean; q += d * d;
+      d = v[i].w - mean; q += d * d;
+    }
+  }
+  q = vkd::wave_sum(q);
+  const float var = q / static_cast<float>(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+  float4* outr = reinterpret_cast<float4*>(ln_out + base);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    if (c < nvec) {
+      const float4 g = Param<PT>::load4(gamma, c);
+      const float4 b = Param<PT>::load4(beta, c);
+      float4 o;
+      o.x = (v[i].x - mean) * inv * g.x + b.x;
+      o.y = (v[i].y - mean) * inv * g.y + b.y;
+      o.z = (v[i].z - mean) * inv * g.z + b.z;
+      o.w = (v[i].w - mean) * inv * g.w + b.w;
+      outr[c] = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q/K LayerNorm (head_dim 64) + 2D RoPE, in place.
+// ---------------------------------------------------------------------------
+enum PosMode { kPosExplicit = 0, kPosGrid = 1 };
+
+struct QkShape {
+  long long rows_per_tensor;  // heads * total tokens
+  int heads;
+  int tokens_per_view;        // reference form: == total tokens
+  int view_count;
+  int n_special;
+  int gw;
+  int global;
+  int layout;                 // vk_qk_layout
+};
+
+// cos/sin for a coordinate outside the table: angle rounded in f32, trig in
+// double, as the host table does.
+__device__ __forceinline__ void rope_cs_slow(const float* __restrict__ table, int p, int j,
+                                             float* c, float* s) {
+  const float inv_freq = table[(vk::kRopeTableMax + 1) * 32 + j];
+  const float angle = static_cast<float>(p) * inv_freq;
+  *c = static_cast<float>(cos(static_cast<double>(angle)));
+  *s = static_cast<float>(sin(static_cast<double>(angle)));
+}
+
+__device__ __forceinline__ float4 swizzle_xor4(float4 v) {
+  // ds_swizzle bit-mask mode: and_mask 0x1f, or_mask 0, xor_mask 4.
+  constexpr int pat = (4 << 10) | 0x1f;
+  float4 r;
+  r.x = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.x), pat));
+  r.y = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.y), pat));
+  r.z = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.z), pat));
+  r.w = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.w), pat));
+  return r;
+}
+
+template <typename PT, bool HAS_NORM, int POS>
+__global__ __launch_bounds__(256) void qk_norm_rope_rows(
+    float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
+    const PT* __restrict__ qb, const PT* __restrict__ kg, const PT* __restrict__ kb,
+    const float* __restrict__ pos_yx, const float* __restrict__ table, QkShape sh,
+    float eps) {
+  const int l = threadIdx.x & 15;
+  const long long gr = static_cast<long long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const bool valid = gr < 2 * sh.rows_per_tensor;
+  const bool is_k = gr >= sh.rows_per_tensor;
+  const long long r = is_k ? gr - sh.rows_per_tensor : gr;
+
+  // token (sequence index) of this row
+  int py = 0, px = 0;
+  if (valid) {
+    long long t;       // index in the position sequence
+    int lt;            // index inside its view
+    if (sh.layout == VK_QK_HEADS_OUTER) {
+      const long long ntok = static_cast<long long>(sh.tokens_per_view) * sh.view_count;
+      t = r % ntok;
+      lt = static_cast<int>(t % sh.tokens_per_view);
+    } else {
+      const long long per_view = static_cast<long long>(sh.heads) * sh.tokens_per_view;
+      const long long v = r / per_view;
+      lt = static_cast<int>(r % sh.tokens_per_view);
+      t = v * sh.tokens_per_view + lt;
+    }
+    if (POS == kPosExplicit) {
+      py = static_cast<int>(pos_yx[2 * t]);
+      px = static_cast<int>(pos_yx[2 * t + 1]);
+    } else if (lt >= sh.n_special) {
+      if (sh.global) {
+        py = 1;
+        px = 1;
+      } else {
+        const int p = lt - sh.n_special;
+        py = p / sh.gw + 1;
+        px = p % sh.gw + 1;
+      }
+    }
+  }
+
+  float4* row = reinterpret_cast<float4*>((is_k ? k : q) + r * 64);
+  float4 v = valid ? row[l] : make_float4(0.f, 0.f, 0.f, 0.f);
+
+  if (HAS_NORM) {
+    float s = v.x;
+    s += v.y;
+    s += v.z;
+    s += v.w;
+    s = vkd::row16_sum(s);
+    const float mean = s / 64.0f;
+    float d, sq;
+    d = v.x - mean; sq = d * d;
+    d = v.y - mean; sq += d * d;
+    d = v.z - mean; sq += d * d;
+    d = v.w - mean; sq += d * d;
+    sq = vkd::row16_sum(sq);
+    const float var = sq / 64.0f;
+    const float inv = 1.0f / sqrtf(var + eps);
+    const PT* g = is_k ? kg : qg;
+    const PT* b = is_k ? kb : qb;
+    const float4 gv = Param<PT>::load4(g, l);
+    const float4 bv = Param<PT>::load4(b, l);
+    v.x = (v.x - mean) * inv * gv.x + bv.x;
+    v.y = (v.y - mean) * inv * gv.y + bv.y;
+    v.z = (v.z - mean) * inv * gv.z + bv.z;
+    v.w = (v.w - mean) * inv * gv.w + bv.w;
+  }
+
+  // RoPE.  Lanes 0-7 hold the y half (elements 0..31), lanes 8-15 the x half.
+  // Inside a half, lanes with bit 2 clear hold elements j (j < 16) and rotate
+  // against the lane 4 above, which holds element j + 16.
+  const int coord = (l < 8) ? py : px;
+  const int j0 = (l & 3) * 4;
+  float4 c, s;
+  if (coord >= 0 && coord <= vk::kRopeTableMax) {
+    const float* e = table + static_cast<size_t>(coord) * 32;
+    c = *reinterpret_cast<const float4*>(e + j0);
+    s = *reinterpret_cast<const float4*>(e + 16 + j0);
+  } else {
+    rope_cs_slow(table, coord, j0 + 0, &c.x, &s.x);
+    rope_cs_slow(table, coord, j0 + 1, &c.y, &s.y);
+    rope_cs_slow(table, coord, j0 + 2, &c.z, &s.z);
+    rope_cs_slow(table, coord, j0 + 3, &c.w, &s.w);
+  }
+  const float4 p = swizzle_xor4(v);
+  float4 o;
+  if ((l & 4) == 0) {
+    // out[j] = x[j]*cos - x[j+16]*sin
+    o.x = v.x * c.x + (-p.x) * s.x;
+    o.y = v.y * c.y + (-p.y) * s.y;
+    o.z = v.z * c.z + (-p.z) * s.z;
+    o.w = v.w * c.w + (-p.w) * s.w;
+  } else {
+    // out[j+16] = x[j+16]*cos + x[j]*sin
+    o.x = v.x * c.x + p.x * s.x;
+    o.y = v.y * c.y + p.y * s.y;
+    o.z = v.z * c.z + p.z * s.z;
+    o.w = v.w * c.w + p.w * s.w;
+  }
+  if (valid) row[l] = o;
+}
+
+// positions tensor [rows*2] as the reference's host builder produces it
+__global__ void rope_positions_kernel(float* __restrict__ pos, long long rows,
+                                      int tokens_per_view, int n_special, int gw,
+                                      int global) {
+  const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= rows) return;
+  const int lt = static_cast<int>(t % tokens_per_view);
+  float y = 0.0f, x = 0.0f;
+  if (lt >= n_special) {
+    if (global) {
+      y = 1.0f;
+      x = 1.0f;
+    } else {
+      const int p = lt - n_special;
+      y = static_cast<float>(p / gw + 1);
+      x = static_cast<float>(p % gw + 1);
+    }
+  }
+  pos[2 * t] = y;
+  pos[2 * t + 1] = x;
+}
+
+// ---------------------------------------------------------------------------
+// host dispatch helpers
+// ---------------------------------------------------------------------------
+
+bool param_ok(const vk_tensor* t, size_t len) {
+  return t && (t->dtype == VK_F32 || t->dtype == VK_F16) && t->len == len;
+}
+
+int ln_instance_cols(int cols) {
+  int nv = (cols + 255) / 256;
+  if (nv <= 8) return nv;
+  if (nv <= 12) return 12;
+  if (nv <= 16) return 16;
+  if (nv <= 32) return 32;
+  return -1;
+}
+
+template <typename PT>
+int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
+                     const void* b, int rows, int cols, float eps) {
+  const int nv = ln_instance_cols(cols);
+  dim3 grid((rows + 3) / 4), block(256);
+  auto G = static_cast<const PT*>(g);
+  auto B = static_cast<const PT*>(b);
+#define VK_LN_CASE(N) \
+  case N: hipLaunchKernelGGL((layernorm_rows<N, PT>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); break;
+  switch (nv) {
+    VK_LN_CASE(1) VK_LN_CASE(2) VK_LN_CASE(3) VK_LN_CASE(4)
+    VK_LN_CASE(5) VK_LN_CASE(6) VK_LN_CASE(7) VK_LN_CASE(8)
+    VK_LN_CASE(12) VK_LN_CASE(16) VK_LN_CASE(32)
+    default:
+      return vk::set_error(VK_ERR_UNSUPPORTED, "layernorm: no instance for cols=%d", cols);
+  }
+#undef VK_LN_CASE
+  return vk::check_launch("layernorm_rows");
+}
+
+template <typename PT, bool HAS_LS>
+int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
+                     const void* g, const void* b, float* out, int rows, int cols,
+                     float eps) {
+  const int nv = ln_instance_cols(cols);
+  dim3 grid((rows + 3) / 4), block(256);
+  auto LS = static_cast<const PT*>(ls);
+  auto G = static_cast<const PT*>(g);
+  auto B = static_cast<const PT*>(b);
+#define VK_LSLN_CASE(N) \
+  case N: hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps); break;
+  switch (nv) {
+    VK_LSLN_CASE(1) VK_LSLN_CASE(2) VK_LSLN_CASE(3) VK_LSLN_CASE(4)
+    VK_LSLN_CASE(5) VK_LSLN_CASE(6) VK_LSLN_CASE(7) VK_LSLN_CASE(8)
+    VK_LSLN_CASE(12) VK_LSLN_CASE(16) VK_LSLN_CASE(32)
+    default:
+      return vk::set_error(VK_ERR_UNSUPPORTED, "ls_residual_layernorm: no instance for cols=%d", cols);
+  }
+#undef VK_LSLN_CASE
+  return vk::check_launch("ls_residual_layernorm_rows");
+}
+
+template <typename PT, bool HAS_NORM, int POS>
+int launch_qk(vk_runtime* rt, float* q, float* k, const void* qg, const void* qb,
+              const void* kg, const void* kb, const float* pos, const float* table,
+              const QkShape& sh, float eps) {
+  const long long total = 2 * sh.rows_per_tensor;
+  const long long blocks = (total + 15) / 16;
+  hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(256), 0, rt->stream, q, k, static_cast<const PT*>(qg),
+                     static_cast<const PT*>(qb), static_cast<const PT*>(kg),
+                     static_cast<const PT*>(kb), pos, table, sh, eps);
+  return vk::check_launch("qk_norm_rope_rows");
+}
+
+template <int POS>
+int dispatch_qk(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_tensor* qg,
+                const vk_tensor* qb, const vk_tensor* kg, const vk_tensor* kb,
+                const float* pos, const float* table, const QkShape& sh, float eps) {
+  float* Q = static_cast<float*>(q->ptr);
+  float* K = static_cast<float*>(k->ptr);
+  if (!qg) return launch_qk<float, false, POS>(rt, Q, K, nullptr, nullptr, nullptr, nullptr, pos, table, sh, eps);
+  if (qg->dtype == VK_F16)
+    return launch_qk<uint16_t, true, POS>(rt, Q, K, qg->ptr, qb->ptr, kg->ptr, kb->ptr, pos, table, sh, eps);
+  return launch_qk<float, true, POS>(rt, Q, K, qg->ptr, qb->ptr, kg->ptr, kb->ptr, pos, table, sh, eps);
+}
+
+int check_qk_params(const vk_tensor* qg, const vk_tensor* qb, const vk_tensor* kg,
+                    const vk_tensor* kb, size_t head_dim) {
+  const bool any = qg || qb || kg || kb;
+  const bool all = qg && qb && kg && kb;
+  VK_REQUIRE(!any || all, "q/k norm parameters must be all present or all null");
+  if (all) {
+    VK_REQUIRE(param_ok(qg, head_dim) && param_ok(qb, head_dim) && param_ok(kg, head_dim) &&
+                   param_ok(kb, head_dim),
+               "q/k norm parameters must be f32 or f16 vectors of head_dim=%zu", head_dim);
+    VK_REQUIRE(qg->dtype == qb->dtype && qg->dtype == kg->dtype && qg->dtype == kb->dtype,
+               "q/k norm parameters must share one dtype");
+  }
+  return VK_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int vk_layernorm_into_f32(vk_runtime* rt, const vk_tensor* x, const vk_tensor* gamma,
+                          const vk_tensor* beta, size_t rows, size_t cols, float eps,
+                          vk_tensor* out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(x && out, "null tensor");
+  VK_REQUIRE(x->dtype == VK_F32 && out->dtype == VK_F32, "layernorm activations must be f32");
+  VK_REQUIRE(x->len == rows * cols && out->len == rows * cols,
+             "layernorm: x (%zu) / out (%zu) must hold rows*cols=%zu", x->len, out->len,
+             rows * cols);
+  VK_REQUIRE(param_ok(gamma, cols) && param_ok(beta, cols) && gamma->dtype == beta->dtype,
+             "layernorm: gamma/beta must be f32 or f16 vectors of cols=%zu", cols);
+  VK_UNSUPPORTED_IF(cols == 0 || cols % 4 != 0 || cols > 8192,
+                    "layernorm: cols=%zu (need a multiple of 4 up to 8192)", cols);
+  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "layernorm: rows=%zu too large", rows);
+  if (rows == 0) return VK_OK;
+  const float* X = static_cast<const float*>(x->ptr);
+  float* Y = static_cast<float*>(out->ptr);
+  const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+  VK_UNSUPPORTED_IF(ln_instance_cols(c) < 0, "layernorm: cols=%zu", cols);
+  if (gamma->dtype == VK_F16)
+    return launch_layernorm<uint16_t>(rt, X, Y, gamma->ptr, beta->ptr, r, c, eps);
+  return launch_layernorm<float>(rt, X, Y, gamma->ptr, beta->ptr, r, c, eps);
+}
+
+int vk_layernorm_f32(vk_runtime* rt, const vk_tensor* x, const vk_tensor* gamma,
+                     const vk_tensor* beta, size_t rows, size_t cols, float eps,
+                     vk_tensor** out) {
+  VK_REQUIRE(out != nullptr, "null output handle");
+  vk_tensor* t = nullptr;
+  VK_TRY(vk_tensor_alloc(rt, VK_F32, rows * cols, &t));
+  int s = vk_layernorm_into_f32(rt, x, gamma, beta, rows, cols, eps, t);
+  if (s != VK_OK) {
+    vk_tensor_destroy(t);
+    return s;
+  }
+  *out = t;
+  return VK_OK;
+}
+
+int vk_layerscale_residual_layernorm_f32(vk_runtime* rt, vk_tensor* x, const vk_tensor* y,
+                                         const vk_tensor* ls_gamma,
+                                         const vk_tensor* ln_gamma,
+                                         const vk_tensor* ln_beta, size_t rows,
+                                         size_t cols, float eps, vk_tensor* ln_out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(x && y && ln_out, "null tensor");
+  VK_REQUIRE(x->dtype == VK_F32 && y->dtype == VK_F32 && ln_out->dtype == VK_F32,
+             "activations must be f32");
+  VK_REQUIRE(x->len == rows * cols && y->len == rows * cols && ln_out->len == rows * cols,
+             "x, y and ln_out must hold rows*cols=%zu", rows * cols);
+  VK_REQUIRE(x->ptr != y->ptr && x->ptr != ln_out->ptr && y->ptr != ln_out->ptr,
+             "x, y and ln_out must be distinct buffers");
+  VK_REQUIRE(param_ok(ln_gamma, cols) && param_ok(ln_beta, cols) &&
+                 ln_gamma->dtype == ln_beta->dtype,
+             "LayerNorm gamma/beta must be f32 or f16 vectors of cols=%zu", cols);
+  VK_REQUIRE(!ls_gamma || (param_ok(ls_gamma, cols) && ls_gamma->dtype == ln_gamma->dtype),
+             "LayerScale gamma must be a vector of cols=%zu with the LayerNorm dtype", cols);
+  VK_UNSUPPORTED_IF(cols == 0 || cols % 4 != 0 || cols > 8192 || ln_instance_cols(static_cast<int>(cols)) < 0,
+                    "ls_residual_layernorm: cols=%zu", cols);
+  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "rows=%zu too large", rows);
+  if (rows == 0) return VK_OK;
+  float* X = static_cast<float*>(x->ptr);
+  const float* Yb = static_cast<const float*>(y->ptr);
+  float* O = static_cast<float*>(ln_out->ptr);
+  const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+  const void* ls = ls_gamma ? ls_gamma->ptr : nullptr;
+  if (ln_gamma->dtype == VK_F16) {
+    return ls ? launch_ls_res_ln<uint16_t, true>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps)
+              : launch_ls_res_ln<uint16_t, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps);
+  }
+  return ls ? launch_ls_res_ln<float, true>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps)
+            : launch_ls_res_ln<float, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps);
+}
+
+int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_tensor* q_gamma,
+                        const vk_tensor* q_beta, const vk_tensor* k_gamma,
+                        const vk_tensor* k_beta, const vk_tensor* positions, size_t heads,
+                        size_t rows, float freq, float eps) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(q && k && positions, "null tensor");
+  VK_REQUIRE(q->dtype == VK_F32 && k->dtype == VK_F32 && positions->dtype == VK_F32,
+             "q, k and positions must be f32");
+  const size_t head_dim = 64;
+  VK_REQUIRE(heads > 0 && q->len == heads * rows * head_dim && k->len == q->len,
+             "q/k must hold heads*rows*64 = %zu elements (q %zu, k %zu)",
+             heads * rows * head_dim, q->len, k->len);
+  VK_REQUIRE(positions->len == rows * 2, "positions must hold rows*2 = %zu (got %zu)",
+             rows * 2, positions->len);
+  VK_REQUIRE(q->ptr != k->ptr, "q and k must be distinct buffers");
+  VK_TRY(check_qk_params(q_gamma, q_beta, k_gamma, k_beta, head_dim));
+  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "rows=%zu too large", rows);
+  if (rows == 0) return VK_OK;
+  const float* table = nullptr;
+  VK_TRY(vk::rope_table(rt, freq, 64, &table));
+  QkShape sh;
+  sh.rows_per_tensor = static_cast<long long>(heads * rows);
+  sh.heads = static_cast<int>(heads);
+  sh.tokens_per_view = static_cast<int>(rows);
+  sh.view_count = 1;
+  sh.n_special = 0;
+  sh.gw = 1;
+  sh.global = 0;
+  sh.layout = VK_QK_HEADS_OUTER;
+  return dispatch_qk<kPosExplicit>(rt, q, k, q_gamma, q_beta, k_gamma, k_beta,
+                                   static_cast<const float*>(positions->ptr), table, sh, eps);
+}
+
+int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                             const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                             const vk_tensor* k_gamma, const vk_tensor* k_beta, size_t heads,
+                             size_t head_dim, size_t n_special, size_t gh, size_t gw,
+                             size_t view_count, int global, vk_qk_layout layout, float freq,
+                             float eps) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(q && k, "null tensor");
+  VK_REQUIRE(q->dtype == VK_F32 && k->dtype == VK_F32, "q and k must be f32");
+  VK_UNSUPPORTED_IF(head_dim != 64, "qk_norm_rope: head_dim=%zu (qualified: 64)", head_dim);
+  VK_REQUIRE(layout == VK_QK_HEADS_OUTER || layout == VK_QK_VIEWS_OUTER, "unknown layout %d",
+             static_cast<int>(layout));
+  VK_REQUIRE(view_count > 0 && heads > 0 && gw > 0, "view_count, heads and gw must be > 0");
+  const size_t tpv = n_special + gh * gw;
+  const size_t rows = tpv * view_count;
+  VK_REQUIRE(q->len == heads * rows * head_dim && k->len == q->len,
+             "q/k must hold heads*view_count*(n_special+gh*gw)*64 = %zu (q %zu, k %zu)",
+             heads * rows * head_dim, q->len, k->len);
+  VK_REQUIRE(q->ptr != k->ptr, "q and k must be distinct buffers");
+  VK_TRY(check_qk_params(q_gamma, q_beta, k_gamma, k_beta, head_dim));
+  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "rows=%zu too large", rows);
+  if (rows == 0) return VK_OK;
+  const float* table = nullptr;
+  VK_TRY(vk::rope_table(rt, freq, 64, &table));
+  QkShape sh;
+  sh.rows_per_tensor = static_cast<long long>(heads * rows);
+  sh.heads = static_cast<int>(heads);
+  sh.tokens_per_view = static_cast<int>(tpv);
+  sh.view_count = static_cast<int>(view_count);
+  sh.n_special = static_cast<int>(n_special);
+  sh.gw = static_cast<int>(gw);
+  sh.global = global ? 1 : 0;
+  sh.layout = layout;
+  return dispatch_qk<kPosGrid>(rt, q, k, q_gamma, q_beta, k_gamma, k_beta, nullptr, table, sh,
+                               eps);
+}
+
+int vk_rope_positions_f32(vk_runtime* rt, size_t n_special, size_t gh, size_t gw,
+                          size_t view_count, int global, vk_tensor** out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(out != nullptr, "null output handle");
+  VK_REQUIRE(gw > 0 && view_count > 0, "gw and view_count must be > 0");
+  const size_t tpv = n_special + gh * gw;
+  const size_t rows = tpv * view_count;
+  vk_tensor* t = nullptr;
+  VK_TRY(vk_tensor_alloc(rt, VK_F32, rows * 2, &t));
+  if (rows > 0) {
+    const unsigned blocks = static_cast<unsigned>((rows + 255) / 256);
+    hipLaunchKernelGGL(rope_positions_kernel, dim3(blocks), dim3(256), 0, rt->stream,
+                       static_cast<float*>(t->ptr), static_cast<long long>(rows),
+                       static_cast<int>(tpv), static_cast<int>(n_special),
+                       static_cast<int>(gw), global ? 1 : 0);
+    int s = vk::check_launch("rope_positions_kernel");
+    if (s != VK_OK) {
+      vk_tensor_destroy(t);
+      return s;
+    }
+  }
+  *out = t;
+  return VK_OK;
+}
+
+}  // extern "C"

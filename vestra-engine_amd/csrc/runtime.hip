@@ -1,0 +1,396 @@
+// Runtime, tensors, transfers, events and graphs of the C ABI.
+//
+// Mirrors the host-facing half of the reference's device runtime
+// (`vestra_kernels::cuda::CudaRuntime`: new/upload/download/copy/segment
+// copies/prefix overwrite, called from crates/da-engine/src/vit_block.rs:
+// 161-184, 335, 370, 402-478 and backbone.rs:991-1027).
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+
+namespace vk {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int hip_fail(hipError_t e, const char* what) {
+  const int code = (e == hipErrorOutOfMemory) ? VK_ERR_OOM : VK_ERR_HIP;
+  return set_error(code, "%s failed: %s (%d)", what, hipGetErrorString(e),
+                   static_cast<int>(e));
+}
+
+size_t dtype_size(vk_dtype d) {
+  switch (d) {
+    case VK_F32: return 4;
+    case VK_F16: return 2;
+    case VK_U8: return 1;
+  }
+  return 0;
+}
+
+int bind(vk_runtime* rt) {
+  VK_REQUIRE(rt != nullptr, "null runtime");
+  int cur = -1;
+  VK_HIP(hipGetDevice(&cur));
+  if (cur != rt->device) VK_HIP(hipSetDevice(rt->device));
+  return VK_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, what);
+  return VK_OK;
+}
+
+// Host build of the RoPE cos/sin table for head_dim 64 (two rotary halves of
+// 32, 16 frequency pairs each).  inv_freq_j = 1 / base^((2j)/32), each step in
+// f32; angle = (f32)p * inv_freq_j as one f32 product; cos/sin evaluated in
+// double and rounded once (the published RotaryPositionEmbedding2D of
+// Depth-Anything-3 computes the same f32 angle).
+int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out) {
+  VK_UNSUPPORTED_IF(head_dim != 64, "RoPE table supports head_dim 64 (got %d)",
+                    head_dim);
+  uint32_t fbits;
+  std::memcpy(&fbits, &freq, sizeof fbits);
+  auto key = std::make_pair(fbits, head_dim);
+  auto it = rt->rope_tables.find(key);
+  if (it != rt->rope_tables.end()) {
+    *out = it->second;
+    return VK_OK;
+  }
+  const int half = head_dim / 2;
+  const int quarter = half / 2;
+  std::vector<float> inv_freq(quarter);
+  for (int j = 0; j < quarter; ++j) {
+    const float e = static_cast<float>(2 * j) / static_cast<float>(half);
+    inv_freq[j] = 1.0f / std::pow(freq, e);
+  }
+  const size_t entries = static_cast<size_t>(kRopeTableMax) + 1;
+  std::vector<float> host(entries * 32 + 16, 0.0f);
+  for (size_t p = 0; p < entries; ++p) {
+    for (int j = 0; j < quarter; ++j) {
+      const float angle = static_cast<float>(p) * inv_freq[j];
+      host[p * 32 + j] = static_cast<float>(std::cos(static_cast<double>(angle)));
+      host[p * 32 + 16 + j] = static_cast<float>(std::sin(static_cast<double>(angle)));
+    }
+  }
+  for (int j = 0; j < quarter; ++j) host[entries * 32 + j] = inv_freq[j];
+  VK_TRY(bind(rt));
+  float* dev = nullptr;
+  VK_HIP(hipMalloc(&dev, host.size() * sizeof(float)));
+  hipError_t e = hipMemcpy(dev, host.data(), host.size() * sizeof(float),
+                           hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(dev);
+    return hip_fail(e, "hipMemcpy(rope table)");
+  }
+  rt->rope_tables[key] = dev;
+  *out = dev;
+  return VK_OK;
+}
+
+static int new_tensor(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** out) {
+  VK_REQUIRE(out != nullptr, "null output handle");
+  VK_REQUIRE(dtype == VK_F32 || dtype == VK_F16 || dtype == VK_U8,
+             "unknown dtype %d", static_cast<int>(dtype));
+  VK_TRY(bind(rt));
+  void* p = nullptr;
+  if (len > 0) VK_HIP(hipMalloc(&p, len * dtype_size(dtype)));
+  auto* t = new vk_tensor;
+  t->rt = rt;
+  t->ptr = p;
+  t->len = len;
+  t->dtype = dtype;
+  t->owned = true;
+  *out = t;
+  return VK_OK;
+}
+
+static int upload(vk_runtime* rt, vk_dtype dtype, const void* host, size_t len,
+                  vk_tensor** out) {
+  VK_REQUIRE(host != nullptr || len == 0, "null host pointer");
+  vk_tensor* t = nullptr;
+  VK_TRY(new_tensor(rt, dtype, len, &t));
+  if (len > 0) {
+    hipError_t e = hipMemcpyAsync(t->ptr, host, len * dtype_size(dtype),
+                                  hipMemcpyHostToDevice, rt->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) {
+      vk_tensor_destroy(t);
+      return hip_fail(e, "upload");
+    }
+  }
+  *out = t;
+  return VK_OK;
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" {
+
+const char* vk_last_error(void) { return g_last_error.c_str(); }
+
+int vk_abi_version(void) { return VK_ABI_VERSION; }
+
+int vk_runtime_create(int device, vk_runtime** out) {
+  clear_error();
+  VK_REQUIRE(out != nullptr, "null output handle");
+  int count = 0;
+  VK_HIP(hipGetDeviceCount(&count));
+  VK_REQUIRE(device >= 0 && device < count, "device %d out of range (%d devices)",
+             device, count);
+  VK_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  VK_HIP(hipGetDeviceProperties(&prop, device));
+  auto* rt = new vk_runtime;
+  rt->device = device;
+  rt->cu_count = prop.multiProcessorCount;
+  // Default priority, non-blocking with respect to the null stream.
+  hipError_t e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete rt;
+    return hip_fail(e, "hipStreamCreateWithFlags");
+  }
+  *out = rt;
+  return VK_OK;
+}
+
+int vk_runtime_destroy(vk_runtime* rt) {
+  if (!rt) return VK_OK;
+  VK_TRY(bind(rt));
+  (void)hipStreamSynchronize(rt->stream);
+  for (auto& kv : rt->rope_tables) (void)hipFree(kv.second);
+  (void)hipStreamDestroy(rt->stream);
+  delete rt;
+  return VK_OK;
+}
+
+int vk_runtime_synchronize(vk_runtime* rt) {
+  VK_TRY(bind(rt));
+  VK_HIP(hipStreamSynchronize(rt->stream));
+  return VK_OK;
+}
+
+void* vk_runtime_stream(vk_runtime* rt) { return rt ? static_cast<void*>(rt->stream) : nullptr; }
+
+int vk_runtime_cu_count(vk_runtime* rt) { return rt ? rt->cu_count : 0; }
+
+int vk_tensor_alloc(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** out) {
+  return new_tensor(rt, dtype, len, out);
+}
+
+int vk_tensor_wrap(vk_runtime* rt, vk_dtype dtype, void* device_ptr, size_t len,
+                   vk_tensor** out) {
+  VK_REQUIRE(rt != nullptr && out != nullptr, "null runtime or output handle");
+  VK_REQUIRE(device_ptr != nullptr || len == 0, "null device pointer");
+  VK_REQUIRE(dtype_size(dtype) != 0, "unknown dtype %d", static_cast<int>(dtype));
+  auto* t = new vk_tensor;
+  t->rt = rt;
+  t->ptr = device_ptr;
+  t->len = len;
+  t->dtype = dtype;
+  t->owned = false;
+  *out = t;
+  return VK_OK;
+}
+
+int vk_tensor_destroy(vk_tensor* t) {
+  if (!t) return VK_OK;
+  if (t->owned && t->ptr) {
+    VK_TRY(bind(t->rt));
+    // Stream-ordered: pending kernels that read the buffer finish first.
+    (void)hipStreamSynchronize(t->rt->stream);
+    VK_HIP(hipFree(t->ptr));
+  }
+  delete t;
+  return VK_OK;
+}
+
+size_t vk_tensor_len(const vk_tensor* t) { return t ? t->len : 0; }
+
+int vk_tensor_dtype(const vk_tensor* t) { return t ? static_cast<int>(t->dtype) : -1; }
+
+void* vk_tensor_device_ptr(const vk_tensor* t) { return t ? t->ptr : nullptr; }
+
+int vk_upload_f32(vk_runtime* rt, const float* host, size_t len, vk_tensor** out) {
+  return upload(rt, VK_F32, host, len, out);
+}
+
+int vk_upload_f16(vk_runtime* rt, const uint16_t* host, size_t len, vk_tensor** out) {
+  return upload(rt, VK_F16, host, len, out);
+}
+
+int vk_upload_u8(vk_runtime* rt, const uint8_t* host, size_t len, vk_tensor** out) {
+  return upload(rt, VK_U8, host, len, out);
+}
+
+static int write_host(vk_runtime* rt, vk_tensor* t, vk_dtype dtype,
+                      const void* host, size_t len) {
+  VK_REQUIRE(t != nullptr && (host != nullptr || len == 0), "null tensor or host pointer");
+  VK_REQUIRE(t->dtype == dtype, "tensor dtype %d, expected %d",
+             static_cast<int>(t->dtype), static_cast<int>(dtype));
+  VK_REQUIRE(t->len == len, "length mismatch: tensor %zu, host %zu", t->len, len);
+  VK_TRY(bind(rt));
+  if (len == 0) return VK_OK;
+  VK_HIP(hipMemcpyAsync(t->ptr, host, len * dtype_size(dtype), hipMemcpyHostToDevice,
+                        rt->stream));
+  VK_HIP(hipStreamSynchronize(rt->stream));
+  return VK_OK;
+}
+
+int vk_write_f32(vk_runtime* rt, vk_tensor* t, const float* host, size_t len) {
+  return write_host(rt, t, VK_F32, host, len);
+}
+
+int vk_write_u8(vk_runtime* rt, vk_tensor* t, const uint8_t* host, size_t len) {
+  return write_host(rt, t, VK_U8, host, len);
+}
+
+int vk_download_f32(vk_runtime* rt, const vk_tensor* t, float* host, size_t len) {
+  VK_REQUIRE(t != nullptr && (host != nullptr || len == 0), "null tensor or host pointer");
+  VK_REQUIRE(t->dtype == VK_F32, "download_f32 of a non-f32 tensor");
+  VK_REQUIRE(t->len == len, "length mismatch: tensor %zu, host %zu", t->len, len);
+  VK_TRY(bind(rt));
+  if (len > 0)
+    VK_HIP(hipMemcpyAsync(host, t->ptr, len * 4, hipMemcpyDeviceToHost, rt->stream));
+  VK_HIP(hipStreamSynchronize(rt->stream));
+  return VK_OK;
+}
+
+int vk_copy_f32(vk_runtime* rt, const vk_tensor* src, vk_tensor** out) {
+  VK_REQUIRE(src != nullptr, "null source");
+  return vk_copy_segment_f32(rt, src, 0, src->len, out);
+}
+
+int vk_copy_segment_f32(vk_runtime* rt, const vk_tensor* src, size_t offset,
+                        size_t len, vk_tensor** out) {
+  VK_REQUIRE(src != nullptr && out != nullptr, "null source or output handle");
+  VK_REQUIRE(src->dtype == VK_F32, "copy_segment_f32 of a non-f32 tensor");
+  VK_REQUIRE(offset <= src->len && len <= src->len - offset,
+             "segment [%zu, +%zu) outside tensor of %zu", offset, len, src->len);
+  vk_tensor* t = nullptr;
+  VK_TRY(new_tensor(rt, VK_F32, len, &t));
+  if (len > 0) {
+    hipError_t e = hipMemcpyAsync(t->ptr, static_cast<const float*>(src->ptr) + offset,
+                                  len * 4, hipMemcpyDeviceToDevice, rt->stream);
+    if (e != hipSuccess) {
+      vk_tensor_destroy(t);
+      return hip_fail(e, "copy_segment");
+    }
+  }
+  *out = t;
+  return VK_OK;
+}
+
+int vk_copy_segment_into_f32(vk_runtime* rt, vk_tensor* dst, size_t dst_offset,
+                             const vk_tensor* src, size_t src_offset, size_t len) {
+  VK_REQUIRE(dst != nullptr && src != nullptr, "null tensor");
+  VK_REQUIRE(dst->dtype == VK_F32 && src->dtype == VK_F32, "non-f32 tensor");
+  VK_REQUIRE(src_offset <= src->len && len <= src->len - src_offset,
+             "source segment [%zu, +%zu) outside tensor of %zu", src_offset, len, src->len);
+  VK_REQUIRE(dst_offset <= dst->len && len <= dst->len - dst_offset,
+             "destination segment [%zu, +%zu) outside tensor of %zu", dst_offset, len,
+             dst->len);
+  VK_TRY(bind(rt));
+  if (len == 0) return VK_OK;
+  VK_HIP(hipMemcpyAsync(static_cast<float*>(dst->ptr) + dst_offset,
+                        static_cast<const float*>(src->ptr) + src_offset, len * 4,
+                        hipMemcpyDeviceToDevice, rt->stream));
+  return VK_OK;
+}
+
+int vk_overwrite_prefix_f32(vk_runtime* rt, vk_tensor* tokens, const vk_tensor* prefix,
+                            size_t len) {
+  return vk_copy_segment_into_f32(rt, tokens, 0, prefix, 0, len);
+}
+
+int vk_event_create(vk_runtime* rt, vk_event** out) {
+  VK_REQUIRE(out != nullptr, "null output handle");
+  VK_TRY(bind(rt));
+  auto* e = new vk_event;
+  e->rt = rt;
+  hipError_t err = hipEventCreate(&e->ev);
+  if (err != hipSuccess) {
+    delete e;
+    return hip_fail(err, "hipEventCreate");
+  }
+  *out = e;
+  return VK_OK;
+}
+
+int vk_event_destroy(vk_event* ev) {
+  if (!ev) return VK_OK;
+  (void)hipEventDestroy(ev->ev);
+  delete ev;
+  return VK_OK;
+}
+
+int vk_event_record(vk_runtime* rt, vk_event* ev) {
+  VK_REQUIRE(ev != nullptr, "null event");
+  VK_TRY(bind(rt));
+  VK_HIP(hipEventRecord(ev->ev, rt->stream));
+  return VK_OK;
+}
+
+int vk_event_elapsed_ms(vk_event* start, vk_event* stop, float* ms) {
+  VK_REQUIRE(start && stop && ms, "null argument");
+  VK_HIP(hipEventSynchronize(stop->ev));
+  VK_HIP(hipEventElapsedTime(ms, start->ev, stop->ev));
+  return VK_OK;
+}
+
+int vk_graph_begin_capture(vk_runtime* rt) {
+  VK_TRY(bind(rt));
+  VK_HIP(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal));
+  return VK_OK;
+}
+
+int vk_graph_end_capture(vk_runtime* rt, vk_graph** out) {
+  VK_REQUIRE(out != nullptr, "null output handle");
+  VK_TRY(bind(rt));
+  hipGraph_t g = nullptr;
+  VK_HIP(hipStreamEndCapture(rt->stream, &g));
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_fail(e, "hipGraphInstantiate");
+  }
+  auto* vg = new vk_graph;
+  vg->graph = g;
+  vg->exec = exec;
+  *out = vg;
+  return VK_OK;
+}
+
+int vk_graph_launch(vk_runtime* rt, vk_graph* g) {
+  VK_REQUIRE(g != nullptr, "null graph");
+  VK_TRY(bind(rt));
+  VK_HIP(hipGraphLaunch(g->exec, rt->stream));
+  return VK_OK;
+}
+
+int vk_graph_destroy(vk_graph* g) {
+  if (!g) return VK_OK;
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  delete g;
+  return VK_OK;
+}
+
+}  // extern "C"

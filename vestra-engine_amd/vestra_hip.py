@@ -1,0 +1,495 @@
+"""Python binding of libvestra_hip.so (the C ABI declared in include/vestra_hip.h).
+
+The classes mirror the reference engine's device runtime,
+``vestra_kernels::cuda::CudaRuntime`` (called from
+crates/da-engine/src/vit_block.rs:136-667 and patch_embed.rs:139-245): the
+same method names, argument meaning and error behaviour.  A failed call raises
+``VestraError`` carrying the C status and message (the reference's
+``CudaError::Kernel(String)``); ``UnsupportedShape`` marks a shape outside the
+qualified subset, which the reference maps to ``None`` / CPU fallback
+(vit_block.rs:331-333).
+
+The library must be built in-tree (``make -C vestra-engine_amd``); importing
+this module without it raises immediately -- there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvestra_hip.so")
+
+VK_OK = 0
+VK_ERR_INVALID = -1
+VK_ERR_UNSUPPORTED = -2
+VK_ERR_HIP = -3
+VK_ERR_OOM = -4
+
+VK_F32, VK_F16, VK_U8 = 0, 1, 2
+VK_QK_HEADS_OUTER, VK_QK_VIEWS_OUTER = 0, 1
+
+VK_BLOCK_FUSE_LS_LN = 1
+VK_BLOCK_SKIP_LN1 = 2
+VK_BLOCK_FUSE_NEXT_LN1 = 4
+
+QK_NORM_EPS = 1e-5  # vit_block.rs:686
+
+
+class VestraError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+class UnsupportedShape(VestraError):
+    pass
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `make -C {_HERE}` "
+            "(there is no non-HIP fallback)")
+    return C.CDLL(LIB_PATH)
+
+
+lib = _load()
+
+_vp = C.c_void_p
+_sz = C.c_size_t
+_i = C.c_int
+_f = C.c_float
+_pp = C.POINTER(C.c_void_p)
+
+
+class VitConfig(C.Structure):
+    _fields_ = [("embed_dim", _sz), ("num_heads", _sz), ("head_dim", _sz),
+                ("mlp_hidden", _sz), ("num_register", _sz), ("ln_eps", _f),
+                ("qk_norm_eps", _f), ("rope_freq", _f), ("rope_start", _i),
+                ("qknorm_start", _i), ("alt_start", _i)]
+
+
+class VitLayer(C.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "norm1_gamma", "norm1_beta", "qnorm_gamma", "qnorm_beta", "knorm_gamma",
+        "knorm_beta", "ls1", "norm2_gamma", "norm2_beta", "ls2")]
+
+
+class VitActivations(C.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "tokens", "ln1", "q", "k", "attn_proj", "ln2", "hidden", "mlp_out")]
+
+
+_SIGS = {
+    "vk_last_error": ([], C.c_char_p),
+    "vk_abi_version": ([], _i),
+    "vk_runtime_create": ([_i, _pp], _i),
+    "vk_runtime_destroy": ([_vp], _i),
+    "vk_runtime_synchronize": ([_vp], _i),
+    "vk_runtime_stream": ([_vp], _vp),
+    "vk_runtime_cu_count": ([_vp], _i),
+    "vk_tensor_alloc": ([_vp, _i, _sz, _pp], _i),
+    "vk_tensor_wrap": ([_vp, _i, _vp, _sz, _pp], _i),
+    "vk_tensor_destroy": ([_vp], _i),
+    "vk_tensor_len": ([_vp], _sz),
+    "vk_tensor_dtype": ([_vp], _i),
+    "vk_tensor_device_ptr": ([_vp], _vp),
+    "vk_upload_f32": ([_vp, _vp, _sz, _pp], _i),
+    "vk_upload_f16": ([_vp, _vp, _sz, _pp], _i),
+    "vk_upload_u8": ([_vp, _vp, _sz, _pp], _i),
+    "vk_write_f32": ([_vp, _vp, _vp, _sz], _i),
+    "vk_write_u8": ([_vp, _vp, _vp, _sz], _i),
+    "vk_download_f32": ([_vp, _vp, _vp, _sz], _i),
+    "vk_copy_f32": ([_vp, _vp, _pp], _i),
+    "vk_copy_segment_f32": ([_vp, _vp, _sz, _sz, _pp], _i),
+    "vk_copy_segment_into_f32": ([_vp, _vp, _sz, _vp, _sz, _sz], _i),
+    "vk_overwrite_prefix_f32": ([_vp, _vp, _vp, _sz], _i),
+    "vk_layernorm_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _f, _pp], _i),
+    "vk_layernorm_into_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _f, _vp], _i),
+    "vk_gelu_f32_inplace": ([_vp, _vp], _i),
+    "vk_gelu_erf_f32_inplace": ([_vp, _vp], _i),
+    "vk_add_f32_inplace": ([_vp, _vp, _vp], _i),
+    "vk_layerscale_f32_inplace": ([_vp, _vp, _vp, _sz, _sz], _i),
+    "vk_layerscale_residual_f32": ([_vp, _vp, _vp, _vp, _sz, _sz], _i),
+    "vk_layerscale_residual_layernorm_f32": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _vp], _i),
+    "vk_qk_norm_rope_f32": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _f], _i),
+    "vk_qk_norm_rope_grid_f32": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i, _f, _f], _i),
+    "vk_rope_positions_f32": ([_vp, _sz, _sz, _sz, _sz, _i, _pp], _i),
+    "vk_patchify_nchw_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _pp], _i),
+    "vk_linear_prepare_f32": ([_vp, _sz, _sz, _vp, _vp, _vp, _pp], _i),
+    "vk_linear_prepare_oihw_f32": ([_vp, _sz, _sz, _vp, _vp, _pp], _i),
+    "vk_linear_destroy": ([_vp], _i),
+    "vk_linear_input_features": ([_vp], _sz),
+    "vk_linear_run_f32": ([_vp, _vp, _vp, _sz, _pp], _i),
+    "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
+    "vk_pos_embed_bicubic_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _f, _pp], _i),
+    "vk_patch_embed_u8": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp], _i),
+    "vk_vit_block_fused_ops": (
+        [_vp, C.POINTER(VitConfig), _sz, C.POINTER(VitLayer), C.POINTER(VitLayer),
+         C.POINTER(VitActivations), _sz, _sz, _sz, _vp, C.c_uint], _i),
+    "vk_event_create": ([_vp, _pp], _i),
+    "vk_event_destroy": ([_vp], _i),
+    "vk_event_record": ([_vp, _vp], _i),
+    "vk_event_elapsed_ms": ([_vp, _vp, C.POINTER(C.c_float)], _i),
+    "vk_graph_begin_capture": ([_vp], _i),
+    "vk_graph_end_capture": ([_vp, _pp], _i),
+    "vk_graph_launch": ([_vp, _vp], _i),
+    "vk_graph_destroy": ([_vp], _i),
+}
+
+for _name, (_args, _res) in _SIGS.items():
+    _fn = getattr(lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _res
+
+
+def _check(status: int) -> None:
+    if status != VK_OK:
+        msg = lib.vk_last_error().decode(errors="replace")
+        cls = UnsupportedShape if status == VK_ERR_UNSUPPORTED else VestraError
+        raise cls(status, msg)
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    # data_as keeps a reference to the array alive as long as the pointer
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Tensor:
+    """Owned (or wrapped) device tensor: ``CudaTensorF32`` of the reference."""
+
+    def __init__(self, rt: "Runtime", handle: C.c_void_p):
+        self.rt = rt
+        self.handle = handle
+
+    def __len__(self) -> int:
+        return int(lib.vk_tensor_len(self.handle))
+
+    @property
+    def dtype(self) -> int:
+        return int(lib.vk_tensor_dtype(self.handle))
+
+    @property
+    def device_ptr(self) -> int:
+        return int(lib.vk_tensor_device_ptr(self.handle) or 0)
+
+    def numpy(self) -> np.ndarray:
+        return self.rt.download_f32(self)
+
+    def write(self, host: np.ndarray) -> None:
+        if host.dtype == np.uint8:
+            h = np.ascontiguousarray(host).reshape(-1)
+            _check(lib.vk_write_u8(self.rt.handle, self.handle, _ptr(h), h.size))
+        else:
+            h = np.ascontiguousarray(host, dtype=np.float32).reshape(-1)
+            _check(lib.vk_write_f32(self.rt.handle, self.handle, _ptr(h), h.size))
+
+    def free(self) -> None:
+        if self.handle:
+            _check(lib.vk_tensor_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.vk_tensor_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def _h(t: Optional[Tensor]):
+    return None if t is None else t.handle
+
+
+class Linear:
+    """``CudaLinearF32``: cached device weights, ``run(x, rows)``."""
+
+    def __init__(self, rt: "Runtime", handle: C.c_void_p):
+        self.rt = rt
+        self.handle = handle
+
+    def input_features(self) -> int:
+        return int(lib.vk_linear_input_features(self.handle))
+
+    def run(self, x: Tensor, rows: int) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_linear_run_f32(self.rt.handle, self.handle, x.handle, rows, C.byref(out)))
+        return Tensor(self.rt, out)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.vk_linear_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self, rt: "Runtime"):
+        self.rt = rt
+        h = C.c_void_p()
+        _check(lib.vk_event_create(rt.handle, C.byref(h)))
+        self.handle = h
+
+    def record(self) -> None:
+        _check(lib.vk_event_record(self.rt.handle, self.handle))
+
+    def elapsed_ms(self, stop: "Event") -> float:
+        ms = C.c_float()
+        _check(lib.vk_event_elapsed_ms(self.handle, stop.handle, C.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            lib.vk_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    def __init__(self, rt: "Runtime", handle: C.c_void_p):
+        self.rt = rt
+        self.handle = handle
+
+    def launch(self) -> None:
+        _check(lib.vk_graph_launch(self.rt.handle, self.handle))
+
+    def __del__(self):
+        try:
+            lib.vk_graph_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Runtime:
+    """``vestra_kernels::cuda::CudaRuntime`` on one MI355X (one HIP stream)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        _check(lib.vk_runtime_create(device, C.byref(h)))
+        self.handle = h
+
+    # -- runtime -------------------------------------------------------------
+    def synchronize(self) -> None:
+        _check(lib.vk_runtime_synchronize(self.handle))
+
+    def cu_count(self) -> int:
+        return int(lib.vk_runtime_cu_count(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib.vk_runtime_destroy(self.handle))
+            self.handle = None
+
+    # -- tensors -------------------------------------------------------------
+    def alloc_f32(self, n: int) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_tensor_alloc(self.handle, VK_F32, n, C.byref(out)))
+        return Tensor(self, out)
+
+    def upload_f32(self, host: np.ndarray) -> Tensor:
+        h = np.ascontiguousarray(host, dtype=np.float32).reshape(-1)
+        out = C.c_void_p()
+        _check(lib.vk_upload_f32(self.handle, _ptr(h), h.size, C.byref(out)))
+        return Tensor(self, out)
+
+    def upload_f16(self, host: np.ndarray) -> Tensor:
+        h = np.ascontiguousarray(host, dtype=np.float16).reshape(-1).view(np.uint16)
+        out = C.c_void_p()
+        _check(lib.vk_upload_f16(self.handle, _ptr(h), h.size, C.byref(out)))
+        return Tensor(self, out)
+
+    def upload_u8(self, host: np.ndarray) -> Tensor:
+        h = np.ascontiguousarray(host, dtype=np.uint8).reshape(-1)
+        out = C.c_void_p()
+        _check(lib.vk_upload_u8(self.handle, _ptr(h), h.size, C.byref(out)))
+        return Tensor(self, out)
+
+    def download_f32(self, t: Tensor) -> np.ndarray:
+        out = np.empty(len(t), dtype=np.float32)
+        _check(lib.vk_download_f32(self.handle, t.handle, _ptr(out), out.size))
+        return out
+
+    def copy_f32(self, t: Tensor) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_copy_f32(self.handle, t.handle, C.byref(out)))
+        return Tensor(self, out)
+
+    def copy_segment_f32(self, t: Tensor, offset: int, length: int) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_copy_segment_f32(self.handle, t.handle, offset, length, C.byref(out)))
+        return Tensor(self, out)
+
+    def copy_segment_into_f32(self, dst: Tensor, dst_offset: int, src: Tensor,
+                              src_offset: int, length: int) -> None:
+        _check(lib.vk_copy_segment_into_f32(self.handle, dst.handle, dst_offset, src.handle,
+                                            src_offset, length))
+
+    def overwrite_prefix_f32(self, tokens: Tensor, prefix: Tensor, length: int) -> None:
+        _check(lib.vk_overwrite_prefix_f32(self.handle, tokens.handle, prefix.handle, length))
+
+    # -- fused per-token operations -----------------------------------------
+    def layernorm_f32_cpu_order(self, x: Tensor, gamma: Tensor, beta: Tensor, rows: int,
+                                cols: int, eps: float) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_layernorm_f32(self.handle, x.handle, gamma.handle, beta.handle, rows,
+                                    cols, eps, C.byref(out)))
+        return Tensor(self, out)
+
+    def layernorm_into_f32(self, x: Tensor, gamma: Tensor, beta: Tensor, rows: int,
+                           cols: int, eps: float, out: Tensor) -> None:
+        _check(lib.vk_layernorm_into_f32(self.handle, x.handle, gamma.handle, beta.handle,
+                                         rows, cols, eps, out.handle))
+
+    def gelu_f32_in_place(self, x: Tensor) -> None:
+        _check(lib.vk_gelu_f32_inplace(self.handle, x.handle))
+
+    def gelu_erf_f32_in_place(self, x: Tensor) -> None:
+        _check(lib.vk_gelu_erf_f32_inplace(self.handle, x.handle))
+
+    def add_f32_in_place(self, dst: Tensor, src: Tensor) -> None:
+        _check(lib.vk_add_f32_inplace(self.handle, dst.handle, src.handle))
+
+    def layerscale_f32_in_place(self, x: Tensor, gamma: Tensor, rows: int, cols: int) -> None:
+        _check(lib.vk_layerscale_f32_inplace(self.handle, x.handle, gamma.handle, rows, cols))
+
+    def layerscale_residual_f32(self, x: Tensor, y: Tensor, gamma: Optional[Tensor],
+                                rows: int, cols: int) -> None:
+        _check(lib.vk_layerscale_residual_f32(self.handle, x.handle, y.handle, _h(gamma),
+                                              rows, cols))
+
+    def layerscale_residual_layernorm_f32(self, x: Tensor, y: Tensor,
+                                          ls_gamma: Optional[Tensor], ln_gamma: Tensor,
+                                          ln_beta: Tensor, rows: int, cols: int, eps: float,
+                                          ln_out: Tensor) -> None:
+        _check(lib.vk_layerscale_residual_layernorm_f32(
+            self.handle, x.handle, y.handle, _h(ls_gamma), ln_gamma.handle, ln_beta.handle,
+            rows, cols, eps, ln_out.handle))
+
+    def qk_norm_rope_f32_da3_base(self, q: Tensor, k: Tensor, q_gamma: Optional[Tensor],
+                                  q_beta: Optional[Tensor], k_gamma: Optional[Tensor],
+                                  k_beta: Optional[Tensor], positions: Tensor, heads: int,
+                                  rows: int, freq: float = 100.0,
+                                  eps: float = QK_NORM_EPS) -> None:
+        _check(lib.vk_qk_norm_rope_f32(self.handle, q.handle, k.handle, _h(q_gamma),
+                                       _h(q_beta), _h(k_gamma), _h(k_beta), positions.handle,
+                                       heads, rows, freq, eps))
+
+    def qk_norm_rope_grid_f32(self, q: Tensor, k: Tensor, q_gamma: Optional[Tensor],
+                              q_beta: Optional[Tensor], k_gamma: Optional[Tensor],
+                              k_beta: Optional[Tensor], heads: int, head_dim: int,
+                              n_special: int, gh: int, gw: int, view_count: int,
+                              global_layer: bool, layout: int, freq: float = 100.0,
+                              eps: float = QK_NORM_EPS) -> None:
+        _check(lib.vk_qk_norm_rope_grid_f32(
+            self.handle, q.handle, k.handle, _h(q_gamma), _h(q_beta), _h(k_gamma), _h(k_beta),
+            heads, head_dim, n_special, gh, gw, view_count, 1 if global_layer else 0, layout,
+            freq, eps))
+
+    def rope_positions_f32(self, n_special: int, gh: int, gw: int, view_count: int,
+                           global_layer: bool) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_rope_positions_f32(self.handle, n_special, gh, gw, view_count,
+                                         1 if global_layer else 0, C.byref(out)))
+        return Tensor(self, out)
+
+    # -- patch embedding -----------------------------------------------------
+    def patchify_nchw_f32(self, img: Tensor, h: int, w: int, patch: int,
+                          channels: int) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_patchify_nchw_f32(self.handle, img.handle, h, w, patch, channels,
+                                        C.byref(out)))
+        return Tensor(self, out)
+
+    def prepare_linear_f32(self, in_features: int, out_features: int, weight: np.ndarray,
+                           bias: np.ndarray, ls_gamma: Optional[np.ndarray] = None) -> Linear:
+        w = np.ascontiguousarray(weight, dtype=np.float32).reshape(-1)
+        b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        g = None if ls_gamma is None else np.ascontiguousarray(ls_gamma, dtype=np.float32)
+        out = C.c_void_p()
+        _check(lib.vk_linear_prepare_f32(self.handle, in_features, out_features, _ptr(w),
+                                         _ptr(b), None if g is None else _ptr(g),
+                                         C.byref(out)))
+        return Linear(self, out)
+
+    def prepare_linear_oihw_f32(self, in_features: int, out_features: int,
+                                weight_oihw: np.ndarray, bias: np.ndarray) -> Linear:
+        w = np.ascontiguousarray(weight_oihw, dtype=np.float32).reshape(-1)
+        b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        out = C.c_void_p()
+        _check(lib.vk_linear_prepare_oihw_f32(self.handle, in_features, out_features, _ptr(w),
+                                              _ptr(b), C.byref(out)))
+        return Linear(self, out)
+
+    def prepend_cls_add_pos_f32(self, patches: Tensor, cls: Tensor, pos: Tensor,
+                                n_patches: int, embed: int) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_prepend_cls_add_pos_f32(self.handle, patches.handle, cls.handle,
+                                              pos.handle, n_patches, embed, C.byref(out)))
+        return Tensor(self, out)
+
+    def pos_embed_bicubic_f32(self, pos_embed: Tensor, grid: int, embed: int, gh: int,
+                              gw: int, interp_offset: float = 0.1) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_pos_embed_bicubic_f32(self.handle, pos_embed.handle, grid, embed, gh, gw,
+                                            interp_offset, C.byref(out)))
+        return Tensor(self, out)
+
+    def patch_embed_u8(self, img_hwc: Tensor, h: int, w: int, patch: int,
+                       mean: Sequence[float], std: Sequence[float], proj: Linear, cls: Tensor,
+                       registers: Optional[Tensor], n_register: int, pos_table: Tensor,
+                       out: Tensor) -> None:
+        m = (C.c_float * 3)(*mean)
+        s = (C.c_float * 3)(*std)
+        _check(lib.vk_patch_embed_u8(self.handle, img_hwc.handle, h, w, patch,
+                                     C.cast(m, C.c_void_p), C.cast(s, C.c_void_p),
+                                     proj.handle, cls.handle, _h(registers), n_register,
+                                     pos_table.handle, out.handle))
+
+    # -- block sequence ------------------------------------------------------
+    def vit_block_fused_ops(self, cfg: VitConfig, layer_idx: int, layer: VitLayer,
+                            next_layer: Optional[VitLayer], act: VitActivations, gh: int,
+                            gw: int, view_count: int, camera: Optional[Tensor],
+                            flags: int = 0) -> None:
+        _check(lib.vk_vit_block_fused_ops(
+            self.handle, C.byref(cfg), layer_idx, C.byref(layer),
+            None if next_layer is None else C.byref(next_layer), C.byref(act), gh, gw,
+            view_count, _h(camera), flags))
+
+    # -- timing / graphs -----------------------------------------------------
+    def event(self) -> Event:
+        return Event(self)
+
+    def begin_capture(self) -> None:
+        _check(lib.vk_graph_begin_capture(self.handle))
+
+    def end_capture(self) -> Graph:
+        out = C.c_void_p()
+        _check(lib.vk_graph_end_capture(self.handle, C.byref(out)))
+        return Graph(self, out)
+
+
+def layer_struct(**tensors: Optional[Tensor]) -> VitLayer:
+    """Builds a VitLayer from named tensors (missing names are NULL)."""
+    lay = VitLayer()
+    for name, _ in VitLayer._fields_:
+        t = tensors.get(name)
+        setattr(lay, name, None if t is None else t.handle.value)
+    return lay
+
+
+def activations_struct(**tensors: Tensor) -> VitActivations:
+    act = VitActivations()
+    for name, _ in VitActivations._fields_:
+        t = tensors.get(name)
+        setattr(act, name, None if t is None else t.handle.value)
+    return act
