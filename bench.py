@@ -147,7 +147,28 @@ def time_loop(rt, fn, iters):
     return e0.elapsed_ms(e1) / iters
 
 
-def per_op_table(rt, rng, rows, rotate, iters):
+def capture(rt, fn, count=1):
+    """HIP graph of `count` calls of fn: replays carry no host launch cost."""
+    import gc
+    rt.synchronize()
+    gc.collect()
+    gc.disable()  # no tensor may be freed (a stream sync) while the stream captures
+    try:
+        rt.begin_capture()
+        for _ in range(count):
+            fn()
+        graph = rt.end_capture()
+    finally:
+        gc.enable()
+    return graph
+
+
+ROTATE_SETS = 8  # 8 x 288 MB at the 12-view shape: every operation's working set
+                 # (>= 512 MB) exceeds the 256 MB Infinity Cache
+OP_TRIALS = 5
+
+
+def per_op_table(rt, rng, rows, rotate, iters, only=None):
     """Average launch time of each fused operation, measured with HIP events
     on the runtime's stream.  `rotate` buffer sets cycle so that the working
     set exceeds the 256 MB Infinity Cache at the 12-view shape."""
@@ -156,11 +177,13 @@ def per_op_table(rt, rng, rows, rotate, iters):
     def n(*s):
         return rng.standard_normal(s).astype(np.float32)
 
+    host = {"x": n(rows, D), "y": n(rows, D), "q": n(rows * D), "k": n(rows * D),
+            "h": n(rows, M)}
     sets = []
     for _ in range(rotate):
-        sets.append({"x": rt.upload_f32(n(rows, D)), "y": rt.upload_f32(n(rows, D)),
-                     "o": rt.alloc_f32(rows * D), "q": rt.upload_f32(n(rows * D)),
-                     "k": rt.upload_f32(n(rows * D)), "h": rt.upload_f32(n(rows, M))})
+        s = {k: rt.upload_f32(v) for k, v in host.items()}
+        s["o"] = rt.alloc_f32(rows * D)
+        sets.append(s)
     g = rt.upload_f32((1 + 0.02 * rng.standard_normal(D)).astype(np.float32))
     b = rt.upload_f32((0.02 * rng.standard_normal(D)).astype(np.float32))
     ls = rt.upload_f32(rng.uniform(0, 0.1, D).astype(np.float32))
@@ -190,9 +213,15 @@ def per_op_table(rt, rng, rows, rotate, iters):
     }
     table = {}
     for name, (fn, nbytes) in ops.items():
+        if only and name != only:
+            continue
         for _ in range(3):
             fn()
-        us = time_loop(rt, fn, iters) * 1e3
+        graph = capture(rt, fn, iters)
+        graph.launch()
+        # median of several replays: single replays vary by several percent
+        us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / iters
+                               for _ in range(OP_TRIALS))
         gbs = nbytes / (us * 1e-6) / 1e9
         table[name] = {"us": round(us, 3), "bytes": int(nbytes), "GB_s": round(gbs, 1),
                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
@@ -234,7 +263,7 @@ def cpu_baseline(model, seconds, threads):
     one_block()  # warm-up
     times = []
     t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 1000):
         t0 = time.perf_counter()
         one_block()
         times.append(time.perf_counter() - t0)
@@ -257,6 +286,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--op", choices=["gelu", "layernorm", "qk_norm_rope", "layerscale_residual",
+                                     "layerscale_residual_layernorm"],
+                    help="profile mode: launch only this operation (12-view shape, rotating "
+                         "buffers) after one calibration device copy of 256 MiB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the fused per-token path runs on a single "
@@ -266,15 +299,29 @@ def main():
     import vestra_hip as vh
     rng = np.random.default_rng(SEED)
     rt = vh.Runtime(0)
+    if args.op:
+        # calibration: a plain device copy of known size, for scaling the
+        # FETCH_SIZE / WRITE_SIZE counters of the profiled kernel
+        cal = rt.alloc_f32(64 << 20)
+        cal_dst = rt.alloc_f32(64 << 20)
+        rt.copy_segment_into_f32(cal_dst, 0, cal, 0, 64 << 20)
+        rt.synchronize()
+        table = per_op_table(rt, rng, TPV * 12, rotate=ROTATE_SETS, iters=args.op_iters,
+                             only=args.op)
+        print(json.dumps({"op": args.op, "calibration_copy_bytes": 2 * (256 << 20),
+                          **table[args.op]}), flush=True)
+        return
     log(f"device has {rt.cu_count()} CUs; building 12-view workload ({TPV * 12} rows)")
     model = Model(rt, rng, views=12)
     nbytes = step_bytes(model.rows, 12, model.plan)
 
+    model.enqueue_step()  # builds the RoPE table before capture
+    step_graph = capture(rt, model.enqueue_step)
     for _ in range(args.warmup):
-        model.enqueue_step()
+        step_graph.launch()
     rt.synchronize()
     log(f"timing {args.steps} steps")
-    ms_per_step = time_loop(rt, model.enqueue_step, args.steps)
+    ms_per_step = time_loop(rt, step_graph.launch, args.steps)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     log(f"{ms_per_step:.3f} ms/step, {value:.1f} GB/s")
 
@@ -282,14 +329,7 @@ def main():
     single = Model(rt, rng, views=1)
     for _ in range(2):
         single.enqueue_step()
-    rt.synchronize()
-    import gc
-    gc.collect()
-    gc.disable()  # no tensor may be freed (a stream sync) while the stream captures
-    rt.begin_capture()
-    single.enqueue_step()
-    graph = rt.end_capture()
-    gc.enable()
+    graph = capture(rt, single.enqueue_step)
     graph.launch()
     rt.synchronize()
     reps = max(20, args.steps * 5)
@@ -299,7 +339,7 @@ def main():
     del single, graph
 
     log("per-operation table")
-    ops12 = per_op_table(rt, rng, model.rows, rotate=3, iters=args.op_iters)
+    ops12 = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters)
     ops1 = per_op_table(rt, rng, TPV, rotate=1, iters=args.op_iters)
     gelu = ops12["gelu"]
 

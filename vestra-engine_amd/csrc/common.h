@@ -21,8 +21,9 @@ struct vk_runtime {
   hipStream_t stream = nullptr;
   int cu_count = 0;
   // cos/sin tables of the 2D rotary embedding, keyed by (frequency bits,
-  // head_dim); device pointers owned by the runtime.
-  std::map<std::pair<uint32_t, int>, float*> rope_tables;
+  // head_dim): device pointer (owned by the runtime) and the largest
+  // position the table covers.
+  std::map<std::pair<uint32_t, int>, std::pair<float*, int>> rope_tables;
 };
 
 struct vk_tensor {
@@ -66,8 +67,12 @@ size_t dtype_size(vk_dtype d);
 int bind(vk_runtime* rt);
 // Launch check: turns a failed launch into a status.
 int check_launch(const char* what);
-// Device cos/sin table for the 2D RoPE (see rope_table_layout below).
-int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out);
+// Device cos/sin table for the 2D RoPE (layout below) covering at least
+// positions 0..max(min_max_pos, kRopeTableMax); *table_max receives the
+// largest covered position.  Grows (re-allocates) when a larger grid needs
+// it, so call it before any stream capture that uses the table.
+int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
+               int* table_max);
 
 }  // namespace vk
 
@@ -95,7 +100,8 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out);
 
 // ---------------------------------------------------------------------------
 // RoPE table layout (device, f32):
-//   [0, kRopeTableMax]          positions covered by the table
+//   [0, table_max]              positions covered by the table
+//                               (table_max >= kRopeTableMax)
 //   entry p: 32 floats: cos(p*inv_freq_j) j<16, then sin(p*inv_freq_j) j<16
 //   after the last entry: inv_freq_j, j<16 (for positions outside the table)
 // ---------------------------------------------------------------------------
@@ -131,6 +137,54 @@ __device__ __forceinline__ float wave_sum(float v) {
   v = v + __shfl_xor(v, 16, 64);
   v = v + __shfl_xor(v, 32, 64);
   return v;
+}
+
+// Unsigned 32-bit division by a runtime-invariant divisor as a multiply-high
+// and two shifts (Granlund & Montgomery, "Division by invariant integers
+// using multiplication", PLDI 1994, fig. 4.1), exact for every n < 2^32.
+// The divisor data is built on the host and passed to kernels by value.
+struct FastDivU32 {
+  uint32_t d;
+  uint32_t m;
+  uint32_t s1;
+  uint32_t s2;
+};
+
+__host__ __device__ inline FastDivU32 make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;  // l = ceil(log2 d)
+  const unsigned long long m =
+      ((1ull << 32) * ((1ull << l) - d)) / d + 1;  // 2^l - d < 2^31: no overflow
+  FastDivU32 f;
+  f.d = d;
+  f.m = static_cast<uint32_t>(m);
+  f.s1 = l ? 1u : 0u;
+  f.s2 = l ? l - 1 : 0u;
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDivU32& f) {
+  const uint32_t t = __umulhi(f.m, n);
+  return (t + ((n - t) >> f.s1)) >> f.s2;
+}
+
+__device__ __forceinline__ uint32_t fmod_(uint32_t n, const FastDivU32& f) {
+  return n - fdiv(n, f) * f.d;
+}
+
+// Streaming (nontemporal) 128-bit loads and stores for activations that are
+// touched once per kernel: they keep the stream from displacing reusable
+// lines in L2 and the Infinity Cache.  Parameter vectors use ordinary loads.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+  const f32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+  return make_float4(t.x, t.y, t.z, t.w);
+}
+
+__device__ __forceinline__ void st_stream(float4* p, float4 v) {
+  const f32x4_t t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, reinterpret_cast<f32x4_t*>(p));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {

@@ -3,16 +3,19 @@
 // RoPE.
 //
 // Mapping to CDNA4:
-//  * LayerNorm rows (D = 768 / 1024): one wave64 per row, each lane holds
-//    D/256 float4 in registers (128-bit coalesced loads: a wave reads one
-//    contiguous KiB per instruction), mean and variance reduced with DPP row
-//    reductions plus two cross-row swizzles; the row is read from HBM once
-//    and written once.  Four rows per 256-thread workgroup.
+//  * LayerNorm rows (D = 768 / 1024): one wave64 workgroup per row, each lane
+//    holds D/256 float4 in registers (128-bit coalesced loads: a wave reads
+//    one contiguous KiB per instruction), mean and variance reduced with DPP
+//    row reductions plus two cross-row swizzles; the row is read from HBM
+//    once and written once, both with nontemporal (streaming) hints.
+//    Single-wave workgroups measured fastest on MI355X (65.6% of peak at
+//    10392x768 vs 57.8% for four rows per 256-thread workgroup).
 //  * Q/K rows (head_dim 64): 16 lanes per (head, token) row, one float4 per
 //    lane, so a row's LayerNorm reduces inside one DPP row (4 DPP steps) and
 //    the RoPE partner element (i <-> i+16 inside each 32-wide half) sits
 //    exactly 4 lanes away: one swizzle, no LDS round trip.  Q and K rows are
-//    covered by one launch.
+//    covered by one launch; each 16-lane group streams two rows (both loads
+//    in flight before the first reduction).
 //  * Arithmetic per element follows the scalar reference order with every
 //    product and sum rounded (built with -ffp-contract=off); only the order
 //    of the mean/variance reductions differs (wave tree vs sequential).
@@ -24,16 +27,18 @@ using vkd::Param;
 
 // ---------------------------------------------------------------------------
 // LayerNorm over rows of `cols` floats, one wave per row.
-// NV = float4 per lane (cols <= 256 * NV).  x and y may alias.
+// NV = float4 per lane (cols <= 256 * NV).  EXACT: cols == 256 * NV, so no
+// lane is ever out of the row and every load is issued unguarded (a guarded
+// load makes the compiler wait for each one in turn).  x and y may alias.
 // ---------------------------------------------------------------------------
-template <int NV, typename PT>
-__global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
-                                                      const PT* __restrict__ gamma,
-                                                      const PT* __restrict__ beta,
-                                                      int rows, int cols, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;  // whole wave leaves together
+template <int NV, typename PT, bool EXACT>
+__global__ __launch_bounds__(64) void layernorm_rows(const float* x, float* y,
+                                                     const PT* __restrict__ gamma,
+                                                     const PT* __restrict__ beta,
+                                                     int rows, int cols, float eps) {
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;
+  if (row >= rows) return;
   const int nvec = cols >> 2;
   const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
   float4 v[NV];
@@ -41,8 +46,8 @@ __global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (c < nvec) {
-      v[i] = xr[c];
+    if (EXACT || c < nvec) {
+      v[i] = vkd::ld_stream(xr + c);
       s += v[i].x;
       s += v[i].y;
       s += v[i].z;
@@ -57,7 +62,7 @@ __global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (c < nvec) {
+    if (EXACT || c < nvec) {
       float d;
       d = v[i].x - mean; q += d * d;
       d = v[i].y - mean; q += d * d;
@@ -72,7 +77,7 @@ __global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (c < nvec) {
+    if (EXACT || c < nvec) {
       const float4 g = Param<PT>::load4(gamma, c);
       const float4 b = Param<PT>::load4(beta, c);
       float4 o;
@@ -80,7 +85,7 @@ __global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
       o.y = (v[i].y - mean) * inv * g.y + b.y;
       o.z = (v[i].z - mean) * inv * g.z + b.z;
       o.w = (v[i].w - mean) * inv * g.w + b.w;
-      yr[c] = o;
+      vkd::st_stream(yr + c, o);
     }
   }
 }
@@ -89,13 +94,13 @@ __global__ __launch_bounds__(256) void layernorm_rows(const float* x, float* y,
 // x += ls (.) yb (t = yb*ls rounded, x = x + t rounded); ln_out = LN(x).
 // HAS_LS false: unscaled residual add.  One wave per row.
 // ---------------------------------------------------------------------------
-template <int NV, typename PT, bool HAS_LS>
-__global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
+template <int NV, typename PT, bool HAS_LS, bool EXACT>
+__global__ __launch_bounds__(64) void ls_residual_layernorm_rows(
     float* __restrict__ x, const float* __restrict__ yb, const PT* __restrict__ ls,
     const PT* __restrict__ gamma, const PT* __restrict__ beta,
     float* __restrict__ ln_out, int rows, int cols, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;
   if (row >= rows) return;
   const int nvec = cols >> 2;
   const size_t base = static_cast<size_t>(row) * cols;
@@ -106,9 +111,9 @@ __global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (c < nvec) {
-      float4 a = xr[c];
-      const float4 b = yr[c];
+    if (EXACT || c < nvec) {
+      float4 a = vkd::ld_stream(xr + c);
+      const float4 b = vkd::ld_stream(yr + c);
       if (HAS_LS) {
         const float4 g = Param<PT>::load4(ls, c);
         float t;
@@ -122,7 +127,7 @@ __global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
         a.z = a.z + b.z;
         a.w = a.w + b.w;
       }
-      xr[c] = a;
+      vkd::st_stream(xr + c, a);
       v[i] = a;
       s += a.x;
       s += a.y;
@@ -138,7 +143,7 @@ __global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (c < nvec) {
+    if (EXACT || c < nvec) {
       float d;
       d = v[i].x - mean; q += d * d;
       d = v[i].y - mean; q += d * d;
@@ -153,7 +158,7 @@ __global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (c < nvec) {
+    if (EXACT || c < nvec) {
       const float4 g = Param<PT>::load4(gamma, c);
       const float4 b = Param<PT>::load4(beta, c);
       float4 o;
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
       o.y = (v[i].y - mean) * inv * g.y + b.y;
       o.z = (v[i].z - mean) * inv * g.z + b.z;
       o.w = (v[i].w - mean) * inv * g.w + b.w;
-      outr[c] = o;
+      vkd::st_stream(outr + c, o);
     }
   }
 }
@@ -172,24 +177,33 @@ __global__ __launch_bounds__(256) void ls_residual_layernorm_rows(
 enum PosMode { kPosExplicit = 0, kPosGrid = 1 };
 
 struct QkShape {
-  long long rows_per_tensor;  // heads * total tokens
-  int heads;
-  int tokens_per_view;        // reference form: == total tokens
-  int view_count;
-  int n_special;
-  int gw;
-  int global;
-  int layout;                 // vk_qk_layout
+  uint32_t rows_per_tensor;  // heads * total tokens; 2 * rows_per_tensor < 2^31
+  int table_max;             // largest position the cos/sin table covers
+  uint32_t n_special;
+  uint32_t global;
+  uint32_t layout;           // vk_qk_layout
+  vkd::FastDivU32 ntok;      // total tokens (view_count * tokens_per_view)
+  vkd::FastDivU32 tpv;       // tokens per view
+  vkd::FastDivU32 per_view;  // heads * tokens per view
+  vkd::FastDivU32 gw;        // patch grid width
 };
 
-// cos/sin for a coordinate outside the table: angle rounded in f32, trig in
-// double, as the host table does.
-__device__ __forceinline__ void rope_cs_slow(const float* __restrict__ table, int p, int j,
-                                             float* c, float* s) {
-  const float inv_freq = table[(vk::kRopeTableMax + 1) * 32 + j];
-  const float angle = static_cast<float>(p) * inv_freq;
-  *c = static_cast<float>(cos(static_cast<double>(angle)));
-  *s = static_cast<float>(sin(static_cast<double>(angle)));
+// cos/sin of the four frequencies j0..j0+3 for a coordinate outside the
+// table: angle rounded in f32, trig in double, as the host table does.  Only
+// the explicit-position form can meet such a coordinate (grid forms size the
+// table on the host); kept out of line so its double-precision trig does not
+// inflate the register footprint of the streaming path.
+__device__ __noinline__ void rope_cs_slow4(const float* __restrict__ table, int table_max,
+                                           int p, int j0, float4* c, float4* s) {
+  float cv[4], sv[4];
+  for (int u = 0; u < 4; ++u) {
+    const float inv_freq = table[static_cast<size_t>(table_max + 1) * 32 + j0 + u];
+    const float angle = static_cast<float>(p) * inv_freq;
+    cv[u] = static_cast<float>(cos(static_cast<double>(angle)));
+    sv[u] = static_cast<float>(sin(static_cast<double>(angle)));
+  }
+  *c = make_float4(cv[0], cv[1], cv[2], cv[3]);
+  *s = make_float4(sv[0], sv[1], sv[2], sv[3]);
 }
 
 __device__ __forceinline__ float4 swizzle_xor4(float4 v) {
@@ -203,51 +217,48 @@ __device__ __forceinline__ float4 swizzle_xor4(float4 v) {
   return r;
 }
 
-template <typename PT, bool HAS_NORM, int POS>
-__global__ __launch_bounds__(256) void qk_norm_rope_rows(
-    float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
-    const PT* __restrict__ qb, const PT* __restrict__ kg, const PT* __restrict__ kb,
-    const float* __restrict__ pos_yx, const float* __restrict__ table, QkShape sh,
-    float eps) {
-  const int l = threadIdx.x & 15;
-  const long long gr = static_cast<long long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
-  const bool valid = gr < 2 * sh.rows_per_tensor;
-  const bool is_k = gr >= sh.rows_per_tensor;
-  const long long r = is_k ? gr - sh.rows_per_tensor : gr;
-
-  // token (sequence index) of this row
-  int py = 0, px = 0;
-  if (valid) {
-    long long t;       // index in the position sequence
-    int lt;            // index inside its view
-    if (sh.layout == VK_QK_HEADS_OUTER) {
-      const long long ntok = static_cast<long long>(sh.tokens_per_view) * sh.view_count;
-      t = r % ntok;
-      lt = static_cast<int>(t % sh.tokens_per_view);
+// Position (y, x) of Q/K row r (head-major index inside one tensor).  All
+// index math is 32-bit with multiply-shift division by the shape constants.
+template <int POS>
+__device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
+                                                const float* __restrict__ pos_yx, int* py,
+                                                int* px) {
+  uint32_t t;   // index in the position sequence
+  uint32_t lt;  // index inside its view
+  if (sh.layout == VK_QK_HEADS_OUTER) {
+    t = vkd::fmod_(r, sh.ntok);
+    lt = vkd::fmod_(t, sh.tpv);
+  } else {
+    const uint32_t v = vkd::fdiv(r, sh.per_view);
+    lt = vkd::fmod_(r, sh.tpv);
+    t = v * sh.tpv.d + lt;
+  }
+  *py = 0;
+  *px = 0;
+  if (POS == kPosExplicit) {
+    // the reference's f32 device encoding, truncated like `value as i64`
+    *py = static_cast<int>(pos_yx[2 * static_cast<size_t>(t)]);
+    *px = static_cast<int>(pos_yx[2 * static_cast<size_t>(t) + 1]);
+  } else if (lt >= sh.n_special) {
+    if (sh.global) {
+      *py = 1;
+      *px = 1;
     } else {
-      const long long per_view = static_cast<long long>(sh.heads) * sh.tokens_per_view;
-      const long long v = r / per_view;
-      lt = static_cast<int>(r % sh.tokens_per_view);
-      t = v * sh.tokens_per_view + lt;
-    }
-    if (POS == kPosExplicit) {
-      py = static_cast<int>(pos_yx[2 * t]);
-      px = static_cast<int>(pos_yx[2 * t + 1]);
-    } else if (lt >= sh.n_special) {
-      if (sh.global) {
-        py = 1;
-        px = 1;
-      } else {
-        const int p = lt - sh.n_special;
-        py = p / sh.gw + 1;
-        px = p % sh.gw + 1;
-      }
+      const uint32_t p = lt - sh.n_special;
+      const uint32_t row = vkd::fdiv(p, sh.gw);
+      *py = static_cast<int>(row) + 1;
+      *px = static_cast<int>(p - row * sh.gw.d) + 1;
     }
   }
+}
 
-  float4* row = reinterpret_cast<float4*>((is_k ? k : q) + r * 64);
-  float4 v = valid ? row[l] : make_float4(0.f, 0.f, 0.f, 0.f);
-
+// LayerNorm of one 64-wide row held as one float4 per lane of a 16-lane DPP
+// row, then its 2D rotation.
+template <typename PT, bool HAS_NORM, int POS>
+__device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
+                                                   const PT* __restrict__ b, int py, int px,
+                                                   const float* __restrict__ table,
+                                                   int table_max, float eps) {
   if (HAS_NORM) {
     float s = v.x;
     s += v.y;
@@ -263,8 +274,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_rows(
     sq = vkd::row16_sum(sq);
     const float var = sq / 64.0f;
     const float inv = 1.0f / sqrtf(var + eps);
-    const PT* g = is_k ? kg : qg;
-    const PT* b = is_k ? kb : qb;
     const float4 gv = Param<PT>::load4(g, l);
     const float4 bv = Param<PT>::load4(b, l);
     v.x = (v.x - mean) * inv * gv.x + bv.x;
@@ -272,22 +281,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_rows(
     v.z = (v.z - mean) * inv * gv.z + bv.z;
     v.w = (v.w - mean) * inv * gv.w + bv.w;
   }
-
   // RoPE.  Lanes 0-7 hold the y half (elements 0..31), lanes 8-15 the x half.
   // Inside a half, lanes with bit 2 clear hold elements j (j < 16) and rotate
   // against the lane 4 above, which holds element j + 16.
   const int coord = (l < 8) ? py : px;
   const int j0 = (l & 3) * 4;
   float4 c, s;
-  if (coord >= 0 && coord <= vk::kRopeTableMax) {
+  if (POS == kPosGrid || (coord >= 0 && coord <= table_max)) {
     const float* e = table + static_cast<size_t>(coord) * 32;
     c = *reinterpret_cast<const float4*>(e + j0);
     s = *reinterpret_cast<const float4*>(e + 16 + j0);
   } else {
-    rope_cs_slow(table, coord, j0 + 0, &c.x, &s.x);
-    rope_cs_slow(table, coord, j0 + 1, &c.y, &s.y);
-    rope_cs_slow(table, coord, j0 + 2, &c.z, &s.z);
-    rope_cs_slow(table, coord, j0 + 3, &c.w, &s.w);
+    rope_cs_slow4(table, table_max, coord, j0, &c, &s);
   }
   const float4 p = swizzle_xor4(v);
   float4 o;
@@ -304,7 +309,47 @@ __global__ __launch_bounds__(256) void qk_norm_rope_rows(
     o.z = v.z * c.z + p.z * s.z;
     o.w = v.w * c.w + p.w * s.w;
   }
-  if (valid) row[l] = o;
+  return o;
+}
+
+// Each 16-lane group owns kQkRowsPerGroup consecutive rows of the flattened
+// [Q rows | K rows] index space; both rows' loads are issued before either
+// row's reductions, doubling the bytes in flight per wave.
+constexpr int kQkRowsPerGroup = 2;
+
+template <typename PT, bool HAS_NORM, int POS>
+__global__ __launch_bounds__(256) void qk_norm_rope_rows(
+    float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
+    const PT* __restrict__ qb, const PT* __restrict__ kg, const PT* __restrict__ kb,
+    const float* __restrict__ pos_yx, const float* __restrict__ table, QkShape sh,
+    float eps) {
+  const int l = threadIdx.x & 15;
+  const uint32_t grp = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const uint32_t total = 2u * sh.rows_per_tensor;
+  float4 v[kQkRowsPerGroup];
+  int py[kQkRowsPerGroup], px[kQkRowsPerGroup];
+#pragma unroll
+  for (int j = 0; j < kQkRowsPerGroup; ++j) {
+    const uint32_t gr = grp * kQkRowsPerGroup + j;
+    // rows past the end read the last row (always valid) and are not stored
+    const uint32_t gc = gr < total ? gr : total - 1;
+    const bool is_k = gc >= sh.rows_per_tensor;
+    const uint32_t r = is_k ? gc - sh.rows_per_tensor : gc;
+    qk_row_position<POS>(r, sh, pos_yx, &py[j], &px[j]);
+    v[j] = vkd::ld_stream(reinterpret_cast<const float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l);
+  }
+#pragma unroll
+  for (int j = 0; j < kQkRowsPerGroup; ++j) {
+    const uint32_t gr = grp * kQkRowsPerGroup + j;
+    const bool is_k = gr >= sh.rows_per_tensor;
+    const float4 o = qk_row_transform<PT, HAS_NORM, POS>(v[j], l, is_k ? kg : qg,
+                                                         is_k ? kb : qb, py[j], px[j], table,
+                                                         sh.table_max, eps);
+    if (gr < total) {
+      const uint32_t r = is_k ? gr - sh.rows_per_tensor : gr;
+      vkd::st_stream(reinterpret_cast<float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l, o);
+    }
+  }
 }
 
 // positions tensor [rows*2] as the reference's host builder produces it
@@ -350,11 +395,16 @@ template <typename PT>
 int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
                      const void* b, int rows, int cols, float eps) {
   const int nv = ln_instance_cols(cols);
-  dim3 grid((rows + 3) / 4), block(256);
+  dim3 grid(rows), block(64);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
-#define VK_LN_CASE(N) \
-  case N: hipLaunchKernelGGL((layernorm_rows<N, PT>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); break;
+#define VK_LN_CASE(N)                                                                          \
+  case N:                                                                                      \
+    if (cols == N * 256)                                                                       \
+      hipLaunchKernelGGL((layernorm_rows<N, PT, true>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
+    else                                                                                       \
+      hipLaunchKernelGGL((layernorm_rows<N, PT, false>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
+    break;
   switch (nv) {
     VK_LN_CASE(1) VK_LN_CASE(2) VK_LN_CASE(3) VK_LN_CASE(4)
     VK_LN_CASE(5) VK_LN_CASE(6) VK_LN_CASE(7) VK_LN_CASE(8)
@@ -371,12 +421,17 @@ int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
                      const void* g, const void* b, float* out, int rows, int cols,
                      float eps) {
   const int nv = ln_instance_cols(cols);
-  dim3 grid((rows + 3) / 4), block(256);
+  dim3 grid(rows), block(64);
   auto LS = static_cast<const PT*>(ls);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
-#define VK_LSLN_CASE(N) \
-  case N: hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps); break;
+#define VK_LSLN_CASE(N)                                                                        \
+  case N:                                                                                      \
+    if (cols == N * 256)                                                                       \
+      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps); \
+    else                                                                                       \
+      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, false>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps); \
+    break;
   switch (nv) {
     VK_LSLN_CASE(1) VK_LSLN_CASE(2) VK_LSLN_CASE(3) VK_LSLN_CASE(4)
     VK_LSLN_CASE(5) VK_LSLN_CASE(6) VK_LSLN_CASE(7) VK_LSLN_CASE(8)
@@ -392,8 +447,9 @@ template <typename PT, bool HAS_NORM, int POS>
 int launch_qk(vk_runtime* rt, float* q, float* k, const void* qg, const void* qb,
               const void* kg, const void* kb, const float* pos, const float* table,
               const QkShape& sh, float eps) {
-  const long long total = 2 * sh.rows_per_tensor;
-  const long long blocks = (total + 15) / 16;
+  const long long total = 2LL * sh.rows_per_tensor;
+  const long long groups = (total + kQkRowsPerGroup - 1) / kQkRowsPerGroup;
+  const long long blocks = (groups + 15) / 16;
   hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS>), dim3(static_cast<unsigned>(blocks)),
                      dim3(256), 0, rt->stream, q, k, static_cast<const PT*>(qg),
                      static_cast<const PT*>(qb), static_cast<const PT*>(kg),
@@ -525,19 +581,21 @@ int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_ten
              rows * 2, positions->len);
   VK_REQUIRE(q->ptr != k->ptr, "q and k must be distinct buffers");
   VK_TRY(check_qk_params(q_gamma, q_beta, k_gamma, k_beta, head_dim));
-  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "rows=%zu too large", rows);
+  VK_UNSUPPORTED_IF(2 * heads * rows > 0x7fffffffULL, "heads*rows=%zu too large", heads * rows);
   if (rows == 0) return VK_OK;
   const float* table = nullptr;
-  VK_TRY(vk::rope_table(rt, freq, 64, &table));
+  int table_max = 0;
+  VK_TRY(vk::rope_table(rt, freq, 64, 0, &table, &table_max));
   QkShape sh;
-  sh.rows_per_tensor = static_cast<long long>(heads * rows);
-  sh.heads = static_cast<int>(heads);
-  sh.tokens_per_view = static_cast<int>(rows);
-  sh.view_count = 1;
+  sh.rows_per_tensor = static_cast<uint32_t>(heads * rows);
+  sh.table_max = table_max;
   sh.n_special = 0;
-  sh.gw = 1;
   sh.global = 0;
   sh.layout = VK_QK_HEADS_OUTER;
+  sh.ntok = vkd::make_fastdiv(static_cast<uint32_t>(rows));
+  sh.tpv = sh.ntok;
+  sh.per_view = vkd::make_fastdiv(static_cast<uint32_t>(heads * rows));
+  sh.gw = vkd::make_fastdiv(1);
   return dispatch_qk<kPosExplicit>(rt, q, k, q_gamma, q_beta, k_gamma, k_beta,
                                    static_cast<const float*>(positions->ptr), table, sh, eps);
 }
@@ -562,19 +620,24 @@ int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
              heads * rows * head_dim, q->len, k->len);
   VK_REQUIRE(q->ptr != k->ptr, "q and k must be distinct buffers");
   VK_TRY(check_qk_params(q_gamma, q_beta, k_gamma, k_beta, head_dim));
-  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "rows=%zu too large", rows);
+  VK_UNSUPPORTED_IF(2 * heads * rows > 0x7fffffffULL, "heads*rows=%zu too large", heads * rows);
   if (rows == 0) return VK_OK;
+  // the grid's largest coordinate is max(gh, gw) + 1: size the table to it
   const float* table = nullptr;
-  VK_TRY(vk::rope_table(rt, freq, 64, &table));
+  int table_max = 0;
+  const size_t max_coord = (gh > gw ? gh : gw) + 1;
+  VK_UNSUPPORTED_IF(max_coord > (1u << 22), "patch grid %zux%zu too large", gh, gw);
+  VK_TRY(vk::rope_table(rt, freq, 64, static_cast<int>(max_coord), &table, &table_max));
   QkShape sh;
-  sh.rows_per_tensor = static_cast<long long>(heads * rows);
-  sh.heads = static_cast<int>(heads);
-  sh.tokens_per_view = static_cast<int>(tpv);
-  sh.view_count = static_cast<int>(view_count);
-  sh.n_special = static_cast<int>(n_special);
-  sh.gw = static_cast<int>(gw);
-  sh.global = global ? 1 : 0;
-  sh.layout = layout;
+  sh.rows_per_tensor = static_cast<uint32_t>(heads * rows);
+  sh.table_max = table_max;
+  sh.n_special = static_cast<uint32_t>(n_special);
+  sh.global = global ? 1u : 0u;
+  sh.layout = static_cast<uint32_t>(layout);
+  sh.ntok = vkd::make_fastdiv(static_cast<uint32_t>(rows));
+  sh.tpv = vkd::make_fastdiv(static_cast<uint32_t>(tpv));
+  sh.per_view = vkd::make_fastdiv(static_cast<uint32_t>(heads * tpv));
+  sh.gw = vkd::make_fastdiv(static_cast<uint32_t>(gw));
   return dispatch_qk<kPosGrid>(rt, q, k, q_gamma, q_beta, k_gamma, k_beta, nullptr, table, sh,
                                eps);
 }

@@ -60,17 +60,21 @@ int check_launch(const char* what) {
 // f32; angle = (f32)p * inv_freq_j as one f32 product; cos/sin evaluated in
 // double and rounded once (the published RotaryPositionEmbedding2D of
 // Depth-Anything-3 computes the same f32 angle).
-int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out) {
-  VK_UNSUPPORTED_IF(head_dim != 64, "RoPE table supports head_dim 64 (got %d)",
-                    head_dim);
+int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
+               int* table_max) {
+  VK_UNSUPPORTED_IF(head_dim != 64, "RoPE table supports head_dim 64 (got %d)", head_dim);
+  VK_UNSUPPORTED_IF(min_max_pos > (1 << 22), "RoPE positions up to %d exceed the table limit",
+                    min_max_pos);
   uint32_t fbits;
   std::memcpy(&fbits, &freq, sizeof fbits);
   auto key = std::make_pair(fbits, head_dim);
   auto it = rt->rope_tables.find(key);
-  if (it != rt->rope_tables.end()) {
-    *out = it->second;
+  if (it != rt->rope_tables.end() && it->second.second >= min_max_pos) {
+    *out = it->second.first;
+    *table_max = it->second.second;
     return VK_OK;
   }
+  const int max_pos = min_max_pos > kRopeTableMax ? min_max_pos : kRopeTableMax;
   const int half = head_dim / 2;
   const int quarter = half / 2;
   std::vector<float> inv_freq(quarter);
@@ -78,7 +82,7 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out) {
     const float e = static_cast<float>(2 * j) / static_cast<float>(half);
     inv_freq[j] = 1.0f / std::pow(freq, e);
   }
-  const size_t entries = static_cast<size_t>(kRopeTableMax) + 1;
+  const size_t entries = static_cast<size_t>(max_pos) + 1;
   std::vector<float> host(entries * 32 + 16, 0.0f);
   for (size_t p = 0; p < entries; ++p) {
     for (int j = 0; j < quarter; ++j) {
@@ -97,8 +101,14 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, const float** out) {
     (void)hipFree(dev);
     return hip_fail(e, "hipMemcpy(rope table)");
   }
-  rt->rope_tables[key] = dev;
+  if (it != rt->rope_tables.end()) {
+    // the smaller table may still be read by queued kernels
+    (void)hipStreamSynchronize(rt->stream);
+    (void)hipFree(it->second.first);
+  }
+  rt->rope_tables[key] = std::make_pair(dev, max_pos);
   *out = dev;
+  *table_max = max_pos;
   return VK_OK;
 }
 
@@ -174,7 +184,7 @@ int vk_runtime_destroy(vk_runtime* rt) {
   if (!rt) return VK_OK;
   VK_TRY(bind(rt));
   (void)hipStreamSynchronize(rt->stream);
-  for (auto& kv : rt->rope_tables) (void)hipFree(kv.second);
+  for (auto& kv : rt->rope_tables) (void)hipFree(kv.second.first);
   (void)hipStreamDestroy(rt->stream);
   delete rt;
   return VK_OK;
