@@ -210,6 +210,10 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
         "layerscale_residual_layernorm": (lambda: (lambda s: rt.layerscale_residual_layernorm_f32(
             s["x"], s["y"], ls, g, b, rows, D, 1e-6, s["o"]))(nxt()), lsres_ln_bytes(rows)),
         "gelu": (lambda: (lambda s: rt.gelu_f32_in_place(s["h"]))(nxt()), gelu_bytes(rows)),
+        # practical reference: the runtime's plain device copy of a [rows, D] tensor
+        "device_copy": (lambda: (lambda s: rt.copy_segment_into_f32(s["o"], 0, s["x"], 0,
+                                                                    rows * D))(nxt()),
+                        2 * rows * D * 4),
     }
     table = {}
     for name, (fn, nbytes) in ops.items():
@@ -226,6 +230,40 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
         table[name] = {"us": round(us, 3), "bytes": int(nbytes), "GB_s": round(gbs, 1),
                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     return table
+
+
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def patch_embed_timing(rt, rng, h, w, embed, iters):
+    """Fused patch embedding of one u8 image (normalise, unfold, F32-MFMA
+    projection, bias, position add, special rows): time per image and the
+    projection's FLOP rate against the F32 matrix peak."""
+    gh, gw = h // 14, w // 14
+    img = rt.upload_u8(rng.integers(0, 256, (h, w, 3), dtype=np.uint8))
+    wt = (0.02 * rng.standard_normal((embed, 3, 14, 14))).astype(np.float32)
+    bias = (0.02 * rng.standard_normal(embed)).astype(np.float32)
+    proj = rt.prepare_linear_oihw_f32(588, embed, wt, bias)
+    cls = rt.upload_f32((0.02 * rng.standard_normal(embed)).astype(np.float32))
+    regs = rt.upload_f32((0.02 * rng.standard_normal(embed)).astype(np.float32))
+    pos = rt.upload_f32((0.02 * rng.standard_normal((1 + gh * gw) * embed)).astype(np.float32))
+    out = rt.alloc_f32((2 + gh * gw) * embed)
+    mean, std = [0.485, 0.456, 0.406], [0.229, 0.224, 0.225]
+
+    def fn():
+        rt.patch_embed_u8(img, h, w, 14, mean, std, proj, cls, regs, 1, pos, out)
+
+    for _ in range(3):
+        fn()
+    graph = capture(rt, fn, iters)
+    graph.launch()
+    us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / iters
+                           for _ in range(OP_TRIALS))
+    flop = 2 * gh * gw * 588 * embed
+    tflops = flop / (us * 1e-6) / 1e12
+    return {"image": f"{h}x{w}", "patches": gh * gw, "embed": embed, "us": round(us, 3),
+            "flop": flop, "TFLOP_s": round(tflops, 2),
+            "frac_of_f32_mfma_peak": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)}
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -276,6 +314,21 @@ def cpu_baseline(model, seconds, threads):
                        f"(12 views x {TPV}); median of {len(times)} runs after 1 warm-up")}
 
 
+def measured_traffic(op, algorithmic_bytes):
+    """HBM bytes per launch of `op` from the committed PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy of known size), or
+    None when no summary for this shape is present."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["ops"][op]
+    except (OSError, KeyError, ValueError):
+        return None
+    if entry.get("algorithmic_bytes") != algorithmic_bytes:
+        return None
+    return entry["traffic_bytes"]
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -287,7 +340,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--op", choices=["gelu", "layernorm", "qk_norm_rope", "layerscale_residual",
-                                     "layerscale_residual_layernorm"],
+                                     "layerscale_residual_layernorm", "device_copy",
+                                     "patch_embed"],
                     help="profile mode: launch only this operation (12-view shape, rotating "
                          "buffers) after one calibration device copy of 256 MiB")
     args = ap.parse_args()
@@ -299,6 +353,10 @@ def main():
     import vestra_hip as vh
     rng = np.random.default_rng(SEED)
     rt = vh.Runtime(0)
+    if args.op == "patch_embed":
+        print(json.dumps({"op": "patch_embed",
+                          **patch_embed_timing(rt, rng, 336, 504, D, args.op_iters)}), flush=True)
+        return
     if args.op:
         # calibration: a plain device copy of known size, for scaling the
         # FETCH_SIZE / WRITE_SIZE counters of the profiled kernel
@@ -341,6 +399,9 @@ def main():
     log("per-operation table")
     ops12 = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters)
     ops1 = per_op_table(rt, rng, TPV, rotate=1, iters=args.op_iters)
+    log("patch embedding")
+    patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
+             patch_embed_timing(rt, rng, 672, 1008, 1024, args.op_iters)]
     gelu = ops12["gelu"]
 
     cpu = None
@@ -372,10 +433,12 @@ def main():
         "single_image_GB_s": round(single_bytes / (ms_single * 1e-3) / 1e9, 1),
         "ops_12view": ops12,
         "ops_single_image": ops1,
+        "patch_embed": patch,
         "roofline": {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
                      "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "algorithmic_bytes": gelu["bytes"], "avg_launch_us": gelu["us"],
+                     "traffic": measured_traffic("gelu", gelu["bytes"])},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
