@@ -13,11 +13,14 @@
 //
 // Tiling: a 256-thread workgroup (4 waves) owns a 48 (patches) x 64 (embed)
 // output tile; wave w owns 16 embed columns across all 48 rows (three 16x16
-// accumulators).  K is consumed in chunks of 28 = two 14-pixel rows of one
-// channel, staged in LDS as A^T[k][m] and B[k][n] with a row pitch of 80
-// floats, which makes both fragment reads bank-conflict free.  ViT-B at
-// 504x336: 864 x 768 outputs -> 18 x 12 = 216 workgroups, K = 588 -> 21
-// chunks.
+// accumulators).  K is consumed in chunks of 196 = one input channel of a
+// 14x14 patch (3 chunks per image), staged in LDS as A^T[k][m] and B[k][n]
+// with a row pitch of 80 floats, which makes both fragment reads bank-conflict
+// free.  While the MFMAs consume one chunk from LDS, the next chunk's global
+// loads are already in flight into registers, so each chunk's load latency is
+// hidden behind the previous chunk's 147 MFMAs.  The 125 KB of LDS allows one
+// workgroup per CU: ViT-B at 504x336 is 864 x 768 outputs -> 18 x 12 = 216
+// workgroups, one round on 256 CUs.
 #include <cstring>
 #include <vector>
 
@@ -29,12 +32,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 48;
 constexpr int BN = 64;
-constexpr int KC = 28;
+constexpr int KC = 196;
 constexpr int PA = 80;  // LDS pitch of A^T rows (BM + 32)
 constexpr int PB = 80;  // LDS pitch of B rows (BN + 16)
 constexpr int kPatch = 14;
-constexpr int kA_PER_THREAD = (KC * BM + 255) / 256;        // 6
-constexpr int kB_VEC_PER_THREAD = (KC * BN / 4 + 255) / 256;  // 2
+constexpr int kThreads = 256;
+constexpr int kA_PER_THREAD = (KC * BM + kThreads - 1) / kThreads;        // 37
+constexpr int kB_VEC_PER_THREAD = (KC * BN / 4 + kThreads - 1) / kThreads;  // 13
 
 enum Epilogue { kEpiLinear = 0, kEpiTokens = 1 };
 
@@ -51,66 +55,115 @@ struct GemmArgs {
   int n_register;
 };
 
-// A operand from a row-major f32 matrix x[M, K].
+// The loaders below never branch around a global load: a load inside a
+// guard makes the compiler wait for it before the next one, serialising the
+// memory latency.  Slots outside the matrix read a clamped (valid) address
+// and are zeroed when stored to LDS.
+
+// A operand from a row-major f32 matrix x[M, K]; element slot i of a thread
+// covers (m, kk) = (e / KC, e % KC), e = tid + 256 i (k fastest: coalesced).
 struct RowsA {
   const float* x;
-  __device__ __forceinline__ void setup(int, int, int) {}
-  __device__ __forceinline__ void stage(float (*As)[PA], int m0, int k0, int M, int K,
-                                        int tid) const {
+  float reg[kA_PER_THREAD];
+  uint64_t live;  // bit i: slot i inside the matrix for the current chunk
+  __device__ __forceinline__ void init(const float*, int, int, int) {}
+  __device__ __forceinline__ void fetch(int m0, int k0, int M, int K, int tid) {
+    live = 0;
 #pragma unroll
     for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + 256 * i;
-      if (e < KC * BM) {
-        const int kk = e % KC;  // k fastest: coalesced along the row
-        const int m = e / KC;
-        const int gm = m0 + m, gk = k0 + kk;
-        As[kk][m] = (gm < M && gk < K) ? x[static_cast<size_t>(gm) * K + gk] : 0.0f;
-      }
+      const int e = tid + kThreads * i;
+      const int kk = e % KC;
+      const int m = e / KC;
+      const int gm = m0 + m, gk = k0 + kk;
+      const bool ok = e < KC * BM && gm < M && gk < K;
+      live |= static_cast<uint64_t>(ok) << i;
+      const int cm = gm < M ? gm : M - 1;
+      const int ck = gk < K ? gk : K - 1;
+      reg[i] = x[static_cast<size_t>(cm) * K + ck];
+    }
+  }
+  __device__ __forceinline__ void store(float (*As)[PA], int tid) const {
+#pragma unroll
+    for (int i = 0; i < kA_PER_THREAD; ++i) {
+      const int e = tid + kThreads * i;
+      if (e < KC * BM) As[e % KC][e / KC] = ((live >> i) & 1) ? reg[i] : 0.0f;
     }
   }
 };
 
-// A operand gathered from the u8 HWC image, normalised through an LDS table.
+// A operand gathered from the u8 HWC image: one chunk is one input channel c
+// of the 48 patches' 14x14 windows.  Slot i covers (m, kk) = (e % 48, e / 48)
+// (patch fastest), kk = ky*14 + kx; its byte offset for channel 0 is computed
+// once, a chunk adds the channel.  Bytes are normalised at LDS store time.
 struct ImageA {
   const uint8_t* img;
-  int W;        // image width in pixels
-  int gw;       // patches per image row
+  int W;   // image width in pixels
+  int gw;  // patches per image row
   const float* lut;  // LDS, [3][256]
-  int base[kA_PER_THREAD];  // per element slot: byte offset of (patch, ky, kx) for c = 0
-  bool live[kA_PER_THREAD];
+  int off[kA_PER_THREAD];
+  uint32_t reg[kA_PER_THREAD];
+  uint64_t live;
+  int chan;
 
-  __device__ __forceinline__ void setup(int m0, int M, int tid) {
+  __device__ __forceinline__ void init(const float* l, int m0, int M, int tid) {
+    lut = l;
+    live = 0;
 #pragma unroll
     for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + 256 * i;
-      const int m = e % BM;  // patch fastest
+      const int e = tid + kThreads * i;
+      const int m = e % BM;
       const int kk = e / BM;
       const int gm = m0 + m;
-      live[i] = (e < KC * BM) && (gm < M);
-      int off = 0;
-      if (live[i]) {
-        const int py = gm / gw, px = gm % gw;
-        const int ky = kk / kPatch, kx = kk % kPatch;
-        off = ((py * kPatch + ky) * W + px * kPatch + kx) * 3;
-      }
-      base[i] = off;
+      const bool ok = e < KC * BM && gm < M;
+      live |= static_cast<uint64_t>(ok) << i;
+      const int cm = gm < M ? gm : M - 1;
+      const int ckk = kk < KC ? kk : KC - 1;
+      const int py = cm / gw, px = cm - py * gw;
+      const int ky = ckk / kPatch, kx = ckk - ky * kPatch;
+      off[i] = ((py * kPatch + ky) * W + px * kPatch + kx) * 3;
     }
   }
-
-  __device__ __forceinline__ void stage(float (*As)[PA], int, int k0, int, int, int tid) const {
-    // the chunk is rows ky0, ky0+1 of channel c
-    const int c = k0 / (kPatch * kPatch);
-    const int ky0 = (k0 % (kPatch * kPatch)) / kPatch;
-    const int chunk_off = ky0 * W * 3 + c;
-    const float* t = lut + c * 256;
+  __device__ __forceinline__ void fetch(int, int k0, int, int, int) {
+    chan = k0 / (kPatch * kPatch);
+#pragma unroll
+    for (int i = 0; i < kA_PER_THREAD; ++i) reg[i] = img[off[i] + chan];
+  }
+  __device__ __forceinline__ void store(float (*As)[PA], int tid) const {
+    const float* t = lut + chan * 256;
 #pragma unroll
     for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + 256 * i;
-      if (e < KC * BM) {
-        const int m = e % BM;
-        const int kk = e / BM;
-        As[kk][m] = live[i] ? t[img[base[i] + chunk_off]] : 0.0f;
-      }
+      const int e = tid + kThreads * i;
+      if (e < KC * BM) As[e / BM][e % BM] = ((live >> i) & 1) ? t[reg[i]] : 0.0f;
+    }
+  }
+};
+
+struct BRegs {
+  float4 reg[kB_VEC_PER_THREAD];
+  uint32_t live;
+  __device__ __forceinline__ void fetch(const GemmArgs& g, int n0, int k0, int tid) {
+    live = 0;
+#pragma unroll
+    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
+      const int f = tid + kThreads * i;
+      const int kk = f / (BN / 4);
+      const int c4 = f % (BN / 4);
+      const int gk = k0 + kk, gn = n0 + c4 * 4;
+      // N % 4 == 0: a vector never straddles the edge
+      const bool ok = f < KC * BN / 4 && gk < g.K && gn < g.N;
+      live |= static_cast<uint32_t>(ok) << i;
+      const int ck = gk < g.K ? gk : g.K - 1;
+      const int cn = gn < g.N ? gn : g.N - 4;
+      reg[i] = *reinterpret_cast<const float4*>(g.wkn + static_cast<size_t>(ck) * g.N + cn);
+    }
+  }
+  __device__ __forceinline__ void store(float (*Bs)[PB], int tid) const {
+#pragma unroll
+    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
+      const int f = tid + kThreads * i;
+      if (f < KC * BN / 4)
+        *reinterpret_cast<float4*>(&Bs[f / (BN / 4)][(f % (BN / 4)) * 4]) =
+            ((live >> i) & 1) ? reg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
 };
@@ -131,39 +184,34 @@ __global__ __launch_bounds__(256) void mfma_gemm_kernel(ALoader a_src, GemmArgs 
 
   if constexpr (EPI == kEpiTokens) {
     // (v/255 - mean[c]) / std[c], exactly as the scalar normalisation
-    for (int e = tid; e < 3 * 256; e += 256) {
+    for (int e = tid; e < 3 * 256; e += kThreads) {
       const int c = e / 256, v = e % 256;
       const float mean = c == 0 ? m0n : (c == 1 ? m1n : m2n);
       const float sd = c == 0 ? s0 : (c == 1 ? s1 : s2);
       const float u = static_cast<float>(v) / 255.0f;
       lut[e] = (u - mean) / sd;
     }
-    a_src.lut = lut;
-    __syncthreads();
   }
-  a_src.setup(m0, g.M, tid);
+  a_src.init(lut, m0, g.M, tid);
 
   f32x4 acc[3];
 #pragma unroll
   for (int t = 0; t < 3; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  BRegs b_src;
+  a_src.fetch(m0, 0, g.M, g.K, tid);
+  b_src.fetch(g, n0, 0, tid);
+  __syncthreads();  // LUT visible before the first normalised store
   for (int k0 = 0; k0 < g.K; k0 += KC) {
-    a_src.stage(As, m0, k0, g.M, g.K, tid);
-#pragma unroll
-    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
-      const int f = tid + 256 * i;
-      if (f < KC * BN / 4) {
-        const int kk = f / (BN / 4);
-        const int c4 = f % (BN / 4);
-        const int gk = k0 + kk, gn = n0 + c4 * 4;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (gk < g.K && gn < g.N)  // N % 4 == 0: a vector never straddles the edge
-          v = *reinterpret_cast<const float4*>(g.wkn + static_cast<size_t>(gk) * g.N + gn);
-        *reinterpret_cast<float4*>(&Bs[kk][c4 * 4]) = v;
-      }
-    }
+    a_src.store(As, tid);
+    b_src.store(Bs, tid);
     __syncthreads();
-#pragma unroll
+    if (k0 + KC < g.K) {
+      // next chunk's global loads overlap this chunk's MFMAs
+      a_src.fetch(m0, k0 + KC, g.M, g.K, tid);
+      b_src.fetch(g, n0, k0 + KC, tid);
+    }
+#pragma unroll 7
     for (int ks = 0; ks < KC; ks += 4) {
       const float b = Bs[ks + (lane >> 4)][wave * 16 + (lane & 15)];
 #pragma unroll
