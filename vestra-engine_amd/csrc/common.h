@@ -38,7 +38,12 @@ struct vk_linear {
   vk_runtime* rt = nullptr;
   size_t in_features = 0;
   size_t out_features = 0;
-  float* weight_kn = nullptr;  // [in, out], out contiguous
+  size_t k_pitch = 0;          // in_features rounded up to 16
+  float* weight_nk = nullptr;  // [out, k_pitch], input dimension contiguous
+  // For a 3x14x14 patch filter (in_features 588) only: the same rows with
+  // the input dimension reordered (c, ky, kx) -> (ky, kx, c), the order in
+  // which an HWC image holds a patch.
+  float* weight_patch = nullptr;
   float* bias = nullptr;       // [out]
   float* ls_gamma = nullptr;   // [out] or null
 };

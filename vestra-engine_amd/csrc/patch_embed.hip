@@ -1,26 +1,32 @@
-// Patch embedding for gfx950: the only MFMA contraction of the fused path.
+// Patch embedding and the F32 linear for gfx950: the MFMA contractions of
+// the fused path.
 //
 // The 14x14 / stride-14 patch convolution is a GEMM
-//   tokens[p, e] = sum_k A[p, k] * W[e, k] + b[e],   k = c*196 + ky*14 + kx,
-// with A the normalised, unfolded image.  One kernel does it all: the A
-// operand is gathered straight from the u8 HWC image and normalised through a
-// 3x256 lookup table in LDS (the table holds exactly (u8/255 - mean)/std, so
-// the normalisation is bit-identical to the scalar path), the filter is
-// streamed from a [K, N] copy made at prepare time, the products run on
-// v_mfma_f32_16x16x4_f32 (F32 in, F32 accumulate), and the epilogue adds the
-// bias and the position table and writes the assembled token rows (CLS +
-// pos[0], register rows, patch rows) so nothing round-trips through HBM.
+//   tokens[p, e] = sum_k A[p, k] * W[e, k] + b[e]
+// with A the normalised, unfolded image.  patch_embed_kernel does it all in
+// one pass: A is gathered straight from the u8 HWC image and normalised
+// through a 3x256 lookup table in LDS (the table holds exactly
+// (u8/255 - mean)/std, so the normalisation is bit-identical to the scalar
+// path), the filter is read from a copy of its rows reordered at prepare
+// time to the image's byte order, the products run on v_mfma_f32_16x16x4_f32
+// (F32 in, F32 accumulate), and the epilogue adds the bias and the position
+// table and writes the assembled token rows (CLS + pos[0], register rows,
+// patch rows) so nothing round-trips through HBM.
 //
-// Tiling: a 256-thread workgroup (4 waves) owns a 48 (patches) x 64 (embed)
-// output tile; wave w owns 16 embed columns across all 48 rows (three 16x16
-// accumulators).  K is consumed in chunks of 196 = one input channel of a
-// 14x14 patch (3 chunks per image), staged in LDS as A^T[k][m] and B[k][n]
-// with a row pitch of 80 floats, which makes both fragment reads bank-conflict
-// free.  While the MFMAs consume one chunk from LDS, the next chunk's global
-// loads are already in flight into registers, so each chunk's load latency is
-// hidden behind the previous chunk's 147 MFMAs.  The 125 KB of LDS allows one
-// workgroup per CU: ViT-B at 504x336 is 864 x 768 outputs -> 18 x 12 = 216
-// workgroups, one round on 256 CUs.
+// Both kernels compute 48 x 64 output tiles with 8 MFMA waves (two per
+// SIMD).  Wave w computes the 48 x 16 strip w%4 (three 16x16 accumulators)
+// over one half of K (split-K inside the workgroup); the two partial sums
+// meet in LDS before the epilogue.  Two waves per SIMD let one wave's MFMAs
+// run while the other waits on memory.
+//
+// Fragment order.  v_mfma_f32_16x16x4_f32 takes, in lane l, A[l%16][k] and
+// B[k][l%16] for the lane's k = one of 4 per step (lane group g = l/16).  K is
+// walked in blocks of 16: in block b, lane group g holds k = 16b + 4g + j in
+// component j of a 128-bit read, and step j of the block multiplies component
+// j, so four steps cover the block's 16 k once and one ds_read_b128 feeds
+// four MFMAs.  With LDS rows k-contiguous and a row pitch of 4 x odd floats,
+// the 16 rows of a fragment read start on 16 distinct 4-bank groups: no bank
+// conflicts.
 #include <cstring>
 #include <vector>
 
@@ -32,225 +38,435 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 48;
 constexpr int BN = 64;
-constexpr int KC = 196;
-constexpr int PA = 80;  // LDS pitch of A^T rows (BM + 32)
-constexpr int PB = 80;  // LDS pitch of B rows (BN + 16)
+constexpr int kThreads = 512;
 constexpr int kPatch = 14;
-constexpr int kThreads = 256;
-constexpr int kA_PER_THREAD = (KC * BM + kThreads - 1) / kThreads;        // 37
-constexpr int kB_VEC_PER_THREAD = (KC * BN / 4 + kThreads - 1) / kThreads;  // 13
+constexpr int kKAlign = 16;  // weight rows are zero-padded to a 16-block
 
-enum Epilogue { kEpiLinear = 0, kEpiTokens = 1 };
+__device__ __forceinline__ void mfma_block(const float* arow, int t_pitch, const f32x4& b,
+                                           f32x4 acc[3]) {
+  f32x4 a[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) a[t] = *reinterpret_cast<const f32x4*>(arow + t * t_pitch);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][j], b[j], acc[t], 0, 0, 0);
+}
 
-struct GemmArgs {
-  const float* wkn;    // [K, N]
-  const float* bias;   // [N]
-  const float* ls;     // [N] or null (linear epilogue)
-  float* out;
-  int M, N, K;
-  // token epilogue
-  const float* pos;    // [(1 + M), N]
-  const float* cls;    // [N]
-  const float* regs;   // [n_register, N] or null
-  int n_register;
+// Split-K reduction: waves 4-7 hand their partial sums to waves 0-3.  Returns
+// false in waves 4-7, which are then done.
+__device__ __forceinline__ bool reduce_halves(float* red, int strip, int half, int lane,
+                                              f32x4 acc[3]) {
+  if (half == 1) {
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[(strip * 12 + t * 4 + r) * 64 + lane] = acc[t][r];
+  }
+  __syncthreads();
+  if (half == 1) return false;
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] += red[(strip * 12 + t * 4 + r) * 64 + lane];
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// F32 linear: out[m, n] = (sum_k x[m, k] W[n, k] + b[n]) (* ls[n])
+// K is staged through LDS in chunks of 192 (12 blocks); waves 0-3 take blocks
+// 0-5 of a chunk, waves 4-7 blocks 6-11.  While the MFMAs consume one chunk,
+// the next chunk's global loads are in flight into registers.
+// ---------------------------------------------------------------------------
+constexpr int KC = 192;
+constexpr int kLinPitch = 196;  // 4 x 49
+constexpr int kLinBlocks = KC / 16 / 2;  // per half
+constexpr int kA_PER_THREAD = (KC * BM + kThreads - 1) / kThreads;        // 18
+constexpr int kB_VEC_PER_THREAD = (KC * BN / 4 + kThreads - 1) / kThreads;  // 6
+static_assert(kLinPitch % 4 == 0 && (kLinPitch / 4) % 2 == 1, "pitch must be 4 x odd");
+static_assert(KC * BM % kThreads == 0 && KC * BN / 4 % kThreads == 0, "slots divide evenly");
+
+struct LinearArgs {
+  const float* x;     // [M, K]
+  const float* wnk;   // [N, Kp], K contiguous, zero beyond K
+  const float* bias;  // [N]
+  const float* ls;    // [N] or null
+  float* out;         // [M, N]
+  int M, N, K, Kp;
 };
 
-// The loaders below never branch around a global load: a load inside a
-// guard makes the compiler wait for it before the next one, serialising the
-// memory latency.  Slots outside the matrix read a clamped (valid) address
-// and are zeroed when stored to LDS.
+// The loaders never branch around a global load: a load inside a guard
+// makes the compiler wait for it before the next one, serialising the memory
+// latency.  Slots outside the matrix read a clamped (valid) address and are
+// zeroed when stored to LDS.  A slot e = tid + 512 i covers (m, kk) =
+// (e / KC, e % KC): k fastest, so a wave's loads walk along matrix rows and
+// its LDS stores hit consecutive banks.
+struct LinearStage {
+  float a[kA_PER_THREAD];
+  float4 b[kB_VEC_PER_THREAD];
+  uint32_t live_a, live_b;
 
-// A operand from a row-major f32 matrix x[M, K]; element slot i of a thread
-// covers (m, kk) = (e / KC, e % KC), e = tid + 256 i (k fastest: coalesced).
-struct RowsA {
-  const float* x;
-  float reg[kA_PER_THREAD];
-  uint64_t live;  // bit i: slot i inside the matrix for the current chunk
-  __device__ __forceinline__ void init(const float*, int, int, int) {}
-  __device__ __forceinline__ void fetch(int m0, int k0, int M, int K, int tid) {
-    live = 0;
+  __device__ __forceinline__ void fetch(const LinearArgs& g, int m0, int n0, int k0, int tid) {
+    live_a = 0;
 #pragma unroll
     for (int i = 0; i < kA_PER_THREAD; ++i) {
       const int e = tid + kThreads * i;
-      const int kk = e % KC;
-      const int m = e / KC;
+      const int m = e / KC, kk = e % KC;
       const int gm = m0 + m, gk = k0 + kk;
-      const bool ok = e < KC * BM && gm < M && gk < K;
-      live |= static_cast<uint64_t>(ok) << i;
-      const int cm = gm < M ? gm : M - 1;
-      const int ck = gk < K ? gk : K - 1;
-      reg[i] = x[static_cast<size_t>(cm) * K + ck];
-    }
-  }
-  __device__ __forceinline__ void store(float (*As)[PA], int tid) const {
-#pragma unroll
-    for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + kThreads * i;
-      if (e < KC * BM) As[e % KC][e / KC] = ((live >> i) & 1) ? reg[i] : 0.0f;
-    }
-  }
-};
-
-// A operand gathered from the u8 HWC image: one chunk is one input channel c
-// of the 48 patches' 14x14 windows.  Slot i covers (m, kk) = (e % 48, e / 48)
-// (patch fastest), kk = ky*14 + kx; its byte offset for channel 0 is computed
-// once, a chunk adds the channel.  Bytes are normalised at LDS store time.
-struct ImageA {
-  const uint8_t* img;
-  int W;   // image width in pixels
-  int gw;  // patches per image row
-  const float* lut;  // LDS, [3][256]
-  int off[kA_PER_THREAD];
-  uint32_t reg[kA_PER_THREAD];
-  uint64_t live;
-  int chan;
-
-  __device__ __forceinline__ void init(const float* l, int m0, int M, int tid) {
-    lut = l;
-    live = 0;
-#pragma unroll
-    for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + kThreads * i;
-      const int m = e % BM;
-      const int kk = e / BM;
-      const int gm = m0 + m;
-      const bool ok = e < KC * BM && gm < M;
-      live |= static_cast<uint64_t>(ok) << i;
-      const int cm = gm < M ? gm : M - 1;
-      const int ckk = kk < KC ? kk : KC - 1;
-      const int py = cm / gw, px = cm - py * gw;
-      const int ky = ckk / kPatch, kx = ckk - ky * kPatch;
-      off[i] = ((py * kPatch + ky) * W + px * kPatch + kx) * 3;
-    }
-  }
-  __device__ __forceinline__ void fetch(int, int k0, int, int, int) {
-    chan = k0 / (kPatch * kPatch);
-#pragma unroll
-    for (int i = 0; i < kA_PER_THREAD; ++i) reg[i] = img[off[i] + chan];
-  }
-  __device__ __forceinline__ void store(float (*As)[PA], int tid) const {
-    const float* t = lut + chan * 256;
-#pragma unroll
-    for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + kThreads * i;
-      if (e < KC * BM) As[e / BM][e % BM] = ((live >> i) & 1) ? t[reg[i]] : 0.0f;
-    }
-  }
-};
-
-struct BRegs {
-  float4 reg[kB_VEC_PER_THREAD];
-  uint32_t live;
-  __device__ __forceinline__ void fetch(const GemmArgs& g, int n0, int k0, int tid) {
-    live = 0;
-#pragma unroll
-    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
-      const int f = tid + kThreads * i;
-      const int kk = f / (BN / 4);
-      const int c4 = f % (BN / 4);
-      const int gk = k0 + kk, gn = n0 + c4 * 4;
-      // N % 4 == 0: a vector never straddles the edge
-      const bool ok = f < KC * BN / 4 && gk < g.K && gn < g.N;
-      live |= static_cast<uint32_t>(ok) << i;
+      live_a |= static_cast<uint32_t>(gm < g.M && gk < g.K) << i;
+      const int cm = gm < g.M ? gm : g.M - 1;
       const int ck = gk < g.K ? gk : g.K - 1;
-      const int cn = gn < g.N ? gn : g.N - 4;
-      reg[i] = *reinterpret_cast<const float4*>(g.wkn + static_cast<size_t>(ck) * g.N + cn);
+      a[i] = g.x[static_cast<size_t>(cm) * g.K + ck];
     }
-  }
-  __device__ __forceinline__ void store(float (*Bs)[PB], int tid) const {
+    live_b = 0;
 #pragma unroll
     for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
       const int f = tid + kThreads * i;
-      if (f < KC * BN / 4)
-        *reinterpret_cast<float4*>(&Bs[f / (BN / 4)][(f % (BN / 4)) * 4]) =
-            ((live >> i) & 1) ? reg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int n = f / (KC / 4), j = f % (KC / 4);
+      const int gn = n0 + n, gk = k0 + 4 * j;
+      // Kp % 4 == 0 and gk % 4 == 0: a vector never straddles the row end
+      live_b |= static_cast<uint32_t>(gn < g.N && gk < g.Kp) << i;
+      const int cn = gn < g.N ? gn : g.N - 1;
+      const int ck = gk < g.Kp ? gk : g.Kp - 4;
+      b[i] = *reinterpret_cast<const float4*>(g.wnk + static_cast<size_t>(cn) * g.Kp + ck);
+    }
+  }
+  __device__ __forceinline__ void store(float* As, float* Bs, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kA_PER_THREAD; ++i) {
+      const int e = tid + kThreads * i;
+      As[(e / KC) * kLinPitch + e % KC] = ((live_a >> i) & 1) ? a[i] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
+      const int f = tid + kThreads * i;
+      const bool on = (live_b >> i) & 1;
+      const float4 v = make_float4(on ? b[i].x : 0.f, on ? b[i].y : 0.f, on ? b[i].z : 0.f,
+                                   on ? b[i].w : 0.f);
+      *reinterpret_cast<float4*>(Bs + (f / (KC / 4)) * kLinPitch + 4 * (f % (KC / 4))) = v;
     }
   }
 };
 
-template <class ALoader, int EPI>
-__global__ __launch_bounds__(256) void mfma_gemm_kernel(ALoader a_src, GemmArgs g,
-                                                        float m0n, float m1n, float m2n,
-                                                        float s0, float s1, float s2) {
-  __shared__ float As[KC][PA];
-  __shared__ float Bs[KC][PB];
-  __shared__ float lut[EPI == kEpiTokens ? 3 * 256 : 1];
+__global__ __launch_bounds__(kThreads) void linear_kernel(LinearArgs g) {
+  __shared__ __align__(16) float As[BM * kLinPitch];
+  __shared__ __align__(16) float Bs[BN * kLinPitch];
+  __shared__ float red[4 * 12 * 64];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int m0 = blockIdx.x * BM;
-  const int n0 = blockIdx.y * BN;
+  __builtin_assume(tid < kThreads);
+  const int wave = tid >> 6, lane = tid & 63;
+  const int strip = wave & 3, half = wave >> 2;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
 
-  if constexpr (EPI == kEpiTokens) {
-    // (v/255 - mean[c]) / std[c], exactly as the scalar normalisation
-    for (int e = tid; e < 3 * 256; e += kThreads) {
-      const int c = e / 256, v = e % 256;
-      const float mean = c == 0 ? m0n : (c == 1 ? m1n : m2n);
-      const float sd = c == 0 ? s0 : (c == 1 ? s1 : s2);
-      const float u = static_cast<float>(v) / 255.0f;
-      lut[e] = (u - mean) / sd;
-    }
-  }
-  a_src.init(lut, m0, g.M, tid);
+  LinearStage st;
+  st.fetch(g, m0, n0, 0, tid);
 
   f32x4 acc[3];
 #pragma unroll
   for (int t = 0; t < 3; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int kofs = 4 * (lane >> 4) + 16 * kLinBlocks * half;
+  const float* arow = As + (lane & 15) * kLinPitch + kofs;
+  const float* brow = Bs + (strip * 16 + (lane & 15)) * kLinPitch + kofs;
 
-  BRegs b_src;
-  a_src.fetch(m0, 0, g.M, g.K, tid);
-  b_src.fetch(g, n0, 0, tid);
-  __syncthreads();  // LUT visible before the first normalised store
   for (int k0 = 0; k0 < g.K; k0 += KC) {
-    a_src.store(As, tid);
-    b_src.store(Bs, tid);
+    st.store(As, Bs, tid);
     __syncthreads();
-    if (k0 + KC < g.K) {
-      // next chunk's global loads overlap this chunk's MFMAs
-      a_src.fetch(m0, k0 + KC, g.M, g.K, tid);
-      b_src.fetch(g, n0, k0 + KC, tid);
-    }
-#pragma unroll 7
-    for (int ks = 0; ks < KC; ks += 4) {
-      const float b = Bs[ks + (lane >> 4)][wave * 16 + (lane & 15)];
+    if (k0 + KC < g.K) st.fetch(g, m0, n0, k0 + KC, tid);
 #pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        const float a = As[ks + (lane >> 4)][t * 16 + (lane & 15)];
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[t], 0, 0, 0);
-      }
+    for (int j = 0; j < kLinBlocks; ++j) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(brow + 16 * j);
+      mfma_block(arow + 16 * j, 16 * kLinPitch, b, acc);
     }
     __syncthreads();
   }
+  if (!reduce_halves(red, strip, half, lane, acc)) return;
 
   // epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile
-  const int col = n0 + wave * 16 + (lane & 15);
-  if (col < g.N) {
-    const float bias = g.bias[col];
-    float ls = 1.0f;
-    if (EPI == kEpiLinear && g.ls) ls = g.ls[col];
+  const int col = n0 + strip * 16 + (lane & 15);
+  if (col >= g.N) return;
+  const float bias = g.bias[col];
+  const float ls = g.ls ? g.ls[col] : 1.0f;
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
+      if (row < g.M) {
+        float v = acc[t][r] + bias;
+        if (g.ls) v = v * ls;
+        g.out[static_cast<size_t>(row) * g.N + col] = v;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused patch embedding.  K is taken in the image's own order, k = ky*42 +
+// kx*3 + c (the filter is reordered to match at prepare time), so one patch
+// row is 42 contiguous bytes of the HWC image and 42 consecutive k.  The whole
+// A tile (48 patches x 588, 113 KB) lives in LDS, gathered and normalised
+// once; each wave streams its B fragments (16 columns x its half of K)
+// straight from L2 into registers, eight blocks ahead of the MFMAs.
+//
+// The workgroup has 12 waves: waves 0-7 run the MFMAs (two per SIMD, as the
+// linear), waves 8-11 only stage.  Staging overlaps the MFMAs: pixel rows ky
+// 0-7 of every patch (k < 336 = 21 blocks) are normalised into LDS first;
+// then the compute waves run those blocks (waves 0-3 blocks 0-10, waves 4-7
+// blocks 11-20) while the staging waves normalise rows ky 8-13; one barrier
+// later waves 0-3 run blocks 21-28 and waves 4-7 blocks 29-36.
+// ---------------------------------------------------------------------------
+constexpr int kPeRowBytes = 3 * kPatch;    // 42 bytes per patch row
+constexpr int kPeK = kPatch * kPeRowBytes; // 588
+constexpr int kPeKp = 592;                 // 37 blocks of 16
+constexpr int kPeBlocks = kPeKp / 16;
+constexpr int kPeSplitKy = 8;              // first stage: ky < 8
+constexpr int kPeBlocksA = kPeSplitKy * kPeRowBytes / 16;  // 21 blocks in the first stage
+constexpr int kPeRowsA = kPeSplitKy * BM;                  // 384 patch rows
+constexpr int kPeRowsB = (kPatch - kPeSplitKy) * BM;       // 288 patch rows
+constexpr int kPePhase1 = kPeBlocksA / 2 + 1;              // 11 for waves 0-3, 10 for 4-7
+constexpr int kPePhase2 = (kPeBlocks - kPeBlocksA) / 2;    // 8
+constexpr int kPeSeq = kPePhase1 + kPePhase2;              // 19 blocks of waves 0-3
+constexpr int kPeAhead = 8;                // B prefetch distance in blocks
+constexpr int kPePitch = 596;              // A row pitch in LDS: 4 x 149
+constexpr int kPeStagers = 256;            // waves 8-11
+constexpr int kPeThreads = kThreads + kPeStagers;
+static_assert(kPeKp % 16 == 0 && kPeKp >= kPeK && kPeKp == (kPeK + kKAlign - 1) / kKAlign * kKAlign,
+              "weight rows padded to a 16-block");
+static_assert(kPeSplitKy * kPeRowBytes % 16 == 0, "stage boundary on a block boundary");
+static_assert(BM == 48 && kPatch % 2 == 0 && kPeSplitKy % 2 == 0,
+              "patch-row groups of 16 patches x 2 pixel rows");
+static_assert(kPeBlocksA == 2 * kPePhase1 - 1 && kPeBlocks - kPeBlocksA == 2 * kPePhase2,
+              "block split");
+static_assert(kPeRowsA <= kThreads && kPeRowsA % 64 == 0 && kPeRowsB > kPeStagers &&
+                  kPeRowsB <= 2 * kPeStagers && 3 * 256 == kPeThreads,
+              "stage A: one patch row per thread of the first waves; stage B: at most two per "
+              "staging thread; one table entry per thread");
+static_assert(kPePitch % 4 == 0 && (kPePitch / 4) % 2 == 1 && kPePitch >= kPeKp, "pitch 4 x odd");
+
+struct PatchArgs {
+  const uint8_t* img;  // [H, W, 3], 8-byte aligned
+  const float* wpk;    // [N, 592], k = ky*42 + kx*3 + c, zero beyond 588
+  const float* bias;   // [N]
+  const float* pos;    // [(1 + M), N]
+  const float* cls;    // [N]
+  const float* regs;   // [n_register, N] or null
+  float* out;          // [(1 + n_register + M), N]
+  uint32_t img_bytes;  // H*W*3, a multiple of 4
+  int W, gw, M, N, n_register;
+  vkd::FastDivU32 fgw;  // division by gw
+  float mean[3], sd[3];
+};
+
+// One patch row: its 42 bytes, starting at byte `st` of the image, read as
+// five aligned 8-byte words and two 4-byte words (48 bytes from st rounded
+// down to 8; st is even, so that covers st..st+41), then funnel-shifted so
+// that dword i holds row bytes 4i..4i+3, normalised through the table and
+// written to A[m][ky*42 ..] two floats at a time.  Every read stays inside
+// the image: the last word is clamped and is only consumed when it lies
+// inside.
+struct PatchRow {
+  uint32_t w[12];
+  uint32_t s8;
+  __device__ __forceinline__ void load(const uint8_t* img, uint32_t st, uint32_t img_bytes) {
+    const uint32_t a8 = st & ~7u;
+    s8 = st & 7u;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      const uint2 v = *reinterpret_cast<const uint2*>(img + a8 + 8 * j);
+      w[2 * j] = v.x;
+      w[2 * j + 1] = v.y;
+    }
+    w[10] = *reinterpret_cast<const uint32_t*>(img + a8 + 40);
+    const uint32_t a44 = a8 + 44 <= img_bytes - 4 ? a8 + 44 : img_bytes - 4;
+    w[11] = *reinterpret_cast<const uint32_t*>(img + a44);
+  }
+  // w[i] (i < 11) := row bytes 4i..4i+3 (bytes 42, 43 are padding)
+  __device__ __forceinline__ void align() {
+    const bool dw = s8 >= 4;
+    const uint32_t sh = s8 & 3u;
+    uint32_t t[12];
+#pragma unroll
+    for (int i = 0; i < 11; ++i) t[i] = dw ? w[i + 1] : w[i];
+    t[11] = dw ? 0u : w[11];
+#pragma unroll
+    for (int i = 0; i < 11; ++i) w[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
+  }
+  // pairs q0 <= q < q1 of the aligned row (pair q = bytes 2q, 2q+1)
+  __device__ __forceinline__ void store(float2* dst, const float* lut, int q0, int q1) const {
+#pragma unroll
+    for (int q = q0; q < q1; ++q) {
+      const int b = 2 * q;
+      const uint32_t v0 = (w[b >> 2] >> (8 * (b & 3))) & 0xffu;
+      const uint32_t v1 = (w[(b + 1) >> 2] >> (8 * ((b + 1) & 3))) & 0xffu;
+      dst[q] = make_float2(lut[(b % 3) * 256 + v0], lut[((b + 1) % 3) * 256 + v1]);
+    }
+  }
+};
+
+__global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
+  __shared__ float lut[3 * 256];
+  __shared__ __align__(16) float As[BM * kPePitch];
+  __shared__ float red[4 * 12 * 64];
+
+  const int tid = threadIdx.x;
+  __builtin_assume(tid < kPeThreads);
+  const int wave = tid >> 6, lane = tid & 63;
+  const bool stager = tid >= kThreads;
+  const int strip = wave & 3, half = (wave >> 2) & 1;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+
+  // Patch row R of the tile (0..671): each group of 32 rows is 16 patches x
+  // 2 pixel rows, m = 16 (g % 3) + R % 16 and ky = 2 (g / 3) + (R / 16) % 2
+  // with g = R / 32.  A half-wave then reads two pixel rows of 16 adjacent
+  // patches, and its 8-byte LDS writes (row pitch 596 = 20 mod 64 banks,
+  // the second pixel row 42 = 2 mod 4 banks further) hit all 64 banks once.
+  // Rows with ky < 8 are exactly R < 384.
+  auto row_m = [](int r) { return 16 * ((r >> 5) % 3) + (r & 15); };
+  auto row_ky = [](int r) { return 2 * ((r >> 5) / 3) + ((r >> 4) & 1); };
+  // byte offset of a patch row (patches past the image clamp to the last
+  // one: their rows compute values that are never stored)
+  auto row_start = [&](int r) {
+    const int gm = m0 + row_m(r);
+    const int cm = gm < p.M ? gm : p.M - 1;
+    const uint32_t py = vkd::fdiv(static_cast<uint32_t>(cm), p.fgw);
+    const uint32_t px = static_cast<uint32_t>(cm) - py * static_cast<uint32_t>(p.gw);
+    return ((py * kPatch + row_ky(r)) * static_cast<uint32_t>(p.W) + px * kPatch) * 3u;
+  };
+  auto row_dst = [&](int r) {
+    return reinterpret_cast<float2*>(As + row_m(r) * kPePitch + row_ky(r) * kPeRowBytes);
+  };
+
+  // 1. gather.  Stage A (rows 0..383, ky < 8): thread tid holds row tid.
+  // Stage B (rows 384..671): staging thread t = tid - 512 holds rows 384 + t
+  // and, for t < 32, 640 + t.
+  PatchRow row_a, row_b0, row_b1;
+  const int tb = tid - kThreads;
+  const int rb0 = kPeRowsA + (tb >= 0 ? tb : 0);
+  const int rb1 = kPeRowsA + kPeStagers +
+                  (tb >= 0 && tb < kPeRowsB - kPeStagers ? tb : kPeRowsB - kPeStagers - 1);
+  if (tid < kPeRowsA) row_a.load(p.img, row_start(tid), p.img_bytes);
+  if (stager) {
+    row_b0.load(p.img, row_start(rb0), p.img_bytes);
+    row_b1.load(p.img, row_start(rb1), p.img_bytes);
+  }
+
+  // 2. B fragments (compute waves).  Block sequence: waves 0-3 run blocks
+  // 0-10 then 21-28, waves 4-7 blocks 11-20 then 29-36.
+  auto seq_block = [&](int s) {
+    const int b = half ? (s < kPePhase1 - 1 ? kPePhase1 + s
+                                            : kPeBlocksA + kPePhase2 + s - (kPePhase1 - 1))
+                       : (s < kPePhase1 ? s : kPeBlocksA + s - kPePhase1);
+    return b < kPeBlocks ? b : kPeBlocks - 1;
+  };
+  const int col = n0 + strip * 16 + (lane & 15);
+  const int ccol = col < p.N ? col : p.N - 1;
+  const float* wrow = p.wpk + static_cast<size_t>(ccol) * kPeKp + 4 * (lane >> 4);
+  f32x4 bf[kPeSeq];
+  auto load_b = [&](int s) {
+    if (s < kPeSeq) bf[s] = *reinterpret_cast<const f32x4*>(wrow + 16 * seq_block(s));
+  };
+
+  // 3. (v/255 - mean[c]) / std[c], exactly as the scalar normalisation (one
+  // entry per thread), and zeros in the K padding 588..591
+  {
+    const int c = tid / 256, v = tid % 256;
+    const float u = static_cast<float>(v) / 255.0f;
+    lut[tid] = (u - p.mean[c]) / p.sd[c];
+  }
+  if (tid < BM * 4) As[(tid >> 2) * kPePitch + kPeK + (tid & 3)] = 0.0f;
+  __syncthreads();  // LUT visible
+
+  // 4. stage A into LDS; the first B fragments load meanwhile (they are not
+  // needed before phase 1, and issuing them earlier delays the barrier above)
+  if (!stager) {
+#pragma unroll
+    for (int s = 0; s < kPeAhead; ++s) load_b(s);
+  }
+  if (tid < kPeRowsA) {
+    row_a.align();
+    row_a.store(row_dst(tid), lut, 0, kPeRowBytes / 2);
+  }
+  __syncthreads();
+
+  // 5. phase 1: compute waves run stage-A blocks, staging waves stage B
+  f32x4 acc[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* arow = As + (lane & 15) * kPePitch + 4 * (lane >> 4);
+  auto block = [&](int s) { mfma_block(arow + 16 * seq_block(s), 16 * kPePitch, bf[s], acc); };
+  if (stager) {
+    row_b0.align();
+    row_b0.store(row_dst(rb0), lut, 0, kPeRowBytes / 2);
+    if (tb < kPeRowsB - kPeStagers) {
+      row_b1.align();
+      row_b1.store(row_dst(rb1), lut, 0, kPeRowBytes / 2);
+    }
+  } else if (half == 0) {
+#pragma unroll
+    for (int s = 0; s < kPePhase1; ++s) {
+      load_b(s + kPeAhead);
+      block(s);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kPePhase1 - 1; ++s) {
+      load_b(s + kPeAhead);
+      block(s);
+    }
+  }
+  __syncthreads();
+  if (stager) {
+    __syncthreads();  // the split-K reduction's barrier
+    return;
+  }
+
+  // 6. epilogue operands, loaded now so their latency hides behind the MFMAs
+  float bias = 0.0f;
+  float addend[3][4];
+  if (half == 0) {
+    bias = p.bias[ccol];
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
-        if (row < g.M) {
-          float v = acc[t][r] + bias;
-          if (EPI == kEpiLinear) {
-            if (g.ls) v = v * ls;
-            g.out[static_cast<size_t>(row) * g.N + col] = v;
-          } else {
-            v = v + g.pos[static_cast<size_t>(1 + row) * g.N + col];
-            g.out[static_cast<size_t>(1 + g.n_register + row) * g.N + col] = v;
-          }
-        }
+        const int crow = row < p.M ? row : p.M - 1;
+        addend[t][r] = p.pos[static_cast<size_t>(1 + crow) * p.N + ccol];
       }
-    }
-    if (EPI == kEpiTokens && blockIdx.x == 0 && lane < 16) {
-      // special rows of this column strip: CLS + pos[0], then registers
-      g.out[col] = g.cls[col] + g.pos[col];
-      for (int r = 0; r < g.n_register; ++r)
-        g.out[static_cast<size_t>(1 + r) * g.N + col] = g.regs[static_cast<size_t>(r) * g.N + col];
+  }
+
+  // 7. phase 2: stage-B blocks
+  if (half == 0) {
+#pragma unroll
+    for (int s = kPePhase1; s < kPeSeq; ++s) block(s);
+  } else {
+#pragma unroll
+    for (int s = kPePhase1 - 1; s < kPeSeq - 1; ++s) block(s);
+  }
+
+  if (!reduce_halves(red, strip, half, lane, acc)) return;
+
+  // 8. epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile
+  if (col < p.N) {
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
+        if (row < p.M)
+          p.out[static_cast<size_t>(1 + p.n_register + row) * p.N + col] =
+              (acc[t][r] + bias) + addend[t][r];
+      }
+  }
+  if (blockIdx.x == 0) {
+    // special rows of this column strip, four rows per pass (one per lane
+    // group): row 0 = CLS + pos[0], rows 1.. = registers
+    for (int r0 = 0; r0 <= p.n_register; r0 += 4) {
+      const int r = r0 + (lane >> 4);
+      if (r <= p.n_register && col < p.N)
+        p.out[static_cast<size_t>(r) * p.N + col] =
+            r == 0 ? p.cls[col] + p.pos[col] : p.regs[static_cast<size_t>(r - 1) * p.N + col];
     }
   }
 }
@@ -344,13 +560,28 @@ int alloc_copy(const float* host, size_t n, float** dev) {
   return VK_OK;
 }
 
-int make_linear(vk_runtime* rt, size_t in, size_t out, const std::vector<float>& wkn,
+// Weight rows [out][kp] with the input dimension contiguous and zero-padded
+// to kp = in rounded up to a 16-block, so 128-bit loads never straddle rows
+// and a last partial block multiplies zeros.
+int make_linear(vk_runtime* rt, size_t in, size_t out, const std::vector<float>& wnk,
                 const float* bias, const float* ls, vk_linear** res) {
   auto* lin = new vk_linear;
   lin->rt = rt;
   lin->in_features = in;
   lin->out_features = out;
-  int s = alloc_copy(wkn.data(), in * out, &lin->weight_kn);
+  lin->k_pitch = (in + kKAlign - 1) / kKAlign * kKAlign;
+  int s = alloc_copy(wnk.data(), lin->k_pitch * out, &lin->weight_nk);
+  if (s == VK_OK && in == static_cast<size_t>(kPeK)) {
+    // (c, ky, kx) -> (ky, kx, c) for the image-order patch embedding
+    std::vector<float> wp(static_cast<size_t>(kPeKp) * out, 0.0f);
+    for (size_t o = 0; o < out; ++o)
+      for (int c = 0; c < 3; ++c)
+        for (int ky = 0; ky < kPatch; ++ky)
+          for (int kx = 0; kx < kPatch; ++kx)
+            wp[o * kPeKp + ky * kPeRowBytes + kx * 3 + c] =
+                wnk[o * lin->k_pitch + (c * kPatch + ky) * kPatch + kx];
+    s = alloc_copy(wp.data(), wp.size(), &lin->weight_patch);
+  }
   if (s == VK_OK) s = alloc_copy(bias, out, &lin->bias);
   if (s == VK_OK && ls) s = alloc_copy(ls, out, &lin->ls_gamma);
   if (s != VK_OK) {
@@ -373,8 +604,11 @@ int vk_linear_prepare_f32(vk_runtime* rt, size_t in_features, size_t out_feature
   VK_REQUIRE(in_features > 0 && out_features > 0, "empty linear");
   VK_UNSUPPORTED_IF(out_features % 4 != 0, "linear: out_features=%zu must be a multiple of 4",
                     out_features);
-  VK_UNSUPPORTED_IF(in_features > 0x7fffffff || out_features > 0x7fffffff, "linear too large");
-  std::vector<float> w(weight_in_out, weight_in_out + in_features * out_features);
+  VK_UNSUPPORTED_IF(in_features > 0x7ffffff0 || out_features > 0x7fffffff, "linear too large");
+  const size_t kp = (in_features + kKAlign - 1) / kKAlign * kKAlign;
+  std::vector<float> w(kp * out_features, 0.0f);
+  for (size_t i = 0; i < in_features; ++i)
+    for (size_t o = 0; o < out_features; ++o) w[o * kp + i] = weight_in_out[i * out_features + o];
   return make_linear(rt, in_features, out_features, w, bias, ls_gamma, out);
 }
 
@@ -385,10 +619,11 @@ int vk_linear_prepare_oihw_f32(vk_runtime* rt, size_t in_features, size_t out_fe
   VK_REQUIRE(in_features > 0 && out_features > 0, "empty linear");
   VK_UNSUPPORTED_IF(out_features % 4 != 0, "linear: out_features=%zu must be a multiple of 4",
                     out_features);
-  VK_UNSUPPORTED_IF(in_features > 0x7fffffff || out_features > 0x7fffffff, "linear too large");
-  std::vector<float> w(in_features * out_features);
+  VK_UNSUPPORTED_IF(in_features > 0x7ffffff0 || out_features > 0x7fffffff, "linear too large");
+  const size_t kp = (in_features + kKAlign - 1) / kKAlign * kKAlign;
+  std::vector<float> w(kp * out_features, 0.0f);
   for (size_t o = 0; o < out_features; ++o)
-    for (size_t i = 0; i < in_features; ++i) w[i * out_features + o] = weight_out_in[o * in_features + i];
+    std::memcpy(&w[o * kp], weight_out_in + o * in_features, in_features * sizeof(float));
   return make_linear(rt, in_features, out_features, w, bias, nullptr, out);
 }
 
@@ -396,7 +631,8 @@ int vk_linear_destroy(vk_linear* lin) {
   if (!lin) return VK_OK;
   if (lin->rt) (void)vk::bind(lin->rt);
   if (lin->rt) (void)hipStreamSynchronize(lin->rt->stream);
-  if (lin->weight_kn) (void)hipFree(lin->weight_kn);
+  if (lin->weight_nk) (void)hipFree(lin->weight_nk);
+  if (lin->weight_patch) (void)hipFree(lin->weight_patch);
   if (lin->bias) (void)hipFree(lin->bias);
   if (lin->ls_gamma) (void)hipFree(lin->ls_gamma);
   delete lin;
@@ -416,19 +652,19 @@ int vk_linear_run_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, 
   vk_tensor* t = nullptr;
   VK_TRY(vk_tensor_alloc(rt, VK_F32, rows * lin->out_features, &t));
   if (rows > 0) {
-    GemmArgs g{};
-    g.wkn = lin->weight_kn;
+    LinearArgs g{};
+    g.x = static_cast<const float*>(x->ptr);
+    g.wnk = lin->weight_nk;
     g.bias = lin->bias;
     g.ls = lin->ls_gamma;
     g.out = static_cast<float*>(t->ptr);
     g.M = static_cast<int>(rows);
     g.N = static_cast<int>(lin->out_features);
     g.K = static_cast<int>(lin->in_features);
-    RowsA a{static_cast<const float*>(x->ptr)};
+    g.Kp = static_cast<int>(lin->k_pitch);
     dim3 grid((g.M + BM - 1) / BM, (g.N + BN - 1) / BN);
-    hipLaunchKernelGGL((mfma_gemm_kernel<RowsA, kEpiLinear>), grid, dim3(256), 0, rt->stream, a,
-                       g, 0.f, 0.f, 0.f, 1.f, 1.f, 1.f);
-    int s = vk::check_launch("mfma_gemm_kernel<rows>");
+    hipLaunchKernelGGL(linear_kernel, grid, dim3(kThreads), 0, rt->stream, g);
+    int s = vk::check_launch("linear_kernel");
     if (s != VK_OK) {
       vk_tensor_destroy(t);
       return s;
@@ -549,26 +785,31 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t
              (1 + n_register + np) * embed, out->len);
   VK_UNSUPPORTED_IF(h * w * 3 > 0x7fffffffULL || np > 0x7fffffffULL, "image too large");
   for (int c = 0; c < 3; ++c) VK_REQUIRE(std_[c] != 0.0f, "std[%d] is zero", c);
-  GemmArgs g{};
-  g.wkn = proj->weight_kn;
-  g.bias = proj->bias;
-  g.ls = nullptr;
-  g.out = static_cast<float*>(out->ptr);
-  g.M = static_cast<int>(np);
-  g.N = static_cast<int>(embed);
-  g.K = static_cast<int>(proj->in_features);
-  g.pos = static_cast<const float*>(pos_table->ptr);
-  g.cls = static_cast<const float*>(cls->ptr);
-  g.regs = n_register ? static_cast<const float*>(registers->ptr) : nullptr;
-  g.n_register = static_cast<int>(n_register);
-  ImageA a{};
+  VK_REQUIRE(proj->weight_patch != nullptr, "projection has no patch-order filter");
+  VK_UNSUPPORTED_IF(reinterpret_cast<uintptr_t>(img_hwc->ptr) % 8 != 0,
+                    "patch_embed_u8: image must be 8-byte aligned");
+  PatchArgs a{};
   a.img = static_cast<const uint8_t*>(img_hwc->ptr);
+  a.img_bytes = static_cast<uint32_t>(h * w * 3);
+  a.wpk = proj->weight_patch;
+  a.bias = proj->bias;
+  a.pos = static_cast<const float*>(pos_table->ptr);
+  a.cls = static_cast<const float*>(cls->ptr);
+  a.regs = n_register ? static_cast<const float*>(registers->ptr) : nullptr;
+  a.out = static_cast<float*>(out->ptr);
   a.W = static_cast<int>(w);
   a.gw = static_cast<int>(gw);
-  dim3 grid((g.M + BM - 1) / BM, (g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((mfma_gemm_kernel<ImageA, kEpiTokens>), grid, dim3(256), 0, rt->stream, a, g,
-                     mean[0], mean[1], mean[2], std_[0], std_[1], std_[2]);
-  return vk::check_launch("mfma_gemm_kernel<image>");
+  a.fgw = vkd::make_fastdiv(static_cast<uint32_t>(gw));
+  a.M = static_cast<int>(np);
+  a.N = static_cast<int>(embed);
+  a.n_register = static_cast<int>(n_register);
+  for (int c = 0; c < 3; ++c) {
+    a.mean[c] = mean[c];
+    a.sd[c] = std_[c];
+  }
+  dim3 grid((a.M + BM - 1) / BM, (a.N + BN - 1) / BN);
+  hipLaunchKernelGGL(patch_embed_kernel, grid, dim3(kPeThreads), 0, rt->stream, a);
+  return vk::check_launch("patch_embed_kernel");
 }
 
 }  // extern "C"
