@@ -42,6 +42,18 @@ constexpr int kThreads = 512;
 constexpr int kPatch = 14;
 constexpr int kKAlign = 16;  // weight rows are zero-padded to a 16-block
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on
+// XCD i % 8), and each XCD has its own L2.  Renumber so that an XCD's
+// workgroups are consecutive tiles t of an N-major order (t -> m = t % gm,
+// n = t / gm): they then share the same few filter columns in that L2.
+// Bijective for any tile count n: XCD x holds n/8 tiles, one more if
+// x < n % 8.
+__device__ __forceinline__ int xcd_tile(int lin, int n) {
+  const int q = n / 8, r = n % 8;
+  const int xcd = lin % 8, slot = lin / 8;
+  return slot + (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q);
+}
+
 __device__ __forceinline__ void mfma_block(const float* arow, int t_pitch, const f32x4& b,
                                            f32x4 acc[3]) {
   f32x4 a[3];
@@ -158,7 +170,9 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearArgs g) {
   __builtin_assume(tid < kThreads);
   const int wave = tid >> 6, lane = tid & 63;
   const int strip = wave & 3, half = wave >> 2;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int gm = (g.M + BM - 1) / BM;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int m0 = (tile % gm) * BM, n0 = (tile / gm) * BN;
 
   LinearStage st;
   st.fetch(g, m0, n0, 0, tid);
@@ -314,7 +328,10 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
   const int wave = tid >> 6, lane = tid & 63;
   const bool stager = tid >= kThreads;
   const int strip = wave & 3, half = (wave >> 2) & 1;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int gmt = (p.M + BM - 1) / BM;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int mt = tile % gmt;
+  const int m0 = mt * BM, n0 = (tile / gmt) * BN;
 
   // Patch row R of the tile (0..671): each group of 32 rows is 16 patches x
   // 2 pixel rows, m = 16 (g % 3) + R % 16 and ky = 2 (g / 3) + (R / 16) % 2
@@ -459,7 +476,7 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
               (acc[t][r] + bias) + addend[t][r];
       }
   }
-  if (blockIdx.x == 0) {
+  if (mt == 0) {
     // special rows of this column strip, four rows per pass (one per lane
     // group): row 0 = CLS + pos[0], rows 1.. = registers
     for (int r0 = 0; r0 <= p.n_register; r0 += 4) {
@@ -662,8 +679,10 @@ int vk_linear_run_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, 
     g.N = static_cast<int>(lin->out_features);
     g.K = static_cast<int>(lin->in_features);
     g.Kp = static_cast<int>(lin->k_pitch);
-    dim3 grid((g.M + BM - 1) / BM, (g.N + BN - 1) / BN);
-    hipLaunchKernelGGL(linear_kernel, grid, dim3(kThreads), 0, rt->stream, g);
+    const long long tiles = static_cast<long long>((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "linear: %lld tiles", tiles);
+    hipLaunchKernelGGL(linear_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+                       rt->stream, g);
     int s = vk::check_launch("linear_kernel");
     if (s != VK_OK) {
       vk_tensor_destroy(t);
@@ -807,8 +826,10 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t
     a.mean[c] = mean[c];
     a.sd[c] = std_[c];
   }
-  dim3 grid((a.M + BM - 1) / BM, (a.N + BN - 1) / BN);
-  hipLaunchKernelGGL(patch_embed_kernel, grid, dim3(kPeThreads), 0, rt->stream, a);
+  const long long tiles = static_cast<long long>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "patch_embed_u8: %lld tiles", tiles);
+  hipLaunchKernelGGL(patch_embed_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kPeThreads), 0,
+                     rt->stream, a);
   return vk::check_launch("patch_embed_kernel");
 }
 
