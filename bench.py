@@ -344,6 +344,9 @@ def main():
                                      "patch_embed"],
                     help="profile mode: launch only this operation (12-view shape, rotating "
                          "buffers) after one calibration device copy of 256 MiB")
+    ap.add_argument("--sweep", type=str, default=None, metavar="VIEWS",
+                    help="size-sweep mode: the per-operation table at each comma-separated "
+                         "view count (866 rows per view), one JSON line per size")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the fused per-token path runs on a single "
@@ -353,6 +356,17 @@ def main():
     import vestra_hip as vh
     rng = np.random.default_rng(SEED)
     rt = vh.Runtime(0)
+    if args.sweep:
+        # per-launch cost vs size: t(rows) ~ fixed ramp/drain + rows * per-row
+        # stream time; fewer rotating sets at large sizes keep memory bounded
+        for views in [int(v) for v in args.sweep.split(",")]:
+            rows = views * TPV
+            sets = ROTATE_SETS if views <= 12 else max(2, ROTATE_SETS * 12 // views)
+            table = per_op_table(rt, rng, rows, rotate=sets, iters=args.op_iters)
+            print(json.dumps({"views": views, "rows": rows, "rotate_sets": sets, "ops": table}),
+                  flush=True)
+            rt.synchronize()
+        return
     if args.op == "patch_embed":
         print(json.dumps({"op": "patch_embed",
                           **patch_embed_timing(rt, rng, 336, 504, D, args.op_iters)}), flush=True)
