@@ -235,6 +235,41 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
+def linear_epilogue_timing(rt, rng, rows, iters):
+    """The block's MLP projections at `rows` tokens with their per-token
+    epilogues fused (FC1 + bias + GELU; FC2 + bias + LayerScale + residual)
+    against the same linear followed by the separate stream kernel.  Times
+    are medians of graph replays; TFLOP/s counts 2*rows*K*N per linear."""
+    def n(*sh, scale=1.0):
+        return (scale * rng.standard_normal(sh)).astype(np.float32)
+
+    out = {"rows": rows}
+    x1, h = rt.upload_f32(n(rows, D)), rt.alloc_f32(rows * M)
+    fc1 = rt.prepare_linear_f32(D, M, n(D, M, scale=0.02), n(M, scale=0.02))
+    x2, res, y = rt.upload_f32(n(rows, M)), rt.upload_f32(n(rows, D)), rt.alloc_f32(rows * D)
+    fc2 = rt.prepare_linear_f32(M, D, n(M, D, scale=0.02), n(D, scale=0.02),
+                                rng.uniform(0, 0.1, D).astype(np.float32))
+    cases = {
+        "fc1_linear": (lambda: fc1.run_into(x1, rows, h), D),
+        "fc1_linear_then_gelu": (lambda: (fc1.run_into(x1, rows, h), rt.gelu_f32_in_place(h)), D),
+        "fc1_gelu_fused": (lambda: fc1.run_gelu(x1, rows, h), D),
+        "fc2_linear": (lambda: fc2.run_into(x2, rows, y), M),
+        "fc2_linear_then_residual": (lambda: (fc2.run_into(x2, rows, y),
+                                              rt.add_f32_in_place(res, y)), M),
+        "fc2_residual_fused": (lambda: fc2.run_residual(x2, rows, res), M),
+    }
+    for name, (fn, k) in cases.items():
+        fn()
+        graph = capture(rt, fn, iters)
+        graph.launch()
+        us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / iters
+                               for _ in range(OP_TRIALS))
+        flop = 2.0 * rows * k * (M if k == D else D)
+        out[name] = {"us": round(us, 2), "TFLOP_s": round(flop / us / 1e6, 2),
+                     "frac_of_f32_mfma_peak": round(flop / us / 1e6 / MFMA_F32_PEAK_TFLOPS, 4)}
+    return out
+
+
 def patch_embed_timing(rt, rng, h, w, embed, iters):
     """Fused patch embedding of one u8 image (normalise, unfold, F32-MFMA
     projection, bias, position add, special rows): time per image and the
@@ -344,6 +379,9 @@ def main():
                                      "patch_embed"],
                     help="profile mode: launch only this operation (12-view shape, rotating "
                          "buffers) after one calibration device copy of 256 MiB")
+    ap.add_argument("--linear", action="store_true",
+                    help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
+                         "at the 12-view shape")
     ap.add_argument("--sweep", type=str, default=None, metavar="VIEWS",
                     help="size-sweep mode: the per-operation table at each comma-separated "
                          "view count (866 rows per view), one JSON line per size")
@@ -366,6 +404,10 @@ def main():
             print(json.dumps({"views": views, "rows": rows, "rotate_sets": sets, "ops": table}),
                   flush=True)
             rt.synchronize()
+        return
+    if args.linear:
+        print(json.dumps({"linear_epilogues": linear_epilogue_timing(rt, rng, TPV * 12,
+                                                                     args.op_iters)}), flush=True)
         return
     if args.op == "patch_embed":
         print(json.dumps({"op": "patch_embed",

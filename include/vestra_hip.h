@@ -242,6 +242,30 @@ size_t vk_linear_input_features(const vk_linear* lin);
  * accumulation.  New tensor [rows, out]. */
 int vk_linear_run_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
                       size_t rows, vk_tensor** out);
+/* The same into a caller tensor out [rows, out] (no allocation; capturable
+ * in a HIP graph).  out must not overlap x. */
+int vk_linear_run_into_f32(vk_runtime* rt, const vk_linear* lin,
+                           const vk_tensor* x, size_t rows, vk_tensor* out);
+/* FC1 + GELU in one pass: out = GELU(x @ W + b), the erf of
+ * vk_gelu_f32_inplace (A&S 7.1.26), bit-identical to vk_linear_run_into_f32
+ * followed by vk_gelu_f32_inplace.  Replaces CudaLinearF32::run then
+ * CudaRuntime::gelu_f32_in_place (vit_block.rs:578, 642), the reference's own
+ * FC1-epilogue fusion on the CPU (docs/optimization-log.md:292).  The linear
+ * must carry no LayerScale. */
+int vk_linear_run_gelu_f32(vk_runtime* rt, const vk_linear* lin,
+                           const vk_tensor* x, size_t rows, vk_tensor* out);
+/* The same with the device erff (vk_gelu_erf_f32_inplace's GELU). */
+int vk_linear_run_gelu_erf_f32(vk_runtime* rt, const vk_linear* lin,
+                               const vk_tensor* x, size_t rows, vk_tensor* out);
+/* proj / FC2 + LayerScale + residual in one pass:
+ * residual += (x @ W + b) [* gamma], each step rounded as in the unfused
+ * sequence (bit-identical to vk_linear_run_into_f32 then vk_add_f32_inplace).
+ * Replaces CudaLinearF32::run with Some(ls) followed by
+ * CudaRuntime::add_f32_in_place (vit_block.rs:214-222, 303-313, 563-564, 580).
+ * residual [rows, out] must not overlap x. */
+int vk_linear_run_residual_f32(vk_runtime* rt, const vk_linear* lin,
+                               const vk_tensor* x, size_t rows,
+                               vk_tensor* residual);
 
 /* CudaRuntime::prepend_cls_add_pos_f32(patches, cls, pos, n_patches, embed)
  * (patch_embed.rs:234-240): row 0 = cls + pos[0]; row 1+p = patch_p + pos[1+p]. */

@@ -129,6 +129,83 @@ def test_linear_matches_oracle(rt, rng, m, k, n, with_ls):
     assert_dot_parity(out, ref, scale, k, f"linear {m}x{k}x{n}")
 
 
+# ---------------------------------------------------------------- fused linear epilogues
+@pytest.mark.parametrize("m,k,n", [(97, 192, 136), (48, 13, 8), (865, 768, 3072), (865, 3072, 768)])
+def test_linear_into_matches_run(rt, rng, m, k, n):
+    x = rt.upload_f32(normals(rng, m, k))
+    lin = rt.prepare_linear_f32(k, n, normals(rng, k, n, scale=0.02), normals(rng, n, scale=0.02))
+    out = rt.alloc_f32(m * n)
+    lin.run_into(x, m, out)
+    assert np.array_equal(out.numpy(), lin.run(x, m).numpy())
+
+
+@pytest.mark.parametrize("m,k,n", [(97, 192, 136), (48, 13, 8), (865, 768, 3072)])
+@pytest.mark.parametrize("exact_erf", [False, True])
+def test_linear_gelu_fused_is_the_unfused_sequence(rt, rng, m, k, n, exact_erf):
+    # FC1 + GELU (vit_block.rs:578,642): bit-identical to linear then the GELU
+    # stream on the GPU, and within the composed bound of the oracle
+    xh, w, b = normals(rng, m, k), normals(rng, k, n, scale=0.05), normals(rng, n, scale=0.02)
+    x = rt.upload_f32(xh)
+    lin = rt.prepare_linear_f32(k, n, w, b)
+    fused, plain = rt.alloc_f32(m * n), rt.alloc_f32(m * n)
+    lin.run_gelu(x, m, fused, exact_erf=exact_erf)
+    lin.run_into(x, m, plain)
+    (rt.gelu_erf_f32_in_place if exact_erf else rt.gelu_f32_in_place)(plain)
+    got = fused.numpy()
+    assert np.array_equal(got, plain.numpy())
+    if m * k * n <= 4_000_000:
+        pre = oracle.linear(xh, w, b)
+        ref = (oracle.gelu_erff if exact_erf else oracle.gelu)(pre)
+        scale = np.abs(xh).astype(np.float64) @ np.abs(w).astype(np.float64)
+        # |GELU'| <= 1.13: the dot-product bound carries through, then GELU's own
+        bound = (1.13 * (F32_ATOL + F32_RTOL * np.abs(pre) + 2 * np.sqrt(k) * 2.0 ** -24 * scale)
+                 + F32_ATOL + F32_RTOL * np.abs(ref))
+        err = np.abs(got.reshape(m, n).astype(np.float64) - ref)
+        assert np.all(err <= bound), float(np.max(err / bound))
+
+
+@pytest.mark.parametrize("m,k,n,with_ls", [(97, 192, 136, True), (48, 13, 8, False),
+                                           (865, 768, 768, True), (865, 3072, 768, True)])
+def test_linear_residual_fused_is_the_unfused_sequence(rt, rng, m, k, n, with_ls):
+    # proj/FC2 + LayerScale + residual (vit_block.rs:214-222,563-564,580)
+    xh, w, b = normals(rng, m, k), normals(rng, k, n, scale=0.02), normals(rng, n, scale=0.02)
+    ls = rng.uniform(0, 0.1, n).astype(np.float32) if with_ls else None
+    res = normals(rng, m, n)
+    x = rt.upload_f32(xh)
+    lin = rt.prepare_linear_f32(k, n, w, b, ls)
+    fused = rt.upload_f32(res)
+    lin.run_residual(x, m, fused)
+    plain, y = rt.upload_f32(res), rt.alloc_f32(m * n)
+    lin.run_into(x, m, y)
+    rt.add_f32_in_place(plain, y)
+    got = fused.numpy()
+    assert np.array_equal(got, plain.numpy())
+    if m * k * n <= 4_000_000:
+        t = oracle.linear(xh, w, b)
+        if with_ls:
+            t = oracle.layerscale(t, ls)
+        ref = oracle.add(res, t)
+        scale = np.abs(xh).astype(np.float64) @ np.abs(w).astype(np.float64)
+        if with_ls:
+            scale = scale * ls
+        assert_dot_parity(got, ref, scale, k, f"linear+residual {m}x{k}x{n}")
+
+
+def test_linear_fused_entry_points_reject_bad_arguments(rt, rng):
+    x = rt.upload_f32(normals(rng, 4, 8))
+    with_ls = rt.prepare_linear_f32(8, 4, normals(rng, 8, 4), normals(rng, 4),
+                                    rng.uniform(0, 0.1, 4).astype(np.float32))
+    with pytest.raises(vh.VestraError):
+        with_ls.run_gelu(x, 4, rt.alloc_f32(16))      # GELU after a LayerScale: not a reference op
+    plain = rt.prepare_linear_f32(8, 8, normals(rng, 8, 8), normals(rng, 8))
+    with pytest.raises(vh.VestraError):
+        plain.run_residual(x, 4, x)                   # residual overlapping the input
+    with pytest.raises(vh.VestraError):
+        plain.run_into(x, 4, rt.alloc_f32(31))        # wrong output size
+    empty = rt.alloc_f32(0)
+    plain.run_into(rt.alloc_f32(0), 0, empty)         # zero rows: nothing launched
+
+
 def test_pos_embed_bicubic_bit_exact(rt, rng):
     M, E = 37, 768
     pe = normals(rng, M * M + 1, E, scale=0.02)

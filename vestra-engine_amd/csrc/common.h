@@ -79,6 +79,31 @@ int check_launch(const char* what);
 int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
                int* table_max);
 
+// F32 linear out[m, n] = epilogue(sum_k x[m, k] W[n, k] + b[n]).
+struct LinearArgs {
+  const float* x;     // [M, K]
+  const float* wnk;   // [N, Kp], K contiguous, zero beyond K
+  const float* bias;  // [N]
+  const float* ls;    // [N] or null
+  float* out;         // [M, N]
+  int M, N, K, Kp;
+};
+
+// Epilogues of the linear: v = acc + b (then * ls when the linear has one),
+// each rounding as in the unfused sequence, so a fused call gives the same
+// bits as the linear followed by the separate stream kernel.
+namespace linear_epilogue {
+enum LinearEpilogue {
+  kLinStore = 0,     // out = v
+  kLinGelu = 1,      // out = GELU(v), A&S erf (the GELU stream's function)
+  kLinGeluErf = 2,   // out = GELU(v), device erff
+  kLinResidual = 3,  // out += v (out is the residual stream)
+};
+}  // namespace linear_epilogue
+
+// The 128x128-tile linear for K % 4 == 0 and a 16-byte aligned x (linear.hip).
+int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi);
+
 }  // namespace vk
 
 #define VK_REQUIRE(cond, ...)                              \
@@ -194,6 +219,45 @@ __device__ __forceinline__ void st_stream(float4* p, float4 v) {
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on
+// XCD i % 8), and each XCD has its own L2.  Renumber so that an XCD's
+// workgroups are consecutive tiles t of an N-major order (t -> m = t % gm,
+// n = t / gm): they then share the same few weight columns in that L2.
+// Bijective for any tile count n: XCD x holds n/8 tiles, one more if
+// x < n % 8.
+__device__ __forceinline__ int xcd_tile(int lin, int n) {
+  const int q = n / 8, r = n % 8;
+  const int xcd = lin % 8, slot = lin / 8;
+  return slot + (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q);
+}
+
+// Abramowitz & Stegun 7.1.26 erf (|error| < 1.5e-7): the erf of the
+// reference's scalar GELU (docs/plans/2026-07-18-rust-engine-v1.md:870-876),
+// with the same operation order: t = 1/(1 + p*a);
+// y = 1 - ((((a5*t + a4)*t + a3)*t + a2)*t + a1)*t * exp(-a*a); erf = sign*y.
+// Shared by the GELU stream and the linear's GELU epilogue, so both give the
+// same bits.
+__device__ __forceinline__ float erf_as7126(float x) {
+  const float s = __builtin_signbit(x) ? -1.0f : 1.0f;
+  const float a = fabsf(x);
+  const float t = 1.0f / (1.0f + 0.3275911f * a);
+  float p = 1.0614054f * t - 1.4531520f;
+  p = p * t;
+  p = p + 1.4214137f;
+  p = p * t - 0.28449674f;
+  p = p * t + 0.25482959f;
+  const float y = 1.0f - p * t * expf(-a * a);
+  return s * y;
+}
+
+// GELU(v) = 0.5 v (1 + erf(v / sqrt 2)); MODE 0: A&S erf, 1: device erff.
+template <int MODE>
+__device__ __forceinline__ float gelu1(float v) {
+  const float inv_sqrt2 = 0.70710678f;
+  const float e = (MODE == 0) ? erf_as7126(v * inv_sqrt2) : erff(v * inv_sqrt2);
+  return 0.5f * v * (1.0f + e);
 }
 
 // Parameter vector element loads (f32 or binary16 storage).

@@ -14,30 +14,7 @@
 namespace {
 
 using vkd::Param;
-
-// Abramowitz & Stegun 7.1.26 erf (|error| < 1.5e-7): the erf of the
-// reference's scalar GELU (docs/plans/2026-07-18-rust-engine-v1.md:870-876),
-// with the same operation order: t = 1/(1 + p*a);
-// y = 1 - ((((a5*t + a4)*t + a3)*t + a2)*t + a1)*t * exp(-a*a); erf = sign*y.
-__device__ __forceinline__ float erf_as7126(float x) {
-  const float s = __builtin_signbit(x) ? -1.0f : 1.0f;
-  const float a = fabsf(x);
-  const float t = 1.0f / (1.0f + 0.3275911f * a);
-  float p = 1.0614054f * t - 1.4531520f;
-  p = p * t;
-  p = p + 1.4214137f;
-  p = p * t - 0.28449674f;
-  p = p * t + 0.25482959f;
-  const float y = 1.0f - p * t * expf(-a * a);
-  return s * y;
-}
-
-template <int MODE>
-__device__ __forceinline__ float gelu1(float v) {
-  const float inv_sqrt2 = 0.70710678f;
-  const float e = (MODE == 0) ? erf_as7126(v * inv_sqrt2) : erff(v * inv_sqrt2);
-  return 0.5f * v * (1.0f + e);
-}
+using vkd::gelu1;
 
 // One float4 per thread per iteration over a large grid (up to 64
 // workgroups per CU): on MI355X more resident waves beat more loads per

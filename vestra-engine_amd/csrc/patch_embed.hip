@@ -34,6 +34,10 @@
 
 namespace {
 
+using vk::LinearArgs;
+using vkd::xcd_tile;
+using namespace vk::linear_epilogue;
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 48;
@@ -41,18 +45,6 @@ constexpr int BN = 64;
 constexpr int kThreads = 512;
 constexpr int kPatch = 14;
 constexpr int kKAlign = 16;  // weight rows are zero-padded to a 16-block
-
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on
-// XCD i % 8), and each XCD has its own L2.  Renumber so that an XCD's
-// workgroups are consecutive tiles t of an N-major order (t -> m = t % gm,
-// n = t / gm): they then share the same few filter columns in that L2.
-// Bijective for any tile count n: XCD x holds n/8 tiles, one more if
-// x < n % 8.
-__device__ __forceinline__ int xcd_tile(int lin, int n) {
-  const int q = n / 8, r = n % 8;
-  const int xcd = lin % 8, slot = lin / 8;
-  return slot + (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q);
-}
 
 __device__ __forceinline__ void mfma_block(const float* arow, int t_pitch, const f32x4& b,
                                            f32x4 acc[3]) {
@@ -98,15 +90,6 @@ constexpr int kA_PER_THREAD = (KC * BM + kThreads - 1) / kThreads;        // 18
 constexpr int kB_VEC_PER_THREAD = (KC * BN / 4 + kThreads - 1) / kThreads;  // 6
 static_assert(kLinPitch % 4 == 0 && (kLinPitch / 4) % 2 == 1, "pitch must be 4 x odd");
 static_assert(KC * BM % kThreads == 0 && KC * BN / 4 % kThreads == 0, "slots divide evenly");
-
-struct LinearArgs {
-  const float* x;     // [M, K]
-  const float* wnk;   // [N, Kp], K contiguous, zero beyond K
-  const float* bias;  // [N]
-  const float* ls;    // [N] or null
-  float* out;         // [M, N]
-  int M, N, K, Kp;
-};
 
 // The loaders never branch around a global load: a load inside a guard
 // makes the compiler wait for it before the next one, serialising the memory
@@ -161,6 +144,7 @@ struct LinearStage {
   }
 };
 
+template <int EPI>
 __global__ __launch_bounds__(kThreads) void linear_kernel(LinearArgs g) {
   __shared__ __align__(16) float As[BM * kLinPitch];
   __shared__ __align__(16) float Bs[BN * kLinPitch];
@@ -210,7 +194,11 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearArgs g) {
       if (row < g.M) {
         float v = acc[t][r] + bias;
         if (g.ls) v = v * ls;
-        g.out[static_cast<size_t>(row) * g.N + col] = v;
+        float* o = g.out + static_cast<size_t>(row) * g.N + col;
+        if (EPI == kLinStore) *o = v;
+        if (EPI == kLinGelu) *o = vkd::gelu1<0>(v);
+        if (EPI == kLinGeluErf) *o = vkd::gelu1<1>(v);
+        if (EPI == kLinResidual) *o = *o + v;
       }
     }
 }
@@ -609,6 +597,59 @@ int make_linear(vk_runtime* rt, size_t in, size_t out, const std::vector<float>&
   return VK_OK;
 }
 
+int check_linear(const vk_linear* lin, const vk_tensor* x, size_t rows) {
+  VK_REQUIRE(x->dtype == VK_F32, "linear input must be f32");
+  VK_REQUIRE(x->len == rows * lin->in_features, "linear: x holds %zu, rows*in=%zu", x->len,
+             rows * lin->in_features);
+  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "linear: rows=%zu too large", rows);
+  const long long tiles = static_cast<long long>((rows + BM - 1) / BM) *
+                          static_cast<long long>((lin->out_features + BN - 1) / BN);
+  VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "linear: %lld tiles", tiles);
+  return VK_OK;
+}
+
+// Output (or residual) checks; it must not overlap the input, which other
+// workgroups may still be reading while one writes.
+int check_linear_out(const vk_linear* lin, const vk_tensor* x, const vk_tensor* out, size_t rows,
+                     const char* what) {
+  VK_REQUIRE(out->dtype == VK_F32 && out->len == rows * lin->out_features,
+             "linear: %s must be f32 [rows*out=%zu] (holds %zu)", what, rows * lin->out_features,
+             out->len);
+  const char* xb = static_cast<const char*>(x->ptr);
+  const char* ob = static_cast<const char*>(out->ptr);
+  VK_REQUIRE(ob + out->len * 4 <= xb || xb + x->len * 4 <= ob || rows == 0,
+             "linear: %s overlaps the input", what);
+  return VK_OK;
+}
+
+int launch_linear(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
+                  vk_tensor* out, int epi) {
+  if (rows == 0) return VK_OK;
+  LinearArgs g{};
+  g.x = static_cast<const float*>(x->ptr);
+  g.wnk = lin->weight_nk;
+  g.bias = lin->bias;
+  g.ls = lin->ls_gamma;
+  g.out = static_cast<float*>(out->ptr);
+  g.M = static_cast<int>(rows);
+  g.N = static_cast<int>(lin->out_features);
+  g.K = static_cast<int>(lin->in_features);
+  g.Kp = static_cast<int>(lin->k_pitch);
+  // 128x128 tiles wherever rows of x can be read as float4; the 48x64 kernel
+  // (scalar loads of x) for the rest
+  if (g.K % 4 == 0 && reinterpret_cast<uintptr_t>(g.x) % 16 == 0)
+    return vk::launch_linear_wide(rt, g, epi);
+  const unsigned tiles = static_cast<unsigned>(((g.M + BM - 1) / BM) * static_cast<long long>((g.N + BN - 1) / BN));
+  const dim3 grid(tiles), block(kThreads);
+  switch (epi) {
+    case kLinStore: hipLaunchKernelGGL(linear_kernel<kLinStore>, grid, block, 0, rt->stream, g); break;
+    case kLinGelu: hipLaunchKernelGGL(linear_kernel<kLinGelu>, grid, block, 0, rt->stream, g); break;
+    case kLinGeluErf: hipLaunchKernelGGL(linear_kernel<kLinGeluErf>, grid, block, 0, rt->stream, g); break;
+    default: hipLaunchKernelGGL(linear_kernel<kLinResidual>, grid, block, 0, rt->stream, g); break;
+  }
+  return vk::check_launch("linear_kernel");
+}
+
 }  // namespace
 
 extern "C" {
@@ -662,35 +703,54 @@ int vk_linear_run_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, 
                       vk_tensor** out) {
   VK_TRY(vk::bind(rt));
   VK_REQUIRE(lin && x && out, "null argument");
-  VK_REQUIRE(x->dtype == VK_F32, "linear input must be f32");
-  VK_REQUIRE(x->len == rows * lin->in_features, "linear: x holds %zu, rows*in=%zu", x->len,
-             rows * lin->in_features);
-  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "linear: rows=%zu too large", rows);
+  VK_TRY(check_linear(lin, x, rows));
   vk_tensor* t = nullptr;
   VK_TRY(vk_tensor_alloc(rt, VK_F32, rows * lin->out_features, &t));
-  if (rows > 0) {
-    LinearArgs g{};
-    g.x = static_cast<const float*>(x->ptr);
-    g.wnk = lin->weight_nk;
-    g.bias = lin->bias;
-    g.ls = lin->ls_gamma;
-    g.out = static_cast<float*>(t->ptr);
-    g.M = static_cast<int>(rows);
-    g.N = static_cast<int>(lin->out_features);
-    g.K = static_cast<int>(lin->in_features);
-    g.Kp = static_cast<int>(lin->k_pitch);
-    const long long tiles = static_cast<long long>((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "linear: %lld tiles", tiles);
-    hipLaunchKernelGGL(linear_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
-                       rt->stream, g);
-    int s = vk::check_launch("linear_kernel");
-    if (s != VK_OK) {
-      vk_tensor_destroy(t);
-      return s;
-    }
+  const int s = launch_linear(rt, lin, x, rows, t, kLinStore);
+  if (s != VK_OK) {
+    vk_tensor_destroy(t);
+    return s;
   }
   *out = t;
   return VK_OK;
+}
+
+int vk_linear_run_into_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
+                           vk_tensor* out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && out, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
+  return launch_linear(rt, lin, x, rows, out, kLinStore);
+}
+
+int vk_linear_run_gelu_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
+                           vk_tensor* out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && out, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
+  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_gelu: the linear carries a LayerScale");
+  return launch_linear(rt, lin, x, rows, out, kLinGelu);
+}
+
+int vk_linear_run_gelu_erf_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                               size_t rows, vk_tensor* out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && out, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
+  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_gelu_erf: the linear carries a LayerScale");
+  return launch_linear(rt, lin, x, rows, out, kLinGeluErf);
+}
+
+int vk_linear_run_residual_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                               size_t rows, vk_tensor* residual) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && residual, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_linear_out(lin, x, residual, rows, "residual"));
+  return launch_linear(rt, lin, x, rows, residual, kLinResidual);
 }
 
 int vk_patchify_nchw_f32(vk_runtime* rt, const vk_tensor* img, size_t h, size_t w,

@@ -128,6 +128,10 @@ _SIGS = {
     "vk_linear_destroy": ([_vp], _i),
     "vk_linear_input_features": ([_vp], _sz),
     "vk_linear_run_f32": ([_vp, _vp, _vp, _sz, _pp], _i),
+    "vk_linear_run_into_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
+    "vk_linear_run_gelu_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
+    "vk_linear_run_gelu_erf_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
+    "vk_linear_run_residual_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
     "vk_pos_embed_bicubic_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _f, _pp], _i),
     "vk_patch_embed_u8": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp], _i),
@@ -223,6 +227,19 @@ class Linear:
         out = C.c_void_p()
         _check(lib.vk_linear_run_f32(self.rt.handle, self.handle, x.handle, rows, C.byref(out)))
         return Tensor(self.rt, out)
+
+    def run_into(self, x: Tensor, rows: int, out: Tensor) -> None:
+        _check(lib.vk_linear_run_into_f32(self.rt.handle, self.handle, x.handle, rows, out.handle))
+
+    def run_gelu(self, x: Tensor, rows: int, out: Tensor, exact_erf: bool = False) -> None:
+        """FC1 + GELU: out = GELU(x W + b); A&S erf, or the device erff."""
+        fn = lib.vk_linear_run_gelu_erf_f32 if exact_erf else lib.vk_linear_run_gelu_f32
+        _check(fn(self.rt.handle, self.handle, x.handle, rows, out.handle))
+
+    def run_residual(self, x: Tensor, rows: int, residual: Tensor) -> None:
+        """proj / FC2 + LayerScale + residual: residual += (x W + b) [* gamma]."""
+        _check(lib.vk_linear_run_residual_f32(self.rt.handle, self.handle, x.handle, rows,
+                                              residual.handle))
 
     def __del__(self):
         try:
