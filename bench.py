@@ -459,6 +459,8 @@ def main():
     patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
              patch_embed_timing(rt, rng, 672, 1008, 1024, args.op_iters)]
     gelu = ops12["gelu"]
+    log("fused linear epilogues")
+    linear = linear_epilogue_timing(rt, rng, model.rows, 10)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -490,6 +492,7 @@ def main():
         "ops_12view": ops12,
         "ops_single_image": ops1,
         "patch_embed": patch,
+        "linear_epilogues": linear,
         "roofline": {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
                      "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
