@@ -28,6 +28,7 @@
 // the 16 rows of a fragment read start on 16 distinct 4-bank groups: no bank
 // conflicts.
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -214,9 +215,9 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearArgs g) {
 // The workgroup has 12 waves: waves 0-7 run the MFMAs (two per SIMD, as the
 // linear), waves 8-11 only stage.  Staging overlaps the MFMAs: pixel rows ky
 // 0-7 of every patch (k < 336 = 21 blocks) are normalised into LDS first;
-// then the compute waves run those blocks (waves 0-3 blocks 0-10, waves 4-7
+// then the compute waves run those blocks (waves 0-3 blocks 0-9, waves 4-7
 // blocks 11-20) while the staging waves normalise rows ky 8-13; one barrier
-// later waves 0-3 run blocks 21-28 and waves 4-7 blocks 29-36.
+// later waves 0-3 run blocks 21-28 and then 10, waves 4-7 blocks 29-36.
 // ---------------------------------------------------------------------------
 constexpr int kPeRowBytes = 3 * kPatch;    // 42 bytes per patch row
 constexpr int kPeK = kPatch * kPeRowBytes; // 588
@@ -226,9 +227,9 @@ constexpr int kPeSplitKy = 8;              // first stage: ky < 8
 constexpr int kPeBlocksA = kPeSplitKy * kPeRowBytes / 16;  // 21 blocks in the first stage
 constexpr int kPeRowsA = kPeSplitKy * BM;                  // 384 patch rows
 constexpr int kPeRowsB = (kPatch - kPeSplitKy) * BM;       // 288 patch rows
-constexpr int kPePhase1 = kPeBlocksA / 2 + 1;              // 11 for waves 0-3, 10 for 4-7
-constexpr int kPePhase2 = (kPeBlocks - kPeBlocksA) / 2;    // 8
-constexpr int kPeSeq = kPePhase1 + kPePhase2;              // 19 blocks of waves 0-3
+constexpr int kPePhase1 = kPeBlocksA / 2;                  // 10 per wave
+constexpr int kPePhase2 = (kPeBlocks - kPeBlocksA) / 2;    // 8 per wave
+constexpr int kPeSeq = kPePhase1 + kPePhase2 + 1;          // + waves 0-3's stage-A block 10
 constexpr int kPeAhead = 8;                // B prefetch distance in blocks
 constexpr int kPePitch = 596;              // A row pitch in LDS: 4 x 149
 constexpr int kPeStagers = 256;            // waves 8-11
@@ -238,7 +239,7 @@ static_assert(kPeKp % 16 == 0 && kPeKp >= kPeK && kPeKp == (kPeK + kKAlign - 1) 
 static_assert(kPeSplitKy * kPeRowBytes % 16 == 0, "stage boundary on a block boundary");
 static_assert(BM == 48 && kPatch % 2 == 0 && kPeSplitKy % 2 == 0,
               "patch-row groups of 16 patches x 2 pixel rows");
-static_assert(kPeBlocksA == 2 * kPePhase1 - 1 && kPeBlocks - kPeBlocksA == 2 * kPePhase2,
+static_assert(kPeBlocksA == 2 * kPePhase1 + 1 && kPeBlocks - kPeBlocksA == 2 * kPePhase2,
               "block split");
 static_assert(kPeRowsA <= kThreads && kPeRowsA % 64 == 0 && kPeRowsB > kPeStagers &&
                   kPeRowsB <= 2 * kPeStagers && 3 * 256 == kPeThreads,
@@ -358,11 +359,14 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
 
   // 2. B fragments (compute waves).  Block sequence: waves 0-3 run blocks
   // 0-10 then 21-28, waves 4-7 blocks 11-20 then 29-36.
+  // Positions 0-9 run in phase 1 and 10-17 in phase 2 in both halves, so
+  // their code (and the B loads in it) is the same for every wave; waves 0-3
+  // run their 19th block, stage-A block 10, last.
+  const int first1 = half ? kPePhase1 + 1 : 0;
+  const int first2 = kPeBlocksA + half * kPePhase2;
   auto seq_block = [&](int s) {
-    const int b = half ? (s < kPePhase1 - 1 ? kPePhase1 + s
-                                            : kPeBlocksA + kPePhase2 + s - (kPePhase1 - 1))
-                       : (s < kPePhase1 ? s : kPeBlocksA + s - kPePhase1);
-    return b < kPeBlocks ? b : kPeBlocks - 1;
+    return s < kPePhase1 ? first1 + s
+                         : (s < kPePhase1 + kPePhase2 ? first2 + s - kPePhase1 : kPePhase1);
   };
   const int col = n0 + strip * 16 + (lane & 15);
   const int ccol = col < p.N ? col : p.N - 1;
@@ -399,7 +403,40 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
 #pragma unroll
   for (int t = 0; t < 3; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float* arow = As + (lane & 15) * kPePitch + 4 * (lane >> 4);
-  auto block = [&](int s) { mfma_block(arow + 16 * seq_block(s), 16 * kPePitch, bf[s], acc); };
+  // A fragments run two blocks ahead of their MFMAs and B eight; the
+  // scheduling barrier keeps each block's prefetch loads where they are
+  // written (the scheduler otherwise sinks them next to their use)
+  struct AFrag {
+    f32x4 a[3];
+  };
+  auto load_a = [&](int s, AFrag& f) {
+    const float* q = arow + 16 * seq_block(s);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) f.a[t] = *reinterpret_cast<const f32x4*>(q + t * 16 * kPePitch);
+  };
+  auto mma = [&](const AFrag& f, const f32x4& b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[t][j], b[j], acc[t], 0, 0, 0);
+  };
+  // positions s0 <= s < s1 of the sequence
+  auto run_blocks = [&](auto s0c, auto s1c) {
+    constexpr int s0 = decltype(s0c)::value, s1 = decltype(s1c)::value;
+    AFrag f0, f1, f2;
+    load_a(s0, f0);
+    if (s0 + 1 < s1) load_a(s0 + 1, f1);
+#pragma unroll
+    for (int s = s0; s < s1; ++s) {
+      if (s + 2 < s1) load_a(s + 2, f2);
+      load_b(s + kPeAhead);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f0, bf[s]);
+      f0 = f1;
+      f1 = f2;
+    }
+  };
   if (stager) {
     row_b0.align();
     row_b0.store(row_dst(rb0), lut, 0, kPeRowBytes / 2);
@@ -407,18 +444,8 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
       row_b1.align();
       row_b1.store(row_dst(rb1), lut, 0, kPeRowBytes / 2);
     }
-  } else if (half == 0) {
-#pragma unroll
-    for (int s = 0; s < kPePhase1; ++s) {
-      load_b(s + kPeAhead);
-      block(s);
-    }
   } else {
-#pragma unroll
-    for (int s = 0; s < kPePhase1 - 1; ++s) {
-      load_b(s + kPeAhead);
-      block(s);
-    }
+    run_blocks(std::integral_constant<int, 0>{}, std::integral_constant<int, kPePhase1>{});
   }
   __syncthreads();
   if (stager) {
@@ -441,13 +468,13 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
       }
   }
 
-  // 7. phase 2: stage-B blocks
+  // 7. phase 2: stage-B blocks, then waves 0-3's last block
+  run_blocks(std::integral_constant<int, kPePhase1>{},
+             std::integral_constant<int, kPePhase1 + kPePhase2>{});
   if (half == 0) {
-#pragma unroll
-    for (int s = kPePhase1; s < kPeSeq; ++s) block(s);
-  } else {
-#pragma unroll
-    for (int s = kPePhase1 - 1; s < kPeSeq - 1; ++s) block(s);
+    AFrag f;
+    load_a(kPeSeq - 1, f);
+    mma(f, bf[kPeSeq - 1]);
   }
 
   if (!reduce_halves(red, strip, half, lane, acc)) return;
