@@ -236,9 +236,11 @@ MFMA_F32_PEAK_TFLOPS = 157.3
 
 
 def linear_epilogue_timing(rt, rng, rows, iters):
-    """The block's MLP projections at `rows` tokens with their per-token
-    epilogues fused (FC1 + bias + GELU; FC2 + bias + LayerScale + residual)
-    against the same linear followed by the separate stream kernel.  Times
+    """The block's projections at `rows` tokens with their per-token
+    epilogues and layout glue fused (FC1 + bias + GELU; FC2 + bias +
+    LayerScale + residual; QKV storing head-major Q, K, V; the output
+    projection reading the head-major attention output) against the same
+    linear plus the separate stream or permutation kernel.  Times
     are medians of graph replays; TFLOP/s counts 2*rows*K*N per linear."""
     def n(*sh, scale=1.0):
         return (scale * rng.standard_normal(sh)).astype(np.float32)
@@ -249,22 +251,37 @@ def linear_epilogue_timing(rt, rng, rows, iters):
     x2, res, y = rt.upload_f32(n(rows, M)), rt.upload_f32(n(rows, D)), rt.alloc_f32(rows * D)
     fc2 = rt.prepare_linear_f32(M, D, n(M, D, scale=0.02), n(D, scale=0.02),
                                 rng.uniform(0, 0.1, D).astype(np.float32))
+    xq = rt.upload_f32(n(rows, D))
+    qkv = rt.prepare_linear_f32(D, 3 * D, n(D, 3 * D, scale=0.02), n(3 * D, scale=0.02))
+    qkv_out = rt.alloc_f32(rows * 3 * D)
+    q, k, v = (rt.alloc_f32(rows * D) for _ in range(3))
+    hnd, tok = rt.upload_f32(n(H, rows, HD)), rt.alloc_f32(rows * D)
+    proj = rt.prepare_linear_f32(D, D, n(D, D, scale=0.02), n(D, scale=0.02),
+                                 rng.uniform(0, 0.1, D).astype(np.float32))
     cases = {
-        "fc1_linear": (lambda: fc1.run_into(x1, rows, h), D),
-        "fc1_linear_then_gelu": (lambda: (fc1.run_into(x1, rows, h), rt.gelu_f32_in_place(h)), D),
-        "fc1_gelu_fused": (lambda: fc1.run_gelu(x1, rows, h), D),
-        "fc2_linear": (lambda: fc2.run_into(x2, rows, y), M),
+        "fc1_linear": (lambda: fc1.run_into(x1, rows, h), D, M),
+        "fc1_linear_then_gelu": (lambda: (fc1.run_into(x1, rows, h), rt.gelu_f32_in_place(h)),
+                                 D, M),
+        "fc1_gelu_fused": (lambda: fc1.run_gelu(x1, rows, h), D, M),
+        "fc2_linear": (lambda: fc2.run_into(x2, rows, y), M, D),
         "fc2_linear_then_residual": (lambda: (fc2.run_into(x2, rows, y),
-                                              rt.add_f32_in_place(res, y)), M),
-        "fc2_residual_fused": (lambda: fc2.run_residual(x2, rows, res), M),
+                                              rt.add_f32_in_place(res, y)), M, D),
+        "fc2_residual_fused": (lambda: fc2.run_residual(x2, rows, res), M, D),
+        "qkv_linear_then_split": (lambda: (qkv.run_into(xq, rows, qkv_out),
+                                           rt.split_qkv_hnd_into_f32(qkv_out, rows, H, HD, q, k,
+                                                                     v)), D, 3 * D),
+        "qkv_hnd_fused": (lambda: qkv.run_qkv_hnd(xq, rows, H, q, k, v), D, 3 * D),
+        "proj_token_then_residual": (lambda: (rt.hnd_to_token_into_f32(hnd, rows, H, HD, tok),
+                                              proj.run_residual(tok, rows, res)), D, D),
+        "proj_hnd_residual_fused": (lambda: proj.run_hnd_residual(hnd, rows, H, res), D, D),
     }
-    for name, (fn, k) in cases.items():
+    for name, (fn, k_dim, n_dim) in cases.items():
         fn()
         graph = capture(rt, fn, iters)
         graph.launch()
         us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / iters
                                for _ in range(OP_TRIALS))
-        flop = 2.0 * rows * k * (M if k == D else D)
+        flop = 2.0 * rows * k_dim * n_dim
         out[name] = {"us": round(us, 2), "TFLOP_s": round(flop / us / 1e6, 2),
                      "frac_of_f32_mfma_peak": round(flop / us / 1e6 / MFMA_F32_PEAK_TFLOPS, 4)}
     return out

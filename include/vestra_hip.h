@@ -267,6 +267,51 @@ int vk_linear_run_residual_f32(vk_runtime* rt, const vk_linear* lin,
                                const vk_tensor* x, size_t rows,
                                vk_tensor* residual);
 
+/* ------------------------------------------------------------------ */
+/* attention-block layout glue (head_dim contiguous, head-major)        */
+/* ------------------------------------------------------------------ */
+
+/* CudaRuntime::split_qkv_hnd_f32(qkv, rows, heads, head_dim)
+ * (vit_block.rs:539-541): token-major QKV [rows, 3*heads*head_dim], columns
+ * Q | K | V each [heads, head_dim] (vit_block.rs:38-43), to head-major Q, K,
+ * V [heads, rows, head_dim] (the pack loop of vit_block.rs:818-833).
+ * head_dim % 4 == 0.  New tensors / caller tensors (no overlap). */
+int vk_split_qkv_hnd_f32(vk_runtime* rt, const vk_tensor* qkv, size_t rows,
+                         size_t heads, size_t head_dim, vk_tensor** q,
+                         vk_tensor** k, vk_tensor** v);
+int vk_split_qkv_hnd_into_f32(vk_runtime* rt, const vk_tensor* qkv,
+                              size_t rows, size_t heads, size_t head_dim,
+                              vk_tensor* q, vk_tensor* k, vk_tensor* v);
+/* CudaRuntime::hnd_to_token_f32(hnd, rows, heads, head_dim)
+ * (vit_block.rs:560): head-major [heads, rows, head_dim] to token-major
+ * [rows, heads*head_dim]. */
+int vk_hnd_to_token_f32(vk_runtime* rt, const vk_tensor* hnd, size_t rows,
+                        size_t heads, size_t head_dim, vk_tensor** out);
+int vk_hnd_to_token_into_f32(vk_runtime* rt, const vk_tensor* hnd,
+                             size_t rows, size_t heads, size_t head_dim,
+                             vk_tensor* out);
+/* The QKV projection storing head-major Q, K, V directly: bit-identical to
+ * vk_linear_run_into_f32 followed by vk_split_qkv_hnd_into_f32.  The device
+ * form of vestra_kernels::qkv_f32_da3_base (vit_block.rs:813-814), replacing
+ * CudaLinearF32::run + split_qkv_hnd_f32 (vit_block.rs:538-541).
+ * head_dim 64, out_features = 3*heads*64, no LayerScale. */
+int vk_linear_run_qkv_hnd_f32(vk_runtime* rt, const vk_linear* lin,
+                              const vk_tensor* x, size_t rows, size_t heads,
+                              size_t head_dim, vk_tensor* q, vk_tensor* k,
+                              vk_tensor* v);
+/* The output projection reading the head-major attention output
+ * [heads, rows, 64] directly (in_features = heads*64): bit-identical to
+ * vk_hnd_to_token_into_f32 followed by vk_linear_run_into_f32 /
+ * vk_linear_run_residual_f32.  Replaces hnd_to_token_f32 + projection run
+ * (+ add_f32_in_place) (vit_block.rs:560-563). */
+int vk_linear_run_hnd_into_f32(vk_runtime* rt, const vk_linear* lin,
+                               const vk_tensor* hnd, size_t rows, size_t heads,
+                               size_t head_dim, vk_tensor* out);
+int vk_linear_run_hnd_residual_f32(vk_runtime* rt, const vk_linear* lin,
+                                   const vk_tensor* hnd, size_t rows,
+                                   size_t heads, size_t head_dim,
+                                   vk_tensor* residual);
+
 /* CudaRuntime::prepend_cls_add_pos_f32(patches, cls, pos, n_patches, embed)
  * (patch_embed.rs:234-240): row 0 = cls + pos[0]; row 1+p = patch_p + pos[1+p]. */
 int vk_prepend_cls_add_pos_f32(vk_runtime* rt, const vk_tensor* patches,

@@ -61,6 +61,8 @@ _SIGS = {
     "ora_patch_embed_u8": ([_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _sz, _vp,
                             _vp], None),
     "ora_overwrite_prefix_f32": ([_vp, _vp, _sz], None),
+    "ora_split_qkv_hnd": ([_vp, _sz, _sz, _sz, _vp, _vp, _vp], None),
+    "ora_hnd_to_token": ([_vp, _sz, _sz, _sz, _vp], None),
 }
 for _n, (_a, _r) in _SIGS.items():
     _fn = getattr(lib, _n)
@@ -233,6 +235,21 @@ def pos_embed_bicubic(pos_embed, grid: int, embed: int, gh: int, gw: int,
     src = _f32(pos_embed)
     out = np.empty((1 + gh * gw, embed), np.float32)
     lib.ora_pos_embed_bicubic(_p(src), grid, embed, gh, gw, interp_offset, _p(out))
+    return out
+
+
+def split_qkv_hnd(qkv, n: int, heads: int, head_dim: int):
+    """Token-major QKV [n, 3*heads*head_dim] -> head-major Q, K, V [heads, n, head_dim]."""
+    a = _f32(qkv)
+    q, k, v = (np.empty((heads, n, head_dim), np.float32) for _ in range(3))
+    lib.ora_split_qkv_hnd(_p(a), n, heads, head_dim, _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def hnd_to_token(hnd, n: int, heads: int, head_dim: int) -> np.ndarray:
+    """Head-major [heads, n, head_dim] -> token-major [n, heads*head_dim]."""
+    out = np.empty((n, heads * head_dim), np.float32)
+    lib.ora_hnd_to_token(_p(_f32(hnd)), n, heads, head_dim, _p(out))
     return out
 
 

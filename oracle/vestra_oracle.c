@@ -514,3 +514,33 @@ void ora_patch_embed_u8(const uint8_t* img_hwc, size_t h, size_t w,
 void ora_overwrite_prefix_f32(float* tokens, const float* prefix, size_t len) {
   memcpy(tokens, prefix, len * sizeof(float));
 }
+
+/* split_qkv_hnd_f32: token-major QKV [n, 3*heads*head_dim] with column order
+ * Q | K | V, each block [heads, head_dim] head-major, to three head-major
+ * [heads, n, head_dim] tensors: the pack loop of
+ * crates/da-engine/src/vit_block.rs:818-833 (dst = (h*n + t)*head_dim,
+ * src = h*head_dim, + embed for K, + 2*embed for V). */
+void ora_split_qkv_hnd(const float* qkv, size_t n, size_t heads, size_t head_dim,
+                       float* q, float* k, float* v) {
+  const size_t embed = heads * head_dim;
+  for (size_t t = 0; t < n; ++t) {
+    const float* row = qkv + t * 3 * embed;
+    for (size_t h = 0; h < heads; ++h) {
+      const size_t dst = (h * n + t) * head_dim, src = h * head_dim;
+      memcpy(q + dst, row + src, head_dim * sizeof(float));
+      memcpy(k + dst, row + embed + src, head_dim * sizeof(float));
+      memcpy(v + dst, row + 2 * embed + src, head_dim * sizeof(float));
+    }
+  }
+}
+
+/* hnd_to_token_f32: attention output head-major [heads, n, head_dim] back to
+ * token-major [n, heads*head_dim] (the inverse layout of the pack loop above;
+ * crates/da-engine/src/vit_block.rs:560 calls it before the projection). */
+void ora_hnd_to_token(const float* hnd, size_t n, size_t heads, size_t head_dim,
+                      float* out) {
+  for (size_t t = 0; t < n; ++t)
+    for (size_t h = 0; h < heads; ++h)
+      memcpy(out + (t * heads + h) * head_dim, hnd + (h * n + t) * head_dim,
+             head_dim * sizeof(float));
+}

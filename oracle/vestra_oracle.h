@@ -99,6 +99,10 @@ void ora_patch_embed_u8(const uint8_t* img_hwc, size_t h, size_t w,
                         const float* cls, const float* registers,
                         size_t n_register, const float* pos_table, float* out);
 void ora_overwrite_prefix_f32(float* tokens, const float* prefix, size_t len);
+void ora_split_qkv_hnd(const float* qkv, size_t n, size_t heads, size_t head_dim,
+                       float* q, float* k, float* v);
+void ora_hnd_to_token(const float* hnd, size_t n, size_t heads, size_t head_dim,
+                      float* out);
 
 #ifdef __cplusplus
 }

@@ -359,3 +359,29 @@ def test_patch_embed_u8_composes_the_three_steps(rng):
     chw = oracle.normalize_u8_hwc(img, mean, std)
     proj = oracle.patch_project_oihw(chw, 14, wt, b)
     assert np.array_equal(full, oracle.assemble_tokens(proj, 2, 3, cls, None, pos))
+
+
+# ---------------------------------------------------------------- QKV layout glue
+def test_split_qkv_hnd_matches_the_documented_reshape(rng):
+    # vit_block.rs:38-43: columns Q | K | V, each [heads, head_dim] head-major,
+    # i.e. ggml_reshape_4d(qkv, D, H, 3, tok); the pack loop (vit_block.rs:818-833)
+    # moves it to [heads, n, head_dim]
+    n, heads, hd = 7, 3, 8
+    qkv = rng.standard_normal((n, 3 * heads * hd)).astype(np.float32)
+    q, k, v = oracle.split_qkv_hnd(qkv, n, heads, hd)
+    want = qkv.reshape(n, 3, heads, hd).transpose(1, 2, 0, 3)
+    assert np.array_equal(q, want[0]) and np.array_equal(k, want[1]) and np.array_equal(v, want[2])
+    # one element by hand: token 5, K block, head 2, dim 3
+    assert k[2, 5, 3] == qkv[5, heads * hd + 2 * hd + 3]
+    # a transposed read (heads and tokens swapped) would not match
+    assert not np.array_equal(q, qkv[:, :heads * hd].reshape(heads, n, hd))
+
+
+def test_hnd_to_token_inverts_the_split(rng):
+    n, heads, hd = 5, 4, 16
+    hnd = rng.standard_normal((heads, n, hd)).astype(np.float32)
+    tok = oracle.hnd_to_token(hnd, n, heads, hd)
+    assert np.array_equal(tok, hnd.transpose(1, 0, 2).reshape(n, heads * hd))
+    qkv = np.concatenate([tok, tok + 1, tok + 2], axis=1)
+    q, k, v = oracle.split_qkv_hnd(qkv, n, heads, hd)
+    assert np.array_equal(q, hnd) and np.array_equal(k, hnd + 1) and np.array_equal(v, hnd + 2)

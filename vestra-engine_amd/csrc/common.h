@@ -87,6 +87,11 @@ struct LinearArgs {
   const float* ls;    // [N] or null
   float* out;         // [M, N]
   int M, N, K, Kp;
+  // head-major layouts of the attention block (head_dim 64), linear.hip only:
+  float* q_out;  // non-null: out is split Q | K | V into q_out/k_out/v_out [N/192, M, 64]
+  float* k_out;
+  float* v_out;
+  int a_hnd;     // 1: x is head-major [K/64, M, 64] (the attention output)
 };
 
 // Epilogues of the linear: v = acc + b (then * ls when the linear has one),
@@ -101,7 +106,8 @@ enum LinearEpilogue {
 };
 }  // namespace linear_epilogue
 
-// The 128x128-tile linear for K % 4 == 0 and a 16-byte aligned x (linear.hip).
+// The 128x128-tile linear for K % 4 == 0 and a 16-byte aligned x (linear.hip);
+// the head-major layouts of LinearArgs need it.
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi);
 
 }  // namespace vk

@@ -16,6 +16,13 @@
 // k = 16b + 4g + j in component j of a 128-bit read and MFMA step j uses
 // component j, so four steps cover the block's 16 k once.
 //
+// Head-major layouts (head_dim 64): the QKV projection can store Q | K | V
+// straight into three [heads, rows, 64] tensors (the split the attention
+// kernels need), and the output projection can read its input from the
+// head-major attention output; a 64-column strip of a wave is one head, and
+// a float4 of A never crosses a head.  Both are pure address changes: the
+// results are the bits of the linear plus the separate permutation.
+//
 // Traffic: a 128 x 128 tile moves (128 + 128) x 4 bytes of operands per k for
 // 2 x 128 x 128 FLOP, 0.031 byte per FLOP from L2 (the 48 x 64 tiles of the
 // narrow kernel need 0.073).  Tiles are numbered XCD-major (xcd_tile), so
@@ -38,7 +45,9 @@ constexpr int kVec = TM * KC / 4 / kThreads;  // float4 of A (and of B) per thre
 static_assert(TM == TN && TM * KC / 4 % kThreads == 0, "staging slots divide evenly");
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1 && PITCH >= KC, "pitch 4 x odd");
 
-template <int EPI>
+enum Layout { kPlain = 0, kQkvHnd = 1, kAHnd = 2 };
+
+template <int EPI, int LAY>
 __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) {
   __shared__ __align__(16) float As[TM * PITCH];
   __shared__ __align__(16) float Bs[TN * PITCH];
@@ -76,8 +85,11 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
       okb[i] = gn < g.N && gk < g.Kp;
       const int cm = gm < g.M ? gm : g.M - 1;
       const int cn = gn < g.N ? gn : g.N - 1;
-      ra[i] = *reinterpret_cast<const float4*>(g.x + static_cast<size_t>(cm) * g.K +
-                                                (gk < g.K ? gk : g.K - 4));
+      const int ck = gk < g.K ? gk : g.K - 4;
+      const size_t ia = LAY == kAHnd
+                            ? (static_cast<size_t>(ck >> 6) * g.M + cm) * 64 + (ck & 63)
+                            : static_cast<size_t>(cm) * g.K + ck;
+      ra[i] = *reinterpret_cast<const float4*>(g.x + ia);
       rb[i] = *reinterpret_cast<const float4*>(g.wnk + static_cast<size_t>(cn) * g.Kp +
                                                 (gk < g.Kp ? gk : g.Kp - 4));
     }
@@ -153,7 +165,16 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
         if (row < g.M && col < g.N) {
           float v = acc[t][u][r] + bias[u];
           if (g.ls) v = v * ls[u];
-          float* o = g.out + static_cast<size_t>(row) * g.N + col;
+          float* o;
+          if constexpr (LAY == kQkvHnd) {
+            const int embed = g.N / 3;
+            const int which = col >= embed ? (col >= 2 * embed ? 2 : 1) : 0;
+            const int c = col - which * embed;
+            float* base = which == 0 ? g.q_out : (which == 1 ? g.k_out : g.v_out);
+            o = base + (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
+          } else {
+            o = g.out + static_cast<size_t>(row) * g.N + col;
+          }
           if (EPI == kLinStore) *o = v;
           if (EPI == kLinGelu) *o = vkd::gelu1<0>(v);
           if (EPI == kLinGeluErf) *o = vkd::gelu1<1>(v);
@@ -171,19 +192,33 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi) {
       static_cast<long long>((g.M + TM - 1) / TM) * static_cast<long long>((g.N + TN - 1) / TN);
   VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "linear: %lld tiles", tiles);
   const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
-  switch (epi) {
-    case kLinStore:
-      hipLaunchKernelGGL(linear_wide_kernel<kLinStore>, grid, block, 0, rt->stream, g);
-      break;
-    case kLinGelu:
-      hipLaunchKernelGGL(linear_wide_kernel<kLinGelu>, grid, block, 0, rt->stream, g);
-      break;
-    case kLinGeluErf:
-      hipLaunchKernelGGL(linear_wide_kernel<kLinGeluErf>, grid, block, 0, rt->stream, g);
-      break;
-    default:
-      hipLaunchKernelGGL(linear_wide_kernel<kLinResidual>, grid, block, 0, rt->stream, g);
-      break;
+  if (g.q_out) {
+    VK_REQUIRE(epi == kLinStore, "linear: the Q|K|V split takes the store epilogue");
+    hipLaunchKernelGGL((linear_wide_kernel<kLinStore, kQkvHnd>), grid, block, 0, rt->stream, g);
+  } else if (g.a_hnd) {
+    if (epi == kLinResidual)
+      hipLaunchKernelGGL((linear_wide_kernel<kLinResidual, kAHnd>), grid, block, 0, rt->stream, g);
+    else if (epi == kLinStore)
+      hipLaunchKernelGGL((linear_wide_kernel<kLinStore, kAHnd>), grid, block, 0, rt->stream, g);
+    else
+      return set_error(VK_ERR_INVALID, "linear: head-major input takes store or residual");
+  } else {
+    switch (epi) {
+      case kLinStore:
+        hipLaunchKernelGGL((linear_wide_kernel<kLinStore, kPlain>), grid, block, 0, rt->stream, g);
+        break;
+      case kLinGelu:
+        hipLaunchKernelGGL((linear_wide_kernel<kLinGelu, kPlain>), grid, block, 0, rt->stream, g);
+        break;
+      case kLinGeluErf:
+        hipLaunchKernelGGL((linear_wide_kernel<kLinGeluErf, kPlain>), grid, block, 0, rt->stream,
+                           g);
+        break;
+      default:
+        hipLaunchKernelGGL((linear_wide_kernel<kLinResidual, kPlain>), grid, block, 0, rt->stream,
+                           g);
+        break;
+    }
   }
   return check_launch("linear_wide_kernel");
 }

@@ -649,6 +649,35 @@ int check_linear_out(const vk_linear* lin, const vk_tensor* x, const vk_tensor* 
   return VK_OK;
 }
 
+LinearArgs linear_args(const vk_linear* lin, const vk_tensor* x, size_t rows, vk_tensor* out) {
+  LinearArgs g{};
+  g.x = static_cast<const float*>(x->ptr);
+  g.wnk = lin->weight_nk;
+  g.bias = lin->bias;
+  g.ls = lin->ls_gamma;
+  g.out = out ? static_cast<float*>(out->ptr) : nullptr;
+  g.M = static_cast<int>(rows);
+  g.N = static_cast<int>(lin->out_features);
+  g.K = static_cast<int>(lin->in_features);
+  g.Kp = static_cast<int>(lin->k_pitch);
+  return g;
+}
+
+bool tensors_disjoint(const vk_tensor* a, const vk_tensor* b) {
+  const char* pa = static_cast<const char*>(a->ptr);
+  const char* pb = static_cast<const char*>(b->ptr);
+  return a->len == 0 || b->len == 0 || pa + a->len * 4 <= pb || pb + b->len * 4 <= pa;
+}
+
+// The head-major forms need the wide kernel: K % 4 == 0 and an aligned x.
+int check_head_layout(const vk_linear* lin, const vk_tensor* x, size_t heads, size_t head_dim) {
+  VK_UNSUPPORTED_IF(head_dim != 64, "linear: head_dim=%zu (qualified: 64)", head_dim);
+  VK_REQUIRE(heads > 0, "linear: heads must be positive");
+  VK_UNSUPPORTED_IF(lin->in_features % 4 != 0 || reinterpret_cast<uintptr_t>(x->ptr) % 16 != 0,
+                    "linear: head-major forms need in_features %% 4 == 0 and an aligned input");
+  return VK_OK;
+}
+
 int launch_linear(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
                   vk_tensor* out, int epi) {
   if (rows == 0) return VK_OK;
@@ -778,6 +807,59 @@ int vk_linear_run_residual_f32(vk_runtime* rt, const vk_linear* lin, const vk_te
   VK_TRY(check_linear(lin, x, rows));
   VK_TRY(check_linear_out(lin, x, residual, rows, "residual"));
   return launch_linear(rt, lin, x, rows, residual, kLinResidual);
+}
+
+int vk_linear_run_qkv_hnd_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                              size_t rows, size_t heads, size_t head_dim, vk_tensor* q,
+                              vk_tensor* k, vk_tensor* v) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && q && k && v, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_head_layout(lin, x, heads, head_dim));
+  VK_REQUIRE(lin->out_features == 3 * heads * head_dim,
+             "linear_run_qkv_hnd: out_features=%zu, expected 3*heads*head_dim=%zu",
+             lin->out_features, 3 * heads * head_dim);
+  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_qkv_hnd: the linear carries a LayerScale");
+  const size_t part = rows * heads * head_dim;
+  for (const vk_tensor* t : {q, k, v})
+    VK_REQUIRE(t->dtype == VK_F32 && t->len == part, "q, k, v must be f32 [rows*heads*64=%zu]",
+               part);
+  VK_REQUIRE(tensors_disjoint(x, q) && tensors_disjoint(x, k) && tensors_disjoint(x, v) &&
+                 tensors_disjoint(q, k) && tensors_disjoint(q, v) && tensors_disjoint(k, v),
+             "linear_run_qkv_hnd: tensors overlap");
+  if (rows == 0) return VK_OK;
+  LinearArgs g = linear_args(lin, x, rows, nullptr);
+  g.q_out = static_cast<float*>(q->ptr);
+  g.k_out = static_cast<float*>(k->ptr);
+  g.v_out = static_cast<float*>(v->ptr);
+  return vk::launch_linear_wide(rt, g, kLinStore);
+}
+
+static int run_hnd(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd, size_t rows,
+                   size_t heads, size_t head_dim, vk_tensor* out, int epi, const char* what) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && hnd && out, "null argument");
+  VK_TRY(check_linear(lin, hnd, rows));
+  VK_TRY(check_head_layout(lin, hnd, heads, head_dim));
+  VK_REQUIRE(lin->in_features == heads * head_dim, "%s: in_features=%zu, expected heads*64=%zu",
+             what, lin->in_features, heads * head_dim);
+  VK_TRY(check_linear_out(lin, hnd, out, rows, epi == kLinResidual ? "residual" : "out"));
+  if (rows == 0) return VK_OK;
+  LinearArgs g = linear_args(lin, hnd, rows, out);
+  g.a_hnd = 1;
+  return vk::launch_linear_wide(rt, g, epi);
+}
+
+int vk_linear_run_hnd_into_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
+                               size_t rows, size_t heads, size_t head_dim, vk_tensor* out) {
+  return run_hnd(rt, lin, hnd, rows, heads, head_dim, out, kLinStore, "linear_run_hnd_into");
+}
+
+int vk_linear_run_hnd_residual_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
+                                   size_t rows, size_t heads, size_t head_dim,
+                                   vk_tensor* residual) {
+  return run_hnd(rt, lin, hnd, rows, heads, head_dim, residual, kLinResidual,
+                 "linear_run_hnd_residual");
 }
 
 int vk_patchify_nchw_f32(vk_runtime* rt, const vk_tensor* img, size_t h, size_t w,

@@ -132,6 +132,13 @@ _SIGS = {
     "vk_linear_run_gelu_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_gelu_erf_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_residual_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
+    "vk_linear_run_qkv_hnd_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp], _i),
+    "vk_linear_run_hnd_into_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
+    "vk_linear_run_hnd_residual_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
+    "vk_split_qkv_hnd_f32": ([_vp, _vp, _sz, _sz, _sz, _pp, _pp, _pp], _i),
+    "vk_split_qkv_hnd_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp], _i),
+    "vk_hnd_to_token_f32": ([_vp, _vp, _sz, _sz, _sz, _pp], _i),
+    "vk_hnd_to_token_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
     "vk_pos_embed_bicubic_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _f, _pp], _i),
     "vk_patch_embed_u8": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp], _i),
@@ -235,6 +242,24 @@ class Linear:
         """FC1 + GELU: out = GELU(x W + b); A&S erf, or the device erff."""
         fn = lib.vk_linear_run_gelu_erf_f32 if exact_erf else lib.vk_linear_run_gelu_f32
         _check(fn(self.rt.handle, self.handle, x.handle, rows, out.handle))
+
+    def run_qkv_hnd(self, x: Tensor, rows: int, heads: int, q: Tensor, k: Tensor,
+                    v: Tensor, head_dim: int = 64) -> None:
+        """QKV projection storing head-major Q, K, V [heads, rows, 64]."""
+        _check(lib.vk_linear_run_qkv_hnd_f32(self.rt.handle, self.handle, x.handle, rows, heads,
+                                             head_dim, q.handle, k.handle, v.handle))
+
+    def run_hnd_into(self, hnd: Tensor, rows: int, heads: int, out: Tensor,
+                     head_dim: int = 64) -> None:
+        """Projection of a head-major input [heads, rows, 64]."""
+        _check(lib.vk_linear_run_hnd_into_f32(self.rt.handle, self.handle, hnd.handle, rows,
+                                              heads, head_dim, out.handle))
+
+    def run_hnd_residual(self, hnd: Tensor, rows: int, heads: int, residual: Tensor,
+                         head_dim: int = 64) -> None:
+        """residual += (hnd as token rows) W + b [* gamma]."""
+        _check(lib.vk_linear_run_hnd_residual_f32(self.rt.handle, self.handle, hnd.handle, rows,
+                                                  heads, head_dim, residual.handle))
 
     def run_residual(self, x: Tensor, rows: int, residual: Tensor) -> None:
         """proj / FC2 + LayerScale + residual: residual += (x W + b) [* gamma]."""
@@ -366,6 +391,30 @@ class Runtime:
                            cols: int, eps: float, out: Tensor) -> None:
         _check(lib.vk_layernorm_into_f32(self.handle, x.handle, gamma.handle, beta.handle,
                                          rows, cols, eps, out.handle))
+
+    def split_qkv_hnd_f32(self, qkv: Tensor, rows: int, heads: int, head_dim: int):
+        """CudaRuntime::split_qkv_hnd_f32: returns head-major (q, k, v)."""
+        q, k, v = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        _check(lib.vk_split_qkv_hnd_f32(self.handle, qkv.handle, rows, heads, head_dim,
+                                        C.byref(q), C.byref(k), C.byref(v)))
+        return Tensor(self, q), Tensor(self, k), Tensor(self, v)
+
+    def split_qkv_hnd_into_f32(self, qkv: Tensor, rows: int, heads: int, head_dim: int,
+                               q: Tensor, k: Tensor, v: Tensor) -> None:
+        _check(lib.vk_split_qkv_hnd_into_f32(self.handle, qkv.handle, rows, heads, head_dim,
+                                             q.handle, k.handle, v.handle))
+
+    def hnd_to_token_f32(self, hnd: Tensor, rows: int, heads: int, head_dim: int) -> Tensor:
+        """CudaRuntime::hnd_to_token_f32: head-major -> token-major rows."""
+        out = C.c_void_p()
+        _check(lib.vk_hnd_to_token_f32(self.handle, hnd.handle, rows, heads, head_dim,
+                                       C.byref(out)))
+        return Tensor(self, out)
+
+    def hnd_to_token_into_f32(self, hnd: Tensor, rows: int, heads: int, head_dim: int,
+                              out: Tensor) -> None:
+        _check(lib.vk_hnd_to_token_into_f32(self.handle, hnd.handle, rows, heads, head_dim,
+                                            out.handle))
 
     def gelu_f32_in_place(self, x: Tensor) -> None:
         _check(lib.vk_gelu_f32_inplace(self.handle, x.handle))
