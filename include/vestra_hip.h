@@ -312,6 +312,23 @@ int vk_linear_run_hnd_residual_f32(vk_runtime* rt, const vk_linear* lin,
                                    size_t heads, size_t head_dim,
                                    vk_tensor* residual);
 
+/* CudaRuntime::attention_online_f32(q, k, v, heads, rows, head_dim)
+ * (vit_block.rs:363, 559) and the CPU vestra_kernels::attention
+ * (vit_block.rs:952): out = softmax(Q K^T / sqrt(head_dim)) V over each of
+ * `heads` independent head-major sequences [rows, head_dim] of q, k, v
+ * ([heads, rows, head_dim]).  A view-major local-layer batch
+ * [views, heads, tokens, 64] is the same call with heads = views*heads and
+ * rows = tokens.  head_dim 64.  New tensor / caller tensor (no overlap with
+ * q, k or v). */
+int vk_attention_online_f32(vk_runtime* rt, const vk_tensor* q,
+                            const vk_tensor* k, const vk_tensor* v,
+                            size_t heads, size_t rows, size_t head_dim,
+                            vk_tensor** out);
+int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q,
+                          const vk_tensor* k, const vk_tensor* v,
+                          size_t heads, size_t rows, size_t head_dim,
+                          vk_tensor* out);
+
 /* CudaRuntime::prepend_cls_add_pos_f32(patches, cls, pos, n_patches, embed)
  * (patch_embed.rs:234-240): row 0 = cls + pos[0]; row 1+p = patch_p + pos[1+p]. */
 int vk_prepend_cls_add_pos_f32(vk_runtime* rt, const vk_tensor* patches,

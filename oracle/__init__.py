@@ -63,6 +63,7 @@ _SIGS = {
     "ora_overwrite_prefix_f32": ([_vp, _vp, _sz], None),
     "ora_split_qkv_hnd": ([_vp, _sz, _sz, _sz, _vp, _vp, _vp], None),
     "ora_hnd_to_token": ([_vp, _sz, _sz, _sz, _vp], None),
+    "ora_attention_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], None),
 }
 for _n, (_a, _r) in _SIGS.items():
     _fn = getattr(lib, _n)
@@ -250,6 +251,13 @@ def hnd_to_token(hnd, n: int, heads: int, head_dim: int) -> np.ndarray:
     """Head-major [heads, n, head_dim] -> token-major [n, heads*head_dim]."""
     out = np.empty((n, heads * head_dim), np.float32)
     lib.ora_hnd_to_token(_p(_f32(hnd)), n, heads, head_dim, _p(out))
+    return out
+
+
+def attention(q, k, v, batches: int, n: int, head_dim: int) -> np.ndarray:
+    """softmax(Q K^T / sqrt(head_dim)) V over `batches` sequences [n, head_dim]."""
+    out = np.empty((batches, n, head_dim), np.float32)
+    lib.ora_attention_f32(_p(_f32(q)), _p(_f32(k)), _p(_f32(v)), batches, n, head_dim, _p(out))
     return out
 
 

@@ -544,3 +544,44 @@ void ora_hnd_to_token(const float* hnd, size_t n, size_t heads, size_t head_dim,
       memcpy(out + (t * heads + h) * head_dim, hnd + (h * n + t) * head_dim,
              head_dim * sizeof(float));
 }
+
+/* Scaled dot-product attention softmax(Q K^T / sqrt(head_dim)) V over each of
+ * `batches` independent head-major sequences [n, head_dim] (a head of one
+ * view, or a head of the whole flattened sequence): the core of Op::Attention
+ * (crates/da-graph/src/graph.rs:370-400, cpu_backend.rs:198-260) and of the
+ * reference's `attention_online_f32` / `vestra_kernels::attention`
+ * (crates/da-engine/src/vit_block.rs:363, 559, 952).  The reference's own
+ * kernel is outside the tree; this restatement is the textbook max-shifted
+ * softmax: s_j = (sum_d q_d k_jd) * (1/sqrt(head_dim)), p_j = expf(s_j - max),
+ * out = (sum_j p_j v_j) / (sum_j p_j), every sum sequential in f32. */
+void ora_attention_f32(const float* q, const float* k, const float* v, size_t batches,
+                       size_t n, size_t head_dim, float* out) {
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  #pragma omp parallel for schedule(static)
+  for (long long bi = 0; bi < (long long)(batches * n); ++bi) {
+    const size_t b = (size_t)bi / n, i = (size_t)bi % n;
+    const float* qi = q + (b * n + i) * head_dim;
+    const float* kb = k + b * n * head_dim;
+    const float* vb = v + b * n * head_dim;
+    float* o = out + (b * n + i) * head_dim;
+    float* s = (float*)malloc(n * sizeof(float));
+    float mx = -INFINITY;
+    for (size_t j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (size_t d = 0; d < head_dim; ++d) acc += qi[d] * kb[j * head_dim + d];
+      s[j] = acc * scale;
+      if (s[j] > mx) mx = s[j];
+    }
+    float l = 0.0f;
+    for (size_t j = 0; j < n; ++j) {
+      s[j] = expf(s[j] - mx);
+      l += s[j];
+    }
+    for (size_t d = 0; d < head_dim; ++d) {
+      float acc = 0.0f;
+      for (size_t j = 0; j < n; ++j) acc += s[j] * vb[j * head_dim + d];
+      o[d] = acc / l;
+    }
+    free(s);
+  }
+}

@@ -103,6 +103,8 @@ void ora_split_qkv_hnd(const float* qkv, size_t n, size_t heads, size_t head_dim
                        float* q, float* k, float* v);
 void ora_hnd_to_token(const float* hnd, size_t n, size_t heads, size_t head_dim,
                       float* out);
+void ora_attention_f32(const float* q, const float* k, const float* v, size_t batches,
+                       size_t n, size_t head_dim, float* out);
 
 #ifdef __cplusplus
 }

@@ -385,3 +385,47 @@ def test_hnd_to_token_inverts_the_split(rng):
     qkv = np.concatenate([tok, tok + 1, tok + 2], axis=1)
     q, k, v = oracle.split_qkv_hnd(qkv, n, heads, hd)
     assert np.array_equal(q, hnd) and np.array_equal(k, hnd + 1) and np.array_equal(v, hnd + 2)
+
+
+# ---------------------------------------------------------------- attention core
+def _attention_f64(q, k, v):
+    s = np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64)) / np.sqrt(q.shape[-1])
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    return np.einsum("bij,bjd->bid", p / p.sum(axis=-1, keepdims=True), v.astype(np.float64))
+
+
+def test_attention_matches_float64_brute_force(rng):
+    b, n, d = 3, 37, 64
+    q, k, v = (rng.standard_normal((b, n, d)).astype(np.float32) for _ in range(3))
+    got = oracle.attention(q, k, v, b, n, d)
+    ref = _attention_f64(q, k, v)
+    assert np.max(np.abs(got - ref)) < 2e-6
+    # dropping the 1/sqrt(d) scale is a different function
+    wrong = _attention_f64(q * np.sqrt(d).astype(np.float32), k, v)
+    assert np.max(np.abs(got - wrong)) > 1e-2
+
+
+def test_attention_matches_torch_sdpa_twin(rng):
+    torch = pytest.importorskip("torch")
+    b, n, d = 2, 50, 64
+    q, k, v = (rng.standard_normal((b, n, d)).astype(np.float32) for _ in range(3))
+    twin = torch.nn.functional.scaled_dot_product_attention(
+        *(torch.from_numpy(a).double() for a in (q, k, v))).numpy()
+    assert np.max(np.abs(oracle.attention(q, k, v, b, n, d) - twin)) < 2e-6
+
+
+def test_attention_invariants(rng):
+    n, d = 20, 64
+    q, k, v = (rng.standard_normal((1, n, d)).astype(np.float32) for _ in range(3))
+    # one key far ahead of the others selects its value row
+    k2 = k.copy()
+    k2[0, 7] = q[0, 3] * 40
+    assert np.allclose(oracle.attention(q, k2, v, 1, n, d)[0, 3], v[0, 7], atol=1e-6)
+    # identical value rows come back unchanged (up to rounding)
+    vc = np.repeat(v[:, :1], n, axis=1)
+    assert np.allclose(oracle.attention(q, k, vc, 1, n, d), vc, rtol=0, atol=2e-6)
+    # permuting keys and values together changes nothing but rounding
+    perm = rng.permutation(n)
+    assert np.allclose(oracle.attention(q, k[:, perm], v[:, perm], 1, n, d),
+                       oracle.attention(q, k, v, 1, n, d), rtol=0, atol=2e-6)

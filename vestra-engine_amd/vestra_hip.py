@@ -139,6 +139,8 @@ _SIGS = {
     "vk_split_qkv_hnd_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp], _i),
     "vk_hnd_to_token_f32": ([_vp, _vp, _sz, _sz, _sz, _pp], _i),
     "vk_hnd_to_token_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp], _i),
+    "vk_attention_online_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz, _pp], _i),
+    "vk_attention_into_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
     "vk_pos_embed_bicubic_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _f, _pp], _i),
     "vk_patch_embed_u8": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp], _i),
@@ -415,6 +417,19 @@ class Runtime:
                               out: Tensor) -> None:
         _check(lib.vk_hnd_to_token_into_f32(self.handle, hnd.handle, rows, heads, head_dim,
                                             out.handle))
+
+    def attention_online_f32(self, q: Tensor, k: Tensor, v: Tensor, heads: int, rows: int,
+                             head_dim: int) -> Tensor:
+        """CudaRuntime::attention_online_f32: softmax(Q K^T / sqrt(d)) V per head."""
+        out = C.c_void_p()
+        _check(lib.vk_attention_online_f32(self.handle, q.handle, k.handle, v.handle, heads,
+                                           rows, head_dim, C.byref(out)))
+        return Tensor(self, out)
+
+    def attention_into_f32(self, q: Tensor, k: Tensor, v: Tensor, heads: int, rows: int,
+                           head_dim: int, out: Tensor) -> None:
+        _check(lib.vk_attention_into_f32(self.handle, q.handle, k.handle, v.handle, heads,
+                                         rows, head_dim, out.handle))
 
     def gelu_f32_in_place(self, x: Tensor) -> None:
         _check(lib.vk_gelu_f32_inplace(self.handle, x.handle))
