@@ -287,6 +287,36 @@ def linear_epilogue_timing(rt, rng, rows, iters):
     return out
 
 
+def attention_timing(rt, rng, iters):
+    """The attention core (softmax(Q K^T / 8) V, F32 MFMA, online softmax) at
+    the path's shapes: a local layer of the 12-view batch (144 sequences of
+    866 tokens), a global layer (12 heads over the flattened 10,392 rows) and
+    the ViT-L 1008x672 image (16 heads over 3,458 rows).  FLOP counts
+    4*n*n*64 per sequence (two n x n x 64 products)."""
+    out = {}
+    for name, seqs, n in (("local_12view", 12 * H, TPV), ("global_12view", H, 12 * TPV),
+                          ("vitl_1008x672", 16, 3458)):
+        q, k, v = (rt.upload_f32((rng.standard_normal(seqs * n * HD)).astype(np.float32))
+                   for _ in range(3))
+        o = rt.alloc_f32(seqs * n * HD)
+
+        def fn():
+            rt.attention_into_f32(q, k, v, seqs, n, HD, o)
+
+        fn()
+        reps = max(1, iters // 5)
+        graph = capture(rt, fn, reps)
+        graph.launch()
+        us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / reps
+                               for _ in range(OP_TRIALS))
+        flop = 4.0 * seqs * n * n * HD
+        out[name] = {"sequences": seqs, "n": n, "us": round(us, 2),
+                     "TFLOP_s": round(flop / us / 1e6, 2),
+                     "frac_of_f32_mfma_peak": round(flop / us / 1e6 / MFMA_F32_PEAK_TFLOPS, 4)}
+        del q, k, v, o, graph
+    return out
+
+
 def patch_embed_timing(rt, rng, h, w, embed, iters):
     """Fused patch embedding of one u8 image (normalise, unfold, F32-MFMA
     projection, bias, position add, special rows): time per image and the
@@ -399,6 +429,9 @@ def main():
     ap.add_argument("--linear", action="store_true",
                     help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
                          "at the 12-view shape")
+    ap.add_argument("--attention", action="store_true",
+                    help="attention mode: the attention core at the local, global and ViT-L "
+                         "shapes")
     ap.add_argument("--sweep", type=str, default=None, metavar="VIEWS",
                     help="size-sweep mode: the per-operation table at each comma-separated "
                          "view count (866 rows per view), one JSON line per size")
@@ -421,6 +454,9 @@ def main():
             print(json.dumps({"views": views, "rows": rows, "rotate_sets": sets, "ops": table}),
                   flush=True)
             rt.synchronize()
+        return
+    if args.attention:
+        print(json.dumps({"attention": attention_timing(rt, rng, args.op_iters)}), flush=True)
         return
     if args.linear:
         print(json.dumps({"linear_epilogues": linear_epilogue_timing(rt, rng, TPV * 12,
