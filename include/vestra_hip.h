@@ -431,6 +431,57 @@ int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
                            size_t view_count, const vk_tensor* camera,
                            unsigned flags);
 
+/* Cached device parameters of one whole block (the CudaAttentionLayer and
+ * CudaMlpLayer of vit_block.rs:161-184): the vk_vit_layer vectors plus the
+ * four prepared projections.  qkv: D -> 3D with bias, no LayerScale; proj:
+ * D -> D with bias and ls1 as its LayerScale (or none); fc1: D -> M with
+ * bias; fc2: M -> D with bias and ls2 (or none).  qnorm/knorm NULL: no
+ * Q/K-norm. */
+typedef struct vk_vit_block_weights {
+  const vk_tensor* norm1_gamma;
+  const vk_tensor* norm1_beta;
+  const vk_linear* qkv;
+  const vk_tensor* qnorm_gamma;
+  const vk_tensor* qnorm_beta;
+  const vk_tensor* knorm_gamma;
+  const vk_tensor* knorm_beta;
+  const vk_linear* proj;
+  const vk_tensor* norm2_gamma;
+  const vk_tensor* norm2_beta;
+  const vk_linear* fc1;
+  const vk_linear* fc2;
+} vk_vit_block_weights;
+
+/* Device scratch of one block, all f32: ln [rows*D]; q, k, v, attn
+ * [H, rows, 64] each; hidden [rows*M].  Reused by every block of a pass. */
+typedef struct vk_vit_block_workspace {
+  vk_tensor* ln;
+  vk_tensor* q;
+  vk_tensor* k;
+  vk_tensor* v;
+  vk_tensor* attn;
+  vk_tensor* hidden;
+} vk_vit_block_workspace;
+
+/* One whole DA3 ViT block on the device, in place on `tokens`
+ * [rows = view_count*(1+num_register+gh*gw), D]: the device-resident
+ * transformer tail CudaTransformerTailExecutor::run_tail_device
+ * (vit_block.rs:489-582) for all views of a batch at once.
+ *   [camera overwrite at alt_start] -> LN1 -> QKV projection storing
+ *   head-major Q, K, V -> Q/K-norm + 2D RoPE (gated as in
+ *   vk_vit_block_fused_ops) -> attention (global layers: each head over all
+ *   rows; local layers: each head of each view over its own tokens) ->
+ *   output projection (+b, *ls1) read head-major, added to tokens -> LN2 ->
+ *   FC1 (+b) + GELU -> FC2 (+b, *ls2) added to tokens.
+ * Global layers follow backbone.rs:459-460 (alt_start >= 0, layer >=
+ * alt_start, odd layer).  Results equal the unfused reference sequence
+ * within the dot-product bounds of the projections and attention. */
+int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
+                             size_t layer_idx, const vk_vit_block_weights* w,
+                             vk_tensor* tokens, size_t gh, size_t gw,
+                             size_t view_count, const vk_tensor* camera,
+                             const vk_vit_block_workspace* ws);
+
 /* ------------------------------------------------------------------ */
 /* timing and graphs                                                    */
 /* ------------------------------------------------------------------ */

@@ -338,3 +338,59 @@ def block_fused_ops(tokens, q, k, attn_proj, hidden, mlp_out, layer: dict, cfg: 
     hid = gelu(hidden)
     x = layerscale_residual(x, _f32(mlp_out).reshape(rows, D), layer.get("ls2"))
     return {"tokens": x, "ln1": ln1, "q": qo, "k": ko, "ln2": ln2, "hidden": hid}
+
+
+def block_forward(tokens, params: dict, cfg: dict, layer_idx: int, gh: int, gw: int,
+                  view_count: int, camera=None) -> dict:
+    """One whole DA3 ViT block (vit_block.rs:1019-1139; device order of
+    run_tail_device, vit_block.rs:489-582), composed from the functions above.
+
+    params: norm1/norm2 gamma+beta, qkv_w [D, 3D] + qkv_b, optional
+    qnorm/knorm gamma+beta, proj_w [D, D] + proj_b + optional ls1, fc1_w
+    [D, M] + fc1_b, fc2_w [M, D] + fc2_b + optional ls2 (weights in the
+    reference's [in, out] layout).  Local layers attend within each view,
+    global layers (backbone.rs:459-460) over all rows.  Returns dict(tokens,
+    q, k, v, attn, ln2, hidden) with q/k/v/attn head-major [H, rows, 64].
+    """
+    D = cfg["embed_dim"]
+    H = cfg["num_heads"]
+    hd = cfg["head_dim"]
+    n_special = 1 + cfg["num_register"]
+    tpv = n_special + gh * gw
+    rows = tpv * view_count
+    alt = cfg["alt_start"]
+    glob = alt >= 0 and layer_idx >= alt and layer_idx % 2 == 1
+    x = _f32(tokens).reshape(rows, D).copy()
+    if alt >= 0 and layer_idx == alt:
+        cam = _f32(camera).reshape(-1)
+        for v in range(view_count):
+            slot = 1 if v > 0 else 0
+            x[v * tpv] = cam[slot * D:(slot + 1) * D]
+    ln1 = layernorm(x, params["norm1_gamma"], params["norm1_beta"], cfg["ln_eps"])
+    q, k, v = split_qkv_hnd(linear(ln1, params["qkv_w"], params["qkv_b"]), rows, H, hd)
+    use_qkn = cfg["qknorm_start"] >= 0 and layer_idx >= cfg["qknorm_start"] and \
+        params.get("qnorm_gamma") is not None
+    use_rope = cfg["rope_start"] >= 0 and layer_idx >= cfg["rope_start"]
+    if use_qkn:
+        # per (head, token) row: the view split does not matter
+        q = layernorm(q, params["qnorm_gamma"], params["qnorm_beta"], cfg["qk_norm_eps"])
+        k = layernorm(k, params["knorm_gamma"], params["knorm_beta"], cfg["qk_norm_eps"])
+    if use_rope:
+        pos = rope_positions(n_special, gh, gw, view_count, glob).astype(np.int64)
+        q = rope2d(q, H, rows, hd, pos, cfg["rope_freq"]).reshape(H, rows, hd)
+        k = rope2d(k, H, rows, hd, pos, cfg["rope_freq"]).reshape(H, rows, hd)
+    if glob:
+        attn = attention(q, k, v, H, rows, hd)
+    else:
+        # [H, rows, hd] holds head h of view v at rows (h*views + v)*tpv...
+        attn = attention(q, k, v, H * view_count, tpv, hd)
+    attn = attn.reshape(H, rows, hd)
+    y = linear(hnd_to_token(attn, rows, H, hd).reshape(rows, D), params["proj_w"],
+               params["proj_b"])
+    x = layerscale_residual(x, y, params.get("ls1"))
+    ln2 = layernorm(x, params["norm2_gamma"], params["norm2_beta"], cfg["ln_eps"])
+    hidden = gelu(linear(ln2, params["fc1_w"], params["fc1_b"]))
+    y = linear(hidden, params["fc2_w"], params["fc2_b"])
+    x = layerscale_residual(x, y, params.get("ls2"))
+    return {"tokens": x, "q": q.reshape(H, rows, hd), "k": k.reshape(H, rows, hd),
+            "v": v.reshape(H, rows, hd), "attn": attn, "ln2": ln2, "hidden": hidden}

@@ -429,3 +429,31 @@ def test_attention_invariants(rng):
     perm = rng.permutation(n)
     assert np.allclose(oracle.attention(q, k[:, perm], v[:, perm], 1, n, d),
                        oracle.attention(q, k, v, 1, n, d), rtol=0, atol=2e-6)
+
+
+# ---------------------------------------------------------------- whole block
+def test_block_forward_matches_float64_twin(rng):
+    """The oracle's whole-block composition (vit_block.rs:1019-1139) against an
+    independent float64 composition of the same steps (tests/block_twin.py):
+    local layer with 3 views, global layer, and the camera slot at alt_start."""
+    from block_twin import block_f64, config, make_params, normals
+    D, H, M, gh, gw, views = 768, 12, 3072, 4, 6, 3
+    cfg = config(D, H, M)
+    rows = (2 + gh * gw) * views
+    for layer in (2, 4, 5):
+        p = make_params(rng, D, M)
+        x0, cam = normals(rng, rows, D), normals(rng, 2 * D)
+        got = oracle.block_forward(x0, p, cfg, layer, gh, gw, views, cam)
+        ref = block_f64(x0, p, cfg, layer, gh, gw, views, cam)
+        for name in ("tokens", "q", "k", "v", "attn", "ln2", "hidden"):
+            d = np.abs(got[name].astype(np.float64).reshape(-1) - ref[name].reshape(-1)).max()
+            assert d < 2e-5, (layer, name, d)
+        if layer == 2:
+            # attending across views (the global rule on a local layer) is a
+            # different function
+            wrong = block_f64(x0, p, dict(cfg, alt_start=1), 3, gh, gw, views, cam)
+            assert np.abs(got["attn"] - wrong["attn"]).max() > 1e-2
+            # a missing LayerScale is a different function
+            nols = {k: v for k, v in p.items() if k not in ("ls1", "ls2")}
+            wrong = block_f64(x0, nols, cfg, layer, gh, gw, views, cam)
+            assert np.abs(got["tokens"] - wrong["tokens"]).max() > 1e-2

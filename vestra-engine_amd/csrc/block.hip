@@ -128,3 +128,112 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
   }
   return VK_OK;
 }
+
+// ---------------------------------------------------------------------------
+// The whole block on the device (run_tail_device, vit_block.rs:489-582).
+//
+// Q, K, V and the attention output stay head-major [H, rows, 64] for local
+// and global layers alike.  A local layer's attention is per view; in this
+// layout head h of view v is the contiguous run of tpv rows starting at row
+// h*rows + v*tpv = (h*view_count + v)*tpv, so the view-major batch is simply
+// H*view_count sequences of tpv tokens -- no repacking between layer kinds.
+// The QKV projection writes Q, K, V head-major from its epilogue and the
+// output projection reads the attention output head-major, so the
+// reference's split_qkv_hnd / hnd_to_token passes (vit_block.rs:539-541, 560)
+// are not separate launches.  8 launches per block.
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_linear(const vk_linear* l, size_t in, size_t out, const char* name) {
+  VK_REQUIRE(l != nullptr, "block weight %s is null", name);
+  VK_REQUIRE(l->in_features == in && l->out_features == out,
+             "block weight %s is %zu -> %zu, expected %zu -> %zu", name, l->in_features,
+             l->out_features, in, out);
+  return VK_OK;
+}
+
+}  // namespace
+
+extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
+                                        size_t layer_idx, const vk_vit_block_weights* w,
+                                        vk_tensor* tokens, size_t gh, size_t gw,
+                                        size_t view_count, const vk_tensor* camera,
+                                        const vk_vit_block_workspace* ws) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(cfg && w && tokens && ws, "null argument");
+  VK_REQUIRE(view_count > 0 && gw > 0 && gh > 0, "empty grid or view count");
+  const size_t D = cfg->embed_dim;
+  const size_t H = cfg->num_heads;
+  const size_t hd = cfg->head_dim;
+  const size_t M = cfg->mlp_hidden;
+  VK_REQUIRE(D > 0 && H > 0 && M > 0, "empty model dimensions");
+  VK_UNSUPPORTED_IF(hd != 64, "block: head_dim=%zu (qualified: 64)", hd);
+  VK_REQUIRE(H * hd == D, "num_heads*head_dim (%zu) must equal embed_dim (%zu)", H * hd, D);
+  const size_t n_special = 1 + cfg->num_register;
+  const size_t tpv = n_special + gh * gw;
+  const size_t rows = tpv * view_count;
+  VK_TRY(check_len(tokens, rows * D, "tokens"));
+  VK_TRY(check_len(ws->ln, rows * D, "workspace ln"));
+  VK_TRY(check_len(ws->q, rows * D, "workspace q"));
+  VK_TRY(check_len(ws->k, rows * D, "workspace k"));
+  VK_TRY(check_len(ws->v, rows * D, "workspace v"));
+  VK_TRY(check_len(ws->attn, rows * D, "workspace attn"));
+  VK_TRY(check_len(ws->hidden, rows * M, "workspace hidden"));
+  VK_TRY(check_linear(w->qkv, D, 3 * D, "qkv"));
+  VK_TRY(check_linear(w->proj, D, D, "proj"));
+  VK_TRY(check_linear(w->fc1, D, M, "fc1"));
+  VK_TRY(check_linear(w->fc2, M, D, "fc2"));
+
+  const bool global = layer_uses_global(cfg, layer_idx);
+
+  // camera-token slot write at alt_start (backbone.rs:446-457, 746-768)
+  if (cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start)) {
+    VK_REQUIRE(camera != nullptr, "camera token required at alt_start=%d", cfg->alt_start);
+    VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D, "camera token must hold >= %zu f32", D);
+    VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
+               "multi-view camera token must hold reference and source slots (2*%zu)", D);
+    for (size_t v = 0; v < view_count; ++v) {
+      const size_t slot = v > 0 ? 1 : 0;
+      VK_TRY(vk_copy_segment_into_f32(rt, tokens, v * tpv * D, camera, slot * D, D));
+    }
+  }
+
+  // LN1 -> QKV (head-major Q, K, V)
+  VK_TRY(vk_layernorm_into_f32(rt, tokens, w->norm1_gamma, w->norm1_beta, rows, D, cfg->ln_eps,
+                               ws->ln));
+  VK_TRY(vk_linear_run_qkv_hnd_f32(rt, w->qkv, ws->ln, rows, H, hd, ws->q, ws->k, ws->v));
+
+  // Q/K-norm + RoPE, gated as in vk_vit_block_fused_ops (vit_block.rs:835-838)
+  const bool use_qknorm = cfg->qknorm_start >= 0 &&
+                          static_cast<long long>(layer_idx) >= cfg->qknorm_start &&
+                          w->qnorm_gamma != nullptr;
+  const bool use_rope =
+      cfg->rope_start >= 0 && static_cast<long long>(layer_idx) >= cfg->rope_start;
+  if (use_rope) {
+    VK_TRY(vk_qk_norm_rope_grid_f32(
+        rt, ws->q, ws->k, use_qknorm ? w->qnorm_gamma : nullptr,
+        use_qknorm ? w->qnorm_beta : nullptr, use_qknorm ? w->knorm_gamma : nullptr,
+        use_qknorm ? w->knorm_beta : nullptr, H, hd, n_special, gh, gw, view_count,
+        global ? 1 : 0, VK_QK_HEADS_OUTER, cfg->rope_freq, cfg->qk_norm_eps));
+  } else if (use_qknorm) {
+    VK_TRY(vk_layernorm_into_f32(rt, ws->q, w->qnorm_gamma, w->qnorm_beta, rows * H, hd,
+                                 cfg->qk_norm_eps, ws->q));
+    VK_TRY(vk_layernorm_into_f32(rt, ws->k, w->knorm_gamma, w->knorm_beta, rows * H, hd,
+                                 cfg->qk_norm_eps, ws->k));
+  }
+
+  // attention: global -> H sequences of all rows; local -> H*view_count
+  // sequences of one view's tokens
+  VK_TRY(vk_attention_into_f32(rt, ws->q, ws->k, ws->v, global ? H : H * view_count,
+                               global ? rows : tpv, hd, ws->attn));
+
+  // tokens += (attn @ Wproj + b) * ls1
+  VK_TRY(vk_linear_run_hnd_residual_f32(rt, w->proj, ws->attn, rows, H, hd, tokens));
+
+  // LN2 -> FC1 + GELU -> tokens += (hidden @ Wfc2 + b) * ls2
+  VK_TRY(vk_layernorm_into_f32(rt, tokens, w->norm2_gamma, w->norm2_beta, rows, D, cfg->ln_eps,
+                               ws->ln));
+  VK_TRY(vk_linear_run_gelu_f32(rt, w->fc1, ws->ln, rows, ws->hidden));
+  VK_TRY(vk_linear_run_residual_f32(rt, w->fc2, ws->hidden, rows, tokens));
+  return VK_OK;
+}

@@ -85,6 +85,16 @@ class VitActivations(C.Structure):
         "tokens", "ln1", "q", "k", "attn_proj", "ln2", "hidden", "mlp_out")]
 
 
+class VitBlockWeights(C.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "norm1_gamma", "norm1_beta", "qkv", "qnorm_gamma", "qnorm_beta", "knorm_gamma",
+        "knorm_beta", "proj", "norm2_gamma", "norm2_beta", "fc1", "fc2")]
+
+
+class VitBlockWorkspace(C.Structure):
+    _fields_ = [(n, _vp) for n in ("ln", "q", "k", "v", "attn", "hidden")]
+
+
 _SIGS = {
     "vk_last_error": ([], C.c_char_p),
     "vk_abi_version": ([], _i),
@@ -147,6 +157,9 @@ _SIGS = {
     "vk_vit_block_fused_ops": (
         [_vp, C.POINTER(VitConfig), _sz, C.POINTER(VitLayer), C.POINTER(VitLayer),
          C.POINTER(VitActivations), _sz, _sz, _sz, _vp, C.c_uint], _i),
+    "vk_vit_block_forward_f32": (
+        [_vp, C.POINTER(VitConfig), _sz, C.POINTER(VitBlockWeights), _vp, _sz, _sz, _sz, _vp,
+         C.POINTER(VitBlockWorkspace)], _i),
     "vk_event_create": ([_vp, _pp], _i),
     "vk_event_destroy": ([_vp], _i),
     "vk_event_record": ([_vp, _vp], _i),
@@ -553,10 +566,41 @@ class Runtime:
     def begin_capture(self) -> None:
         _check(lib.vk_graph_begin_capture(self.handle))
 
+    def vit_block_forward_f32(self, cfg: VitConfig, layer_idx: int, weights: VitBlockWeights,
+                              tokens: Tensor, gh: int, gw: int, view_count: int,
+                              camera: Optional[Tensor], ws: VitBlockWorkspace) -> None:
+        """run_tail_device: one whole block on the device, in place on tokens."""
+        _check(lib.vk_vit_block_forward_f32(self.handle, C.byref(cfg), layer_idx,
+                                            C.byref(weights), tokens.handle, gh, gw, view_count,
+                                            _h(camera), C.byref(ws)))
+
+    def block_workspace(self, rows: int, embed: int, mlp: int) -> "BlockWorkspace":
+        return BlockWorkspace(self, rows, embed, mlp)
+
     def end_capture(self) -> Graph:
         out = C.c_void_p()
         _check(lib.vk_graph_end_capture(self.handle, C.byref(out)))
         return Graph(self, out)
+
+
+def block_weights_struct(**handles) -> VitBlockWeights:
+    """Builds a VitBlockWeights from named tensors and linears (missing: NULL)."""
+    w = VitBlockWeights()
+    for name, _ in VitBlockWeights._fields_:
+        h = handles.get(name)
+        setattr(w, name, None if h is None else h.handle.value)
+    return w
+
+
+class BlockWorkspace:
+    """Owns the device scratch of vk_vit_block_forward_f32 for `rows` tokens."""
+
+    def __init__(self, rt: "Runtime", rows: int, embed: int, mlp: int):
+        self.tensors = {n: rt.alloc_f32(rows * embed) for n in ("ln", "q", "k", "v", "attn")}
+        self.tensors["hidden"] = rt.alloc_f32(rows * mlp)
+        self.struct = VitBlockWorkspace()
+        for name, t in self.tensors.items():
+            setattr(self.struct, name, t.handle.value)
 
 
 def layer_struct(**tensors: Optional[Tensor]) -> VitLayer:
