@@ -358,6 +358,37 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h,
                       vk_tensor* out);
 
 /* ------------------------------------------------------------------ */
+/* backbone capture and head hand-off                                   */
+/* ------------------------------------------------------------------ */
+
+/* Backbone::post_process_capture (backbone.rs:1139-1179) for view_count
+ * view-major views of n = n_special + n_patch tokens, embed columns:
+ *   cat_token != 0: feat [views, n_patch, 2*embed] with row t =
+ *     [local_x row n_special+t | LN(x row n_special+t)], cam [views, 2*embed]
+ *     = [local_x row 0 | x row 0];
+ *   cat_token == 0: feat [views, n_patch, embed] = LN(x patch rows), cam
+ *     [views, embed] = x row 0; local_x may be NULL.
+ * LN is the final vit.norm (norm_gamma/beta f32 or f16, eps = cfg.ln_eps):
+ * bit-identical to vk_layernorm_into_f32 on the same rows.  local_x is the
+ * pre-alternation snapshot the reference keeps (backbone.rs:488, 635). */
+int vk_capture_f32(vk_runtime* rt, const vk_tensor* local_x,
+                   const vk_tensor* x, size_t n, size_t n_special,
+                   size_t embed, size_t view_count,
+                   const vk_tensor* norm_gamma, const vk_tensor* norm_beta,
+                   float eps, int cat_token, vk_tensor* feat, vk_tensor* cam);
+
+/* token_major_to_chw_with_optional_layernorm (dpt_head.rs:260-301): token
+ * rows tok [n_tok, c] to channel-major out [c, n_tok] (out[ch*n_tok + t]),
+ * each row LayerNorm'd first when gamma/beta are given (the head uses
+ * HEAD_NORM_EPS = 1e-5, dpt_head.rs:101).  Bit-identical to
+ * vk_layernorm_into_f32 followed by the transpose (the reference's
+ * materialised path, dpt_head.rs:513-518).  gamma/beta both NULL: transpose
+ * only.  out must not alias tok. */
+int vk_token_to_chw_f32(vk_runtime* rt, const vk_tensor* tok, size_t n_tok,
+                        size_t c, const vk_tensor* gamma,
+                        const vk_tensor* beta, float eps, vk_tensor* out);
+
+/* ------------------------------------------------------------------ */
 /* one ViT block's fused-op sequence                                    */
 /* ------------------------------------------------------------------ */
 

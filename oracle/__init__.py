@@ -394,3 +394,33 @@ def block_forward(tokens, params: dict, cfg: dict, layer_idx: int, gh: int, gw: 
     x = layerscale_residual(x, y, params.get("ls2"))
     return {"tokens": x, "q": q.reshape(H, rows, hd), "k": k.reshape(H, rows, hd),
             "v": v.reshape(H, rows, hd), "attn": attn, "ln2": ln2, "hidden": hidden}
+
+
+def capture(local_x, x, n: int, n_special: int, embed: int, view_count: int, norm_gamma,
+            norm_beta, eps: float, cat_token: bool):
+    """Backbone::post_process_capture (backbone.rs:1139-1179) per view of a
+    view-major batch: returns (feat [views, n_patch, W], cam [views, W]) with
+    W = 2*embed (cat_token: [local row | LN(x row)], cam [local row 0 | x
+    row 0]) or embed (LN(x row), cam x row 0)."""
+    xv = _f32(x).reshape(view_count, n, embed)
+    feats, cams = [], []
+    for v in range(view_count):
+        normed = layernorm(xv[v, n_special:], norm_gamma, norm_beta, eps)
+        if cat_token:
+            lv = _f32(local_x).reshape(view_count, n, embed)[v]
+            feats.append(np.concatenate([lv[n_special:], normed], axis=1))
+            cams.append(np.concatenate([lv[0], xv[v, 0]]))
+        else:
+            feats.append(normed)
+            cams.append(xv[v, 0].copy())
+    return np.stack(feats), np.stack(cams)
+
+
+def token_to_chw(tok, n_tok: int, c: int, gamma=None, beta=None, eps: float = 1e-5):
+    """The head's materialised hand-off (dpt_head.rs:513-518): scalar
+    LayerNorm of every token row (when gamma/beta are given), then
+    tok_major_to_chw, out[ch, t] = tok[t, ch]."""
+    t = _f32(tok).reshape(n_tok, c)
+    if gamma is not None:
+        t = layernorm(t, gamma, beta, eps)
+    return np.ascontiguousarray(t.T)

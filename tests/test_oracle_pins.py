@@ -457,3 +457,40 @@ def test_block_forward_matches_float64_twin(rng):
             nols = {k: v for k, v in p.items() if k not in ("ls1", "ls2")}
             wrong = block_f64(x0, nols, cfg, layer, gh, gw, views, cam)
             assert np.abs(got["tokens"] - wrong["tokens"]).max() > 1e-2
+
+
+# ---------------------------------------------------------------- capture / head hand-off
+def test_capture_layout_rules(rng):
+    """backbone.rs:1287-1372: cat_token -> feat [n_patch, 2*embed] and cam
+    [2*embed]; without it -> [n_patch, embed] and [embed]; the normalised half
+    is the scalar LayerNorm of the patch rows."""
+    D, n, ns = 8, 5, 1  # 1 CLS + 2x2 patch grid, as the reference's tests
+    x, local = rng.standard_normal((n, D)).astype(np.float32), \
+        rng.standard_normal((n, D)).astype(np.float32)
+    g, b = np.ones(D, np.float32), np.zeros(D, np.float32)
+    feat, cam = oracle.capture(local, x, n, ns, D, 1, g, b, 1e-6, True)
+    assert feat.shape == (1, 4, 2 * D) and cam.shape == (1, 2 * D)
+    assert np.array_equal(feat[0, :, :D], local[1:]) and np.array_equal(cam[0, :D], local[0])
+    assert np.array_equal(cam[0, D:], x[0])
+    normed = feat[0, :, D:].astype(np.float64)
+    assert np.allclose(normed.mean(axis=1), 0, atol=1e-6)
+    assert np.allclose(normed.var(axis=1), 1, atol=1e-4)
+    feat1, cam1 = oracle.capture(None, x, n, ns, D, 1, g, b, 1e-6, False)
+    assert feat1.shape == (1, 4, D) and np.array_equal(feat1[0], feat[0, :, D:])
+    assert np.array_equal(cam1[0], x[0])
+
+
+def test_token_to_chw_reference_vectors_and_layout():
+    """dpt_head.rs:1041-1070 vectors: exact binary inputs; out[ch, t] is the
+    LayerNorm'd tok[t, ch] (eps HEAD_NORM_EPS = 1e-5, dpt_head.rs:101)."""
+    n_tok, c = 35, 16
+    tok = ((np.arange(n_tok * c) * 37 % 251).astype(np.float32) - 125.0) * 0.0078125
+    g = (0.5 + np.arange(c) * 0.03125).astype(np.float32)
+    b = (-0.25 + np.arange(c) * 0.015625).astype(np.float32)
+    out = oracle.token_to_chw(tok, n_tok, c, g, b, 1e-5)
+    t64 = tok.reshape(n_tok, c).astype(np.float64)
+    m = t64.mean(axis=1, keepdims=True)
+    ref = ((t64 - m) / np.sqrt(((t64 - m) ** 2).mean(axis=1, keepdims=True) + 1e-5) * g + b).T
+    assert out.shape == (c, n_tok)
+    assert np.max(np.abs(out - ref)) < 1e-5
+    assert np.array_equal(oracle.token_to_chw(tok, n_tok, c), tok.reshape(n_tok, c).T)

@@ -208,6 +208,57 @@ __device__ __forceinline__ uint32_t fmod_(uint32_t n, const FastDivU32& f) {
   return n - fdiv(n, f) * f.d;
 }
 
+// Mean and 1/sqrt(var + eps) of one row held by a wave as NV float4 per lane
+// (lane l holds float4 l + 64 i of the row): sum in i order, wave tree,
+// then the two-pass biased variance over the same registers.  Every
+// LayerNorm of a full row (block LayerNorm, the fused LayerScale+residual
+// form, the backbone's capture and the head's token->CHW hand-off) goes
+// through here, so they all give the same bits for the same row.  !EXACT:
+// float4 slots at or beyond cols/4 hold zeros and are left out.
+template <int NV, bool EXACT>
+__device__ __forceinline__ void row_mean_inv(const float4 (&v)[NV], int lane, int cols, float eps,
+                                             float* mean_out, float* inv_out) {
+  const int nvec = cols >> 2;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (EXACT || lane + i * 64 < nvec) {
+      s += v[i].x;
+      s += v[i].y;
+      s += v[i].z;
+      s += v[i].w;
+    }
+  }
+  s = wave_sum(s);
+  const float mean = s / static_cast<float>(cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (EXACT || lane + i * 64 < nvec) {
+      float d;
+      d = v[i].x - mean; q += d * d;
+      d = v[i].y - mean; q += d * d;
+      d = v[i].z - mean; q += d * d;
+      d = v[i].w - mean; q += d * d;
+    }
+  }
+  q = wave_sum(q);
+  const float var = q / static_cast<float>(cols);
+  *mean_out = mean;
+  *inv_out = 1.0f / sqrtf(var + eps);
+}
+
+// (v - mean) * inv * gamma + beta, each step rounded: the per-element
+// LayerNorm output of the scalar reference order.
+__device__ __forceinline__ float4 ln_apply4(float4 v, float mean, float inv, float4 g, float4 b) {
+  float4 o;
+  o.x = (v.x - mean) * inv * g.x + b.x;
+  o.y = (v.y - mean) * inv * g.y + b.y;
+  o.z = (v.z - mean) * inv * g.z + b.z;
+  o.w = (v.w - mean) * inv * g.w + b.w;
+  return o;
+}
+
 // Streaming (nontemporal) 128-bit loads and stores for activations that are
 // touched once per kernel: they keep the stream from displacing reusable
 // lines in L2 and the Infinity Cache.  Parameter vectors use ordinary loads.

@@ -42,50 +42,20 @@ __global__ __launch_bounds__(64) void layernorm_rows(const float* x, float* y,
   const int nvec = cols >> 2;
   const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
   float4 v[NV];
-  float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
-    if (EXACT || c < nvec) {
-      v[i] = vkd::ld_stream(xr + c);
-      s += v[i].x;
-      s += v[i].y;
-      s += v[i].z;
-      s += v[i].w;
-    } else {
-      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    v[i] = (EXACT || c < nvec) ? vkd::ld_stream(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  s = vkd::wave_sum(s);
-  const float mean = s / static_cast<float>(cols);
-  float q = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + i * 64;
-    if (EXACT || c < nvec) {
-      float d;
-      d = v[i].x - mean; q += d * d;
-      d = v[i].y - mean; q += d * d;
-      d = v[i].z - mean; q += d * d;
-      d = v[i].w - mean; q += d * d;
-    }
-  }
-  q = vkd::wave_sum(q);
-  const float var = q / static_cast<float>(cols);
-  const float inv = 1.0f / sqrtf(var + eps);
+  float mean, inv;
+  vkd::row_mean_inv<NV, EXACT>(v, lane, cols, eps, &mean, &inv);
   float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
     if (EXACT || c < nvec) {
-      const float4 g = Param<PT>::load4(gamma, c);
-      const float4 b = Param<PT>::load4(beta, c);
-      float4 o;
-      o.x = (v[i].x - mean) * inv * g.x + b.x;
-      o.y = (v[i].y - mean) * inv * g.y + b.y;
-      o.z = (v[i].z - mean) * inv * g.z + b.z;
-      o.w = (v[i].w - mean) * inv * g.w + b.w;
-      vkd::st_stream(yr + c, o);
+      vkd::st_stream(yr + c, vkd::ln_apply4(v[i], mean, inv, Param<PT>::load4(gamma, c),
+                                            Param<PT>::load4(beta, c)));
     }
   }
 }
@@ -107,7 +77,6 @@ __global__ __launch_bounds__(64) void ls_residual_layernorm_rows(
   float4* xr = reinterpret_cast<float4*>(x + base);
   const float4* yr = reinterpret_cast<const float4*>(yb + base);
   float4 v[NV];
-  float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
@@ -129,44 +98,19 @@ __global__ __launch_bounds__(64) void ls_residual_layernorm_rows(
       }
       vkd::st_stream(xr + c, a);
       v[i] = a;
-      s += a.x;
-      s += a.y;
-      s += a.z;
-      s += a.w;
     } else {
       v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  s = vkd::wave_sum(s);
-  const float mean = s / static_cast<float>(cols);
-  float q = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + i * 64;
-    if (EXACT || c < nvec) {
-      float d;
-      d = v[i].x - mean; q += d * d;
-      d = v[i].y - mean; q += d * d;
-      d = v[i].z - mean; q += d * d;
-      d = v[i].w - mean; q += d * d;
-    }
-  }
-  q = vkd::wave_sum(q);
-  const float var = q / static_cast<float>(cols);
-  const float inv = 1.0f / sqrtf(var + eps);
+  float mean, inv;
+  vkd::row_mean_inv<NV, EXACT>(v, lane, cols, eps, &mean, &inv);
   float4* outr = reinterpret_cast<float4*>(ln_out + base);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * 64;
     if (EXACT || c < nvec) {
-      const float4 g = Param<PT>::load4(gamma, c);
-      const float4 b = Param<PT>::load4(beta, c);
-      float4 o;
-      o.x = (v[i].x - mean) * inv * g.x + b.x;
-      o.y = (v[i].y - mean) * inv * g.y + b.y;
-      o.z = (v[i].z - mean) * inv * g.z + b.z;
-      o.w = (v[i].w - mean) * inv * g.w + b.w;
-      vkd::st_stream(outr + c, o);
+      vkd::st_stream(outr + c, vkd::ln_apply4(v[i], mean, inv, Param<PT>::load4(gamma, c),
+                                              Param<PT>::load4(beta, c)));
     }
   }
 }

@@ -149,6 +149,8 @@ _SIGS = {
     "vk_split_qkv_hnd_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp], _i),
     "vk_hnd_to_token_f32": ([_vp, _vp, _sz, _sz, _sz, _pp], _i),
     "vk_hnd_to_token_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp], _i),
+    "vk_capture_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _f, _i, _vp, _vp], _i),
+    "vk_token_to_chw_f32": ([_vp, _vp, _sz, _sz, _vp, _vp, _f, _vp], _i),
     "vk_attention_online_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz, _pp], _i),
     "vk_attention_into_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
@@ -430,6 +432,20 @@ class Runtime:
                               out: Tensor) -> None:
         _check(lib.vk_hnd_to_token_into_f32(self.handle, hnd.handle, rows, heads, head_dim,
                                             out.handle))
+
+    def capture_f32(self, local_x: Optional[Tensor], x: Tensor, n: int, n_special: int,
+                    embed: int, view_count: int, norm_gamma: Tensor, norm_beta: Tensor,
+                    eps: float, cat_token: bool, feat: Tensor, cam: Tensor) -> None:
+        """Backbone::post_process_capture for view_count view-major views."""
+        _check(lib.vk_capture_f32(self.handle, _h(local_x), x.handle, n, n_special, embed,
+                                  view_count, norm_gamma.handle, norm_beta.handle, eps,
+                                  1 if cat_token else 0, feat.handle, cam.handle))
+
+    def token_to_chw_f32(self, tok: Tensor, n_tok: int, c: int, gamma: Optional[Tensor],
+                         beta: Optional[Tensor], eps: float, out: Tensor) -> None:
+        """token_major_to_chw_with_optional_layernorm: [n_tok, c] -> [c, n_tok]."""
+        _check(lib.vk_token_to_chw_f32(self.handle, tok.handle, n_tok, c, _h(gamma), _h(beta),
+                                       eps, out.handle))
 
     def attention_online_f32(self, q: Tensor, k: Tensor, v: Tensor, heads: int, rows: int,
                              head_dim: int) -> Tensor:
