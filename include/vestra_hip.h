@@ -236,6 +236,33 @@ int vk_linear_prepare_f32(vk_runtime* rt, size_t in_features,
 int vk_linear_prepare_oihw_f32(vk_runtime* rt, size_t in_features,
                                size_t out_features, const float* weight_out_in,
                                const float* bias, vk_linear** out);
+/* The same from the weight as a GGUF file stores it: IEEE binary16
+ * (GGML_F16) or Q8_0 blocks (GGML_Q8_0: 34 bytes per 32 values, an f16
+ * scale d then 32 int8 q, value d*q; crates/da-gguf/src/q8_0.rs:10-33).
+ * The reference widens / dequantises at load (Gguf::tensor_f32,
+ * crates/da-gguf/src/reader.rs:279-349) and prepares the f32 values; here
+ * the stored bytes are uploaded and expanded on the device into the same
+ * resident f32 layout.  Both conversions are exact, so runs give the bits
+ * of vk_linear_prepare_f32 / _oihw_f32 on the widened weights.  Q8_0 needs
+ * in*out % 32 == 0 and nbytes == in*out/32*34.  bias / ls_gamma are f32. */
+int vk_linear_prepare_w16(vk_runtime* rt, size_t in_features,
+                          size_t out_features, const uint16_t* weight_in_out,
+                          const float* bias, const float* ls_gamma,
+                          vk_linear** out);
+int vk_linear_prepare_q8_0(vk_runtime* rt, size_t in_features,
+                           size_t out_features, const uint8_t* blocks,
+                           size_t nbytes, const float* bias,
+                           const float* ls_gamma, vk_linear** out);
+int vk_linear_prepare_oihw_w16(vk_runtime* rt, size_t in_features,
+                               size_t out_features,
+                               const uint16_t* weight_out_in,
+                               const float* bias, vk_linear** out);
+/* Gguf::tensor_f32 for F16 and Q8_0 tensors (reader.rs:302-337) on the
+ * device: dst f32 [len] from an f16 tensor, or from u8 Q8_0 blocks holding
+ * n values (n % 32 == 0). */
+int vk_widen_f16_f32(vk_runtime* rt, const vk_tensor* src, vk_tensor* dst);
+int vk_dequantize_q8_0_f32(vk_runtime* rt, const vk_tensor* blocks, size_t n,
+                           vk_tensor* dst);
 int vk_linear_destroy(vk_linear* lin);
 size_t vk_linear_input_features(const vk_linear* lin);
 /* CudaLinearF32::run(x, rows): y = (x @ W + b) [* gamma], F32 MFMA with f32

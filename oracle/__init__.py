@@ -424,3 +424,33 @@ def token_to_chw(tok, n_tok: int, c: int, gamma=None, beta=None, eps: float = 1e
     if gamma is not None:
         t = layernorm(t, gamma, beta, eps)
     return np.ascontiguousarray(t.T)
+
+
+Q8_0_BLOCK, Q8_0_BLOCK_BYTES = 32, 34
+
+
+def dequantize_q8_0(blocks, n: int) -> np.ndarray:
+    """q8_0::dequantize_q8_0 over read_blocks' wire layout (crates/da-gguf/src/
+    q8_0.rs:24-51): per 34-byte block a little-endian f16 scale d, then 32
+    int8 q; out[32*b + j] = f32(d) * f32(q_j) (exact in f32)."""
+    raw = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1, Q8_0_BLOCK_BYTES)
+    if raw.shape[0] * Q8_0_BLOCK != n:
+        raise ValueError(f"{raw.shape[0]} blocks do not hold {n} values")
+    d = f16_to_f32(raw[:, :2].copy().view("<u2").reshape(-1))
+    q = raw[:, 2:].view(np.int8).astype(np.float32)
+    return (d[:, None] * q).astype(np.float32).reshape(-1)
+
+
+def quantize_q8_0(x) -> np.ndarray:
+    """Test-input helper: ggml's Q8_0 quantisation (d = amax/127 rounded to
+    f16, q = round(x/d)) into the 34-byte wire layout."""
+    v = _f32(x).reshape(-1, Q8_0_BLOCK).astype(np.float64)
+    amax = np.abs(v).max(axis=1)
+    d = (amax / 127.0).astype(np.float16)
+    dd = d.astype(np.float64)
+    inv = np.where(dd > 0, 1.0 / np.where(dd > 0, dd, 1.0), 0.0)
+    q = np.clip(np.rint(v * inv[:, None]), -127, 127).astype(np.int8)
+    out = np.empty((v.shape[0], Q8_0_BLOCK_BYTES), np.uint8)
+    out[:, :2] = d.view(np.uint16).astype("<u2").view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out.reshape(-1)

@@ -494,3 +494,30 @@ def test_token_to_chw_reference_vectors_and_layout():
     assert out.shape == (c, n_tok)
     assert np.max(np.abs(out - ref)) < 1e-5
     assert np.array_equal(oracle.token_to_chw(tok, n_tok, c), tok.reshape(n_tok, c).T)
+
+
+# ---------------------------------------------------------------- GGUF Q8_0 weights
+def test_q8_0_reference_block():
+    """crates/da-gguf/tests/q8_0_roundtrip.rs: d = 0.5, q = -16..15 -> d*q."""
+    blk = np.empty(34, np.uint8)
+    blk[:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    out = oracle.dequantize_q8_0(blk, 32)
+    assert np.array_equal(out, 0.5 * (np.arange(32) - 16).astype(np.float32))
+
+
+def test_q8_0_layout_and_round_trip(rng):
+    """Wire layout (little-endian f16 scale, then int8, 34 bytes per block;
+    q8_0.rs:36-51) and the quantise/dequantise round trip within d/2."""
+    x = rng.standard_normal(32 * 40).astype(np.float32) * 0.02
+    raw = oracle.quantize_q8_0(x)
+    assert raw.size == 40 * 34
+    back = oracle.dequantize_q8_0(raw, x.size)
+    d = np.frombuffer(raw.reshape(40, 34)[:, :2].tobytes(), "<f2").astype(np.float64)
+    assert np.all(np.abs(back - x).reshape(40, 32) <= d[:, None] / 2 + 1e-12)
+    # a byte-swapped scale is a different tensor
+    swapped = raw.reshape(40, 34).copy()
+    swapped[:, [0, 1]] = swapped[:, [1, 0]]
+    assert not np.array_equal(oracle.dequantize_q8_0(swapped, x.size), back)
+    with pytest.raises(ValueError):
+        oracle.dequantize_q8_0(raw, x.size + 32)

@@ -135,6 +135,11 @@ _SIGS = {
     "vk_patchify_nchw_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _pp], _i),
     "vk_linear_prepare_f32": ([_vp, _sz, _sz, _vp, _vp, _vp, _pp], _i),
     "vk_linear_prepare_oihw_f32": ([_vp, _sz, _sz, _vp, _vp, _pp], _i),
+    "vk_linear_prepare_w16": ([_vp, _sz, _sz, _vp, _vp, _vp, _pp], _i),
+    "vk_linear_prepare_q8_0": ([_vp, _sz, _sz, _vp, _sz, _vp, _vp, _pp], _i),
+    "vk_linear_prepare_oihw_w16": ([_vp, _sz, _sz, _vp, _vp, _pp], _i),
+    "vk_widen_f16_f32": ([_vp, _vp, _vp], _i),
+    "vk_dequantize_q8_0_f32": ([_vp, _vp, _sz, _vp], _i),
     "vk_linear_destroy": ([_vp], _i),
     "vk_linear_input_features": ([_vp], _sz),
     "vk_linear_run_f32": ([_vp, _vp, _vp, _sz, _pp], _i),
@@ -539,6 +544,44 @@ class Runtime:
         _check(lib.vk_linear_prepare_oihw_f32(self.handle, in_features, out_features, _ptr(w),
                                               _ptr(b), C.byref(out)))
         return Linear(self, out)
+
+    def prepare_linear_w16(self, in_features: int, out_features: int, weight_f16: np.ndarray,
+                           bias: np.ndarray, ls_gamma: Optional[np.ndarray] = None) -> Linear:
+        """prepare_linear_f32 from a GGUF F16 [in, out] weight, widened on the device."""
+        w = np.ascontiguousarray(weight_f16, dtype=np.float16).reshape(-1).view(np.uint16)
+        b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        g = None if ls_gamma is None else np.ascontiguousarray(ls_gamma, dtype=np.float32)
+        out = C.c_void_p()
+        _check(lib.vk_linear_prepare_w16(self.handle, in_features, out_features, _ptr(w), _ptr(b),
+                                         None if g is None else _ptr(g), C.byref(out)))
+        return Linear(self, out)
+
+    def prepare_linear_q8_0(self, in_features: int, out_features: int, blocks: np.ndarray,
+                            bias: np.ndarray, ls_gamma: Optional[np.ndarray] = None) -> Linear:
+        """prepare_linear_f32 from GGUF Q8_0 blocks of an [in, out] weight."""
+        raw = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+        b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        g = None if ls_gamma is None else np.ascontiguousarray(ls_gamma, dtype=np.float32)
+        out = C.c_void_p()
+        _check(lib.vk_linear_prepare_q8_0(self.handle, in_features, out_features, _ptr(raw),
+                                          raw.size, _ptr(b), None if g is None else _ptr(g),
+                                          C.byref(out)))
+        return Linear(self, out)
+
+    def prepare_linear_oihw_w16(self, in_features: int, out_features: int,
+                                weight_oihw_f16: np.ndarray, bias: np.ndarray) -> Linear:
+        w = np.ascontiguousarray(weight_oihw_f16, dtype=np.float16).reshape(-1).view(np.uint16)
+        b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        out = C.c_void_p()
+        _check(lib.vk_linear_prepare_oihw_w16(self.handle, in_features, out_features, _ptr(w),
+                                              _ptr(b), C.byref(out)))
+        return Linear(self, out)
+
+    def widen_f16_f32(self, src: Tensor, dst: Tensor) -> None:
+        _check(lib.vk_widen_f16_f32(self.handle, src.handle, dst.handle))
+
+    def dequantize_q8_0_f32(self, blocks: Tensor, n: int, dst: Tensor) -> None:
+        _check(lib.vk_dequantize_q8_0_f32(self.handle, blocks.handle, n, dst.handle))
 
     def prepend_cls_add_pos_f32(self, patches: Tensor, cls: Tensor, pos: Tensor,
                                 n_patches: int, embed: int) -> Tensor:
