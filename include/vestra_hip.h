@@ -108,6 +108,8 @@ int vk_write_f32(vk_runtime* rt, vk_tensor* t, const float* host, size_t len);
 int vk_write_u8(vk_runtime* rt, vk_tensor* t, const uint8_t* host, size_t len);
 /* CudaRuntime::download_f32 (vit_block.rs:370, 659-662). Blocks. */
 int vk_download_f32(vk_runtime* rt, const vk_tensor* t, float* host, size_t len);
+/* The same for u8 tensors (images). Blocks. */
+int vk_download_u8(vk_runtime* rt, const vk_tensor* t, uint8_t* host, size_t len);
 /* CudaRuntime::copy_f32 (backbone.rs:991-1027). New tensor. */
 int vk_copy_f32(vk_runtime* rt, const vk_tensor* src, vk_tensor** out);
 /* CudaRuntime::copy_segment_f32: new tensor = src[offset .. offset+len]. */
@@ -369,6 +371,50 @@ int vk_prepend_cls_add_pos_f32(vk_runtime* rt, const vk_tensor* patches,
 int vk_pos_embed_bicubic_f32(vk_runtime* rt, const vk_tensor* pos_embed,
                              size_t grid, size_t embed, size_t gh, size_t gw,
                              float interp_offset, vk_tensor** out);
+
+/* ------------------------------------------------------------------ */
+/* image preprocessing                                                  */
+/* ------------------------------------------------------------------ */
+
+/* Resamplers of crates/da-engine/src/preprocess.rs on u8 HWC RGB images:
+ * resize_bilinear_u8 (253-280), resize_cubic_u8 (Keys a = -0.75, 282-338)
+ * and resize_area_u8 (box taps of area_table, 347-409; bilinear when no
+ * axis shrinks).  Bit-identical to the scalar path (same f32/f64 operation
+ * order, round half to even, saturate). */
+typedef enum vk_resize_mode {
+  VK_RESIZE_BILINEAR = 0,
+  VK_RESIZE_CUBIC = 1,
+  VK_RESIZE_AREA = 2
+} vk_resize_mode;
+
+/* Bytes of device workspace vk_resize_u8 needs (0: none). */
+size_t vk_resize_workspace_bytes(size_t sh, size_t sw, size_t dh, size_t dw,
+                                 int mode);
+/* dst [dh, dw, 3] u8 from src [sh, sw, 3] u8.  workspace: any tensor of at
+ * least vk_resize_workspace_bytes bytes (may be NULL when that is 0). */
+int vk_resize_u8(vk_runtime* rt, const vk_tensor* src, size_t sh, size_t sw,
+                 vk_tensor* dst, size_t dh, size_t dw, int mode,
+                 vk_tensor* workspace);
+
+/* The resize half of preprocess (preprocess.rs:432-469): the bound side
+ * (the longer one when upper_bound != 0, else the shorter: "lower*" modes)
+ * scaled to image_size with sizes rounded half to even, cubic when enlarging
+ * and area otherwise, then both sides snapped to the nearest multiple of
+ * patch (a second resize).  vk_preprocess_shape gives the output size (host
+ * only); out is u8 [out_h, out_w, 3], the input of vk_patch_embed_u8. */
+int vk_preprocess_shape(size_t h, size_t w, size_t image_size, size_t patch,
+                        int upper_bound, size_t* out_h, size_t* out_w);
+size_t vk_preprocess_workspace_bytes(size_t h, size_t w, size_t image_size,
+                                     size_t patch, int upper_bound);
+int vk_preprocess_resize_u8(vk_runtime* rt, const vk_tensor* src, size_t h,
+                            size_t w, size_t image_size, size_t patch,
+                            int upper_bound, vk_tensor* workspace,
+                            vk_tensor* out);
+/* The normalisation half (preprocess.rs:471-482): u8 HWC -> f32 NCHW,
+ * (v/255 - mean[c]) / std[c] -- the input of vk_patchify_nchw_f32. */
+int vk_normalize_u8_hwc_nchw_f32(vk_runtime* rt, const vk_tensor* src,
+                                 size_t h, size_t w, const float mean[3],
+                                 const float std_[3], vk_tensor* out);
 
 /* The whole per-image token preparation in one kernel: u8 HWC image ->
  * ImageNet-style normalisation (preprocess.rs:484-500) -> 14x14 unfold ->

@@ -64,6 +64,11 @@ _SIGS = {
     "ora_split_qkv_hnd": ([_vp, _sz, _sz, _sz, _vp, _vp, _vp], None),
     "ora_hnd_to_token": ([_vp, _sz, _sz, _sz, _vp], None),
     "ora_attention_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], None),
+    "ora_resize_bilinear_u8": ([_vp, _sz, _sz, _vp, _sz, _sz], None),
+    "ora_resize_cubic_u8": ([_vp, _sz, _sz, _vp, _sz, _sz], None),
+    "ora_resize_area_u8": ([_vp, _sz, _sz, _vp, _sz, _sz], None),
+    "ora_preprocess_shape": ([_sz, _sz, _sz, _sz, _i, _vp], _i),
+    "ora_preprocess_resize_u8": ([_vp, _sz, _sz, _sz, _sz, _i, _vp], None),
 }
 for _n, (_a, _r) in _SIGS.items():
     _fn = getattr(lib, _n)
@@ -454,3 +459,32 @@ def quantize_q8_0(x) -> np.ndarray:
     out[:, :2] = d.view(np.uint16).astype("<u2").view(np.uint8).reshape(-1, 2)
     out[:, 2:] = q.view(np.uint8)
     return out.reshape(-1)
+
+
+def resize_u8(img_hwc, dh: int, dw: int, mode: str) -> np.ndarray:
+    """resize_{bilinear,cubic,area}_u8 (preprocess.rs:253-409) of a u8 HWC RGB image."""
+    img = np.ascontiguousarray(img_hwc, dtype=np.uint8)
+    sh, sw, _ = img.shape
+    out = np.empty((dh, dw, 3), np.uint8)
+    fn = {"bilinear": lib.ora_resize_bilinear_u8, "cubic": lib.ora_resize_cubic_u8,
+          "area": lib.ora_resize_area_u8}[mode]
+    fn(_p(img), sw, sh, _p(out), dw, dh)
+    return out
+
+
+def preprocess_shape(h: int, w: int, image_size: int, patch: int, upper_bound: bool = True):
+    """(boundary_h, boundary_w, out_h, out_w, scaled) of preprocess (preprocess.rs:432-469)."""
+    d = np.zeros(4, np.uint64)
+    scaled = lib.ora_preprocess_shape(h, w, image_size, patch, 1 if upper_bound else 0, _p(d))
+    return int(d[0]), int(d[1]), int(d[2]), int(d[3]), bool(scaled)
+
+
+def preprocess_resize_u8(img_hwc, image_size: int, patch: int, upper_bound: bool = True):
+    """preprocess's resize and patch snap (preprocess.rs:432-469): u8 HWC at the model size."""
+    img = np.ascontiguousarray(img_hwc, dtype=np.uint8)
+    h, w, _ = img.shape
+    _, _, oh, ow, _ = preprocess_shape(h, w, image_size, patch, upper_bound)
+    out = np.empty((oh, ow, 3), np.uint8)
+    lib.ora_preprocess_resize_u8(_p(img), h, w, image_size, patch, 1 if upper_bound else 0,
+                                 _p(out))
+    return out

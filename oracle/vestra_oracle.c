@@ -585,3 +585,211 @@ void ora_attention_f32(const float* q, const float* k, const float* v, size_t ba
     free(s);
   }
 }
+
+/* ---------------------------------------------------------------------------
+ * Image preprocessing resize (crates/da-engine/src/preprocess.rs:236-482).
+ * u8 HWC RGB in and out; f32 arithmetic where the reference uses f32, f64
+ * where it uses f64, every operation rounded; results rounded half-to-even
+ * and clamped to [0, 255] (saturating_round_u8, preprocess.rs:234-236).
+ * ------------------------------------------------------------------------- */
+static uint8_t sat_round_u8(float v) {
+  float r = rintf(v); /* default rounding mode: ties to even */
+  if (r < 0.0f) r = 0.0f;
+  if (r > 255.0f) r = 255.0f;
+  return (uint8_t)r;
+}
+
+/* cubic_weight, Keys a = -0.75 (preprocess.rs:240-251), f32. */
+static float cubic_w(float x) {
+  const float A = -0.75f;
+  x = fabsf(x);
+  if (x < 1.0f) return ((A + 2.0f) * x - (A + 3.0f)) * x * x + 1.0f;
+  if (x < 2.0f) return (((x - 5.0f) * x + 8.0f) * x - 4.0f) * A;
+  return 0.0f;
+}
+
+/* resize_bilinear_u8 (preprocess.rs:253-280). */
+void ora_resize_bilinear_u8(const uint8_t* src, size_t sw, size_t sh, uint8_t* dst, size_t dw,
+                            size_t dh) {
+  const float sx = (float)sw / (float)dw, sy = (float)sh / (float)dh;
+  for (size_t y = 0; y < dh; ++y) {
+    const float fy = ((float)y + 0.5f) * sy - 0.5f;
+    const long y0 = (long)floorf(fy);
+    const float wy = fy - (float)y0;
+    const size_t y0c = (size_t)clampl(y0, 0, (long)sh - 1), y1c = (size_t)clampl(y0 + 1, 0, (long)sh - 1);
+    for (size_t x = 0; x < dw; ++x) {
+      const float fx = ((float)x + 0.5f) * sx - 0.5f;
+      const long x0 = (long)floorf(fx);
+      const float wx = fx - (float)x0;
+      const size_t x0c = (size_t)clampl(x0, 0, (long)sw - 1), x1c = (size_t)clampl(x0 + 1, 0, (long)sw - 1);
+      for (size_t c = 0; c < 3; ++c) {
+        const float top = (float)src[(y0c * sw + x0c) * 3 + c] * (1.0f - wx) +
+                          (float)src[(y0c * sw + x1c) * 3 + c] * wx;
+        const float bottom = (float)src[(y1c * sw + x0c) * 3 + c] * (1.0f - wx) +
+                             (float)src[(y1c * sw + x1c) * 3 + c] * wx;
+        dst[(y * dw + x) * 3 + c] = sat_round_u8(top * (1.0f - wy) + bottom * wy);
+      }
+    }
+  }
+}
+
+/* Taps of one output coordinate of the cubic resize: fx in f64, the
+ * fractional part rounded to f32, weights in f32 (preprocess.rs:286-300). */
+static void cubic_taps(size_t d, double s, size_t n_src, long idx[4], float w[4]) {
+  const double f = ((double)d + 0.5) * s - 0.5;
+  const long i = (long)floor(f);
+  const float t = (float)(f - (double)i);
+  w[0] = cubic_w(t + 1.0f);
+  w[1] = cubic_w(t);
+  w[2] = cubic_w(t - 1.0f);
+  w[3] = cubic_w(t - 2.0f);
+  for (int k = 0; k < 4; ++k) idx[k] = clampl(i - 1 + k, 0, (long)n_src - 1);
+}
+
+/* resize_cubic_u8 (preprocess.rs:282-338): horizontal pass over every source
+ * row into f32, then the vertical pass, each a 4-tap sum from 0 in tap
+ * order. */
+void ora_resize_cubic_u8(const uint8_t* src, size_t sw, size_t sh, uint8_t* dst, size_t dw,
+                         size_t dh) {
+  const double sx = (double)sw / (double)dw, sy = (double)sh / (double)dh;
+  float* tmp = (float*)malloc(sh * dw * 3 * sizeof(float));
+  for (size_t x = 0; x < dw; ++x) {
+    long ix[4];
+    float wx[4];
+    cubic_taps(x, sx, sw, ix, wx);
+    for (size_t y = 0; y < sh; ++y)
+      for (size_t c = 0; c < 3; ++c) {
+        float sum = 0.0f;
+        for (int k = 0; k < 4; ++k) sum += wx[k] * (float)src[(y * sw + (size_t)ix[k]) * 3 + c];
+        tmp[(y * dw + x) * 3 + c] = sum;
+      }
+  }
+  for (size_t y = 0; y < dh; ++y) {
+    long iy[4];
+    float wy[4];
+    cubic_taps(y, sy, sh, iy, wy);
+    for (size_t x = 0; x < dw; ++x)
+      for (size_t c = 0; c < 3; ++c) {
+        float sum = 0.0f;
+        for (int k = 0; k < 4; ++k) sum += wy[k] * tmp[((size_t)iy[k] * dw + x) * 3 + c];
+        dst[(y * dw + x) * 3 + c] = sat_round_u8(sum);
+      }
+  }
+  free(tmp);
+}
+
+/* area_table taps of one destination (preprocess.rs:347-382), in the
+ * reference's order; returns the count (at most cap). */
+static int area_taps(size_t d, size_t n_src, size_t n_dst, long* src, float* w, int cap) {
+  const double scale = (double)n_src / (double)n_dst;
+  const double start_f = (double)d * scale;
+  const double end_f = start_f + scale;
+  const double cell = fmin(scale, (double)n_src - start_f);
+  size_t start = (size_t)ceil(start_f);
+  size_t end = (size_t)floor(end_f);
+  if (end > n_src - 1) end = n_src - 1;
+  if (start > end) start = end;
+  int n = 0;
+  if ((double)start - start_f > 1e-3 && n < cap) {
+    src[n] = (long)start - 1;
+    w[n++] = (float)(((double)start - start_f) / cell);
+  }
+  for (size_t s = start; s < end && n < cap; ++s) {
+    src[n] = (long)s;
+    w[n++] = (float)(1.0 / cell);
+  }
+  if (end_f - (double)end > 1e-3 && n < cap) {
+    src[n] = (long)end;
+    w[n++] = (float)(fmin(fmin(end_f - (double)end, 1.0), cell) / cell);
+  }
+  return n;
+}
+
+/* resize_area_u8 (preprocess.rs:384-409): bilinear when neither axis shrinks,
+ * else the separable box filter, sums from 0 in tap order. */
+void ora_resize_area_u8(const uint8_t* src, size_t sw, size_t sh, uint8_t* dst, size_t dw,
+                        size_t dh) {
+  if (dw >= sw && dh >= sh) {
+    ora_resize_bilinear_u8(src, sw, sh, dst, dw, dh);
+    return;
+  }
+  enum { CAP = 4096 };
+  long* ts = (long*)malloc(CAP * sizeof(long));
+  float* tw = (float*)malloc(CAP * sizeof(float));
+  float* tmp = (float*)calloc(sh * dw * 3, sizeof(float));
+  for (size_t x = 0; x < dw; ++x) {
+    const int n = area_taps(x, sw, dw, ts, tw, CAP);
+    for (size_t y = 0; y < sh; ++y)
+      for (size_t c = 0; c < 3; ++c) {
+        float acc = 0.0f;
+        for (int k = 0; k < n; ++k) acc += tw[k] * (float)src[(y * sw + (size_t)ts[k]) * 3 + c];
+        tmp[(y * dw + x) * 3 + c] = acc;
+      }
+  }
+  for (size_t y = 0; y < dh; ++y) {
+    const int n = area_taps(y, sh, dh, ts, tw, CAP);
+    for (size_t x = 0; x < dw; ++x)
+      for (size_t c = 0; c < 3; ++c) {
+        float acc = 0.0f;
+        for (int k = 0; k < n; ++k) acc += tw[k] * tmp[((size_t)ts[k] * dw + x) * 3 + c];
+        dst[(y * dw + x) * 3 + c] = sat_round_u8(acc);
+      }
+  }
+  free(ts);
+  free(tw);
+  free(tmp);
+}
+
+static size_t nearest_multiple(size_t v, size_t m) {
+  const size_t down = v / m * m, up = down + m;
+  const size_t du = up - v, dd = v - down;
+  return du <= dd ? up : down;
+}
+
+/* preprocess's resize policy (preprocess.rs:432-469): the bound side (max
+ * for upper-bound modes, min for "lower*") to image_size, sizes rounded half
+ * to even, cubic when enlarging, area otherwise; then both sides snapped to
+ * the nearest patch multiple with a second resize.  dims_out = boundary h,
+ * w, output h, w.  Returns 0 when the scale is exactly 1 (plain copy). */
+int ora_preprocess_shape(size_t h, size_t w, size_t image_size, size_t patch, int upper_bound,
+                         size_t dims_out[4]) {
+  const size_t target = image_size ? image_size : 1, p = patch ? patch : 1;
+  const size_t bound = upper_bound ? (w > h ? w : h) : (w < h ? w : h);
+  const double scale = (double)target / (double)bound;
+  size_t bw = (size_t)nearbyint((double)w * scale), bh = (size_t)nearbyint((double)h * scale);
+  if (bw < 1) bw = 1;
+  if (bh < 1) bh = 1;
+  size_t ow = nearest_multiple(bw, p), oh = nearest_multiple(bh, p);
+  if (ow < 1) ow = 1;
+  if (oh < 1) oh = 1;
+  dims_out[0] = bh;
+  dims_out[1] = bw;
+  dims_out[2] = oh;
+  dims_out[3] = ow;
+  return fabs(scale - 1.0) < 2.220446049250313e-16 ? 0 : 1;
+}
+
+void ora_preprocess_resize_u8(const uint8_t* src, size_t h, size_t w, size_t image_size,
+                              size_t patch, int upper_bound, uint8_t* dst) {
+  size_t d[4];
+  const int scaled = ora_preprocess_shape(h, w, image_size, patch, upper_bound, d);
+  const size_t target = image_size ? image_size : 1;
+  const size_t bound = upper_bound ? (w > h ? w : h) : (w < h ? w : h);
+  const double scale = (double)target / (double)bound;
+  uint8_t* mid = (uint8_t*)malloc(d[0] * d[1] * 3);
+  if (!scaled)
+    memcpy(mid, src, h * w * 3);
+  else if (scale > 1.0)
+    ora_resize_cubic_u8(src, w, h, mid, d[1], d[0]);
+  else
+    ora_resize_area_u8(src, w, h, mid, d[1], d[0]);
+  if (d[2] != d[0] || d[3] != d[1]) {
+    if (d[3] > d[1] || d[2] > d[0])
+      ora_resize_cubic_u8(mid, d[1], d[0], dst, d[3], d[2]);
+    else
+      ora_resize_area_u8(mid, d[1], d[0], dst, d[3], d[2]);
+  } else {
+    memcpy(dst, mid, d[0] * d[1] * 3);
+  }
+  free(mid);
+}

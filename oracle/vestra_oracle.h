@@ -106,6 +106,17 @@ void ora_hnd_to_token(const float* hnd, size_t n, size_t heads, size_t head_dim,
 void ora_attention_f32(const float* q, const float* k, const float* v, size_t batches,
                        size_t n, size_t head_dim, float* out);
 
+void ora_resize_bilinear_u8(const uint8_t* src, size_t sw, size_t sh, uint8_t* dst, size_t dw,
+                            size_t dh);
+void ora_resize_cubic_u8(const uint8_t* src, size_t sw, size_t sh, uint8_t* dst, size_t dw,
+                         size_t dh);
+void ora_resize_area_u8(const uint8_t* src, size_t sw, size_t sh, uint8_t* dst, size_t dw,
+                        size_t dh);
+int ora_preprocess_shape(size_t h, size_t w, size_t image_size, size_t patch, int upper_bound,
+                         size_t dims_out[4]);
+void ora_preprocess_resize_u8(const uint8_t* src, size_t h, size_t w, size_t image_size,
+                              size_t patch, int upper_bound, uint8_t* dst);
+
 #ifdef __cplusplus
 }
 #endif

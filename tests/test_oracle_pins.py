@@ -521,3 +521,75 @@ def test_q8_0_layout_and_round_trip(rng):
     assert not np.array_equal(oracle.dequantize_q8_0(swapped, x.size), back)
     with pytest.raises(ValueError):
         oracle.dequantize_q8_0(raw, x.size + 32)
+
+
+# ---------------------------------------------------------------- preprocessing resize
+def test_preprocess_shape_reference_cases():
+    """preprocess.rs:541-612: 2x2 at image_size 4 / patch 2 -> 4x4; identity at
+    2; 427x640 at 504 / patch 14 -> 336x504 (upper bound); "lower*" modes
+    bound the short side."""
+    assert oracle.preprocess_shape(2, 2, 4, 2)[2:4] == (4, 4)
+    assert oracle.preprocess_shape(2, 2, 2, 2) == (2, 2, 2, 2, False)
+    assert oracle.preprocess_shape(427, 640, 504, 14)[2:4] == (336, 504)
+    assert oracle.preprocess_shape(3, 3, 4, 2)[2:4] == (4, 4)
+    bh, bw, oh, ow, _ = oracle.preprocess_shape(427, 640, 504, 14, upper_bound=False)
+    assert bh == 504 and (oh, ow) == (504, 756)
+    # ties of the boundary size round to even, snaps prefer the larger multiple
+    assert oracle.preprocess_shape(10, 5, 4, 1)[:2] == (4, 2)
+    assert oracle.preprocess_shape(7, 7, 7, 2)[2:4] == (8, 8)
+
+
+def test_preprocess_identity_is_a_copy(rng):
+    img = rng.integers(0, 256, (2, 2, 3), dtype=np.uint8)
+    assert np.array_equal(oracle.preprocess_resize_u8(img, 2, 2), img)
+
+
+@pytest.mark.parametrize("mode", ["bilinear", "cubic", "area"])
+def test_resize_constant_image_stays_constant(mode):
+    for (sh, sw, dh, dw) in ((5, 7, 13, 9), (40, 30, 7, 11), (336, 504, 336, 504)):
+        img = np.full((sh, sw, 3), (17, 128, 254), np.uint8)
+        out = oracle.resize_u8(img, dh, dw, mode)
+        assert np.array_equal(out, np.broadcast_to(img[:1, :1], out.shape)), (mode, sh, sw)
+
+
+def _torch_resize(img, dh, dw, mode):
+    torch = pytest.importorskip("torch")
+    t = torch.from_numpy(img.astype(np.float64)).permute(2, 0, 1)[None]
+    kw = {} if mode == "area" else {"align_corners": False}
+    r = torch.nn.functional.interpolate(t, size=(dh, dw), mode=mode, **kw)
+    return r[0].permute(1, 2, 0).numpy()
+
+
+@pytest.mark.parametrize("mode,torch_mode,shape", [
+    ("bilinear", "bilinear", (23, 31, 40, 57)), ("bilinear", "bilinear", (40, 57, 23, 31)),
+    ("cubic", "bicubic", (23, 31, 40, 57)), ("cubic", "bicubic", (48, 64, 36, 50)),
+    ("area", "area", (48, 60, 12, 20))])
+def test_resize_matches_torch_twins(rng, mode, torch_mode, shape):
+    """Half-pixel centres, clamp-to-edge taps, Keys a = -0.75 (torch's bicubic
+    uses the same kernel), and the box filter at integer factors: within one
+    u8 step of torch's float64 result (the reference rounds from f32)."""
+    sh, sw, dh, dw = shape
+    img = rng.integers(0, 256, (sh, sw, 3), dtype=np.uint8)
+    got = oracle.resize_u8(img, dh, dw, mode).astype(np.float64)
+    twin = np.clip(np.rint(_torch_resize(img, dh, dw, torch_mode)), 0, 255)
+    assert np.max(np.abs(got - twin)) <= 1.0
+
+
+def test_resize_area_matches_exact_box_integral(rng):
+    """Non-integer downscale: the area taps approximate the exact overlap
+    integral of each destination cell (preprocess.rs:347-382)."""
+    sh, sw, dh, dw = 37, 53, 10, 14
+    img = rng.integers(0, 256, (sh, sw, 3), dtype=np.uint8).astype(np.float64)
+
+    def box(n_src, n_dst):
+        m = np.zeros((n_dst, n_src))
+        s = n_src / n_dst
+        for d in range(n_dst):
+            a, b = d * s, (d + 1) * s
+            for i in range(int(np.floor(a)), min(n_src, int(np.ceil(b)))):
+                m[d, i] = max(0.0, min(b, i + 1) - max(a, i)) / s
+        return m
+
+    exact = np.einsum("yi,xj,ijc->yxc", box(sh, dh), box(sw, dw), img)
+    got = oracle.resize_u8(img.astype(np.uint8), dh, dw, "area").astype(np.float64)
+    assert np.max(np.abs(got - np.rint(exact))) <= 1.0

@@ -282,6 +282,16 @@ int vk_download_f32(vk_runtime* rt, const vk_tensor* t, float* host, size_t len)
   return VK_OK;
 }
 
+int vk_download_u8(vk_runtime* rt, const vk_tensor* t, uint8_t* host, size_t len) {
+  VK_REQUIRE(t != nullptr && (host != nullptr || len == 0), "null tensor or host pointer");
+  VK_REQUIRE(t->dtype == VK_U8, "download_u8 of a non-u8 tensor");
+  VK_REQUIRE(t->len == len, "length mismatch: tensor %zu, host %zu", t->len, len);
+  VK_TRY(bind(rt));
+  if (len > 0) VK_HIP(hipMemcpyAsync(host, t->ptr, len, hipMemcpyDeviceToHost, rt->stream));
+  VK_HIP(hipStreamSynchronize(rt->stream));
+  return VK_OK;
+}
+
 int vk_copy_f32(vk_runtime* rt, const vk_tensor* src, vk_tensor** out) {
   VK_REQUIRE(src != nullptr, "null source");
   return vk_copy_segment_f32(rt, src, 0, src->len, out);

@@ -31,6 +31,7 @@ VK_ERR_OOM = -4
 
 VK_F32, VK_F16, VK_U8 = 0, 1, 2
 VK_QK_HEADS_OUTER, VK_QK_VIEWS_OUTER = 0, 1
+VK_RESIZE_BILINEAR, VK_RESIZE_CUBIC, VK_RESIZE_AREA = 0, 1, 2
 
 VK_BLOCK_FUSE_LS_LN = 1
 VK_BLOCK_SKIP_LN1 = 2
@@ -115,6 +116,7 @@ _SIGS = {
     "vk_write_f32": ([_vp, _vp, _vp, _sz], _i),
     "vk_write_u8": ([_vp, _vp, _vp, _sz], _i),
     "vk_download_f32": ([_vp, _vp, _vp, _sz], _i),
+    "vk_download_u8": ([_vp, _vp, _vp, _sz], _i),
     "vk_copy_f32": ([_vp, _vp, _pp], _i),
     "vk_copy_segment_f32": ([_vp, _vp, _sz, _sz, _pp], _i),
     "vk_copy_segment_into_f32": ([_vp, _vp, _sz, _vp, _sz, _sz], _i),
@@ -156,6 +158,12 @@ _SIGS = {
     "vk_hnd_to_token_into_f32": ([_vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_capture_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _f, _i, _vp, _vp], _i),
     "vk_token_to_chw_f32": ([_vp, _vp, _sz, _sz, _vp, _vp, _f, _vp], _i),
+    "vk_resize_workspace_bytes": ([_sz, _sz, _sz, _sz, _i], _sz),
+    "vk_resize_u8": ([_vp, _vp, _sz, _sz, _vp, _sz, _sz, _i, _vp], _i),
+    "vk_preprocess_shape": ([_sz, _sz, _sz, _sz, _i, C.POINTER(_sz), C.POINTER(_sz)], _i),
+    "vk_preprocess_workspace_bytes": ([_sz, _sz, _sz, _sz, _i], _sz),
+    "vk_preprocess_resize_u8": ([_vp, _vp, _sz, _sz, _sz, _sz, _i, _vp, _vp], _i),
+    "vk_normalize_u8_hwc_nchw_f32": ([_vp, _vp, _sz, _sz, _vp, _vp, _vp], _i),
     "vk_attention_online_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz, _pp], _i),
     "vk_attention_into_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
@@ -378,6 +386,11 @@ class Runtime:
         _check(lib.vk_upload_u8(self.handle, _ptr(h), h.size, C.byref(out)))
         return Tensor(self, out)
 
+    def download_u8(self, t: Tensor) -> np.ndarray:
+        out = np.empty(len(t), dtype=np.uint8)
+        _check(lib.vk_download_u8(self.handle, t.handle, _ptr(out), out.size))
+        return out
+
     def download_f32(self, t: Tensor) -> np.ndarray:
         out = np.empty(len(t), dtype=np.float32)
         _check(lib.vk_download_f32(self.handle, t.handle, _ptr(out), out.size))
@@ -451,6 +464,46 @@ class Runtime:
         """token_major_to_chw_with_optional_layernorm: [n_tok, c] -> [c, n_tok]."""
         _check(lib.vk_token_to_chw_f32(self.handle, tok.handle, n_tok, c, _h(gamma), _h(beta),
                                        eps, out.handle))
+
+    def alloc_u8(self, n: int) -> Tensor:
+        out = C.c_void_p()
+        _check(lib.vk_tensor_alloc(self.handle, 2, n, C.byref(out)))
+        return Tensor(self, out)
+
+    def resize_u8(self, src: Tensor, sh: int, sw: int, dst: Tensor, dh: int, dw: int,
+                  mode: int) -> None:
+        """resize_{bilinear,cubic,area}_u8 of preprocess.rs on the device."""
+        need = int(lib.vk_resize_workspace_bytes(sh, sw, dh, dw, mode))
+        ws = self.alloc_u8(need) if need else None
+        _check(lib.vk_resize_u8(self.handle, src.handle, sh, sw, dst.handle, dh, dw, mode,
+                                _h(ws)))
+        self._keep = ws  # the workspace must outlive the queued kernels
+
+    def preprocess_shape(self, h: int, w: int, image_size: int, patch: int,
+                         upper_bound: bool = True):
+        oh, ow = _sz(), _sz()
+        _check(lib.vk_preprocess_shape(h, w, image_size, patch, 1 if upper_bound else 0,
+                                       C.byref(oh), C.byref(ow)))
+        return oh.value, ow.value
+
+    def preprocess_resize_u8(self, src: Tensor, h: int, w: int, image_size: int, patch: int,
+                             upper_bound: bool = True) -> Tensor:
+        """preprocess's resize + patch snap: a new u8 [out_h, out_w, 3] tensor."""
+        oh, ow = self.preprocess_shape(h, w, image_size, patch, upper_bound)
+        out = self.alloc_u8(oh * ow * 3)
+        need = int(lib.vk_preprocess_workspace_bytes(h, w, image_size, patch,
+                                                     1 if upper_bound else 0))
+        ws = self.alloc_u8(need) if need else None
+        _check(lib.vk_preprocess_resize_u8(self.handle, src.handle, h, w, image_size, patch,
+                                           1 if upper_bound else 0, _h(ws), out.handle))
+        self._keep = ws
+        return out
+
+    def normalize_u8_hwc_nchw_f32(self, src: Tensor, h: int, w: int, mean: Sequence[float],
+                                  std: Sequence[float], out: Tensor) -> None:
+        m = (C.c_float * 3)(*mean)
+        s = (C.c_float * 3)(*std)
+        _check(lib.vk_normalize_u8_hwc_nchw_f32(self.handle, src.handle, h, w, m, s, out.handle))
 
     def attention_online_f32(self, q: Tensor, k: Tensor, v: Tensor, heads: int, rows: int,
                              head_dim: int) -> Tensor:
