@@ -9,6 +9,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "vestra_hip.h"
 
@@ -24,6 +25,12 @@ struct vk_runtime {
   // head_dim): device pointer (owned by the runtime) and the largest
   // position the table covers.
   std::map<std::pair<uint32_t, int>, std::pair<float*, int>> rope_tables;
+  // Partial sums of split-K linears (f32).  Grown only outside stream
+  // capture; a replaced buffer is kept until the runtime is destroyed, since
+  // graphs captured earlier may still name it.
+  float* splitk = nullptr;
+  size_t splitk_len = 0;
+  std::vector<float*> splitk_retired;
 };
 
 struct vk_tensor {
@@ -92,6 +99,12 @@ struct LinearArgs {
   float* k_out;
   float* v_out;
   int a_hnd;     // 1: x is head-major [K/64, M, 64] (the attention output)
+  // split-K (linear.hip only): `splits` workgroups share each output tile,
+  // each over a contiguous run of 64-wide k chunks, writing raw sums to
+  // partial [splits, M, N]; a second pass adds them in split order and
+  // applies the epilogue.
+  int splits;
+  float* partial;
 };
 
 // Epilogues of the linear: v = acc + b (then * ls when the linear has one),

@@ -47,6 +47,29 @@ static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1 && PITCH >= KC, "pitch 4 x 
 
 enum Layout { kPlain = 0, kQkvHnd = 1, kAHnd = 2 };
 
+// One output element: v = acc + b (then * ls), each step rounded, through
+// the epilogue into the output layout.
+template <int EPI, int LAY>
+__device__ __forceinline__ void store_out(const LinearArgs& g, int row, int col, float acc,
+                                          float bias, float ls, float old) {
+  float v = acc + bias;
+  if (g.ls) v = v * ls;
+  float* o;
+  if constexpr (LAY == kQkvHnd) {
+    const int embed = g.N / 3;
+    const int which = col >= embed ? (col >= 2 * embed ? 2 : 1) : 0;
+    const int c = col - which * embed;
+    float* base = which == 0 ? g.q_out : (which == 1 ? g.k_out : g.v_out);
+    o = base + (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
+  } else {
+    o = g.out + static_cast<size_t>(row) * g.N + col;
+  }
+  if (EPI == kLinStore) *o = v;
+  if (EPI == kLinGelu) *o = vkd::gelu1<0>(v);
+  if (EPI == kLinGeluErf) *o = vkd::gelu1<1>(v);
+  if (EPI == kLinResidual) *o = old + v;
+}
+
 template <int EPI, int LAY>
 __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) {
   __shared__ __align__(16) float As[TM * PITCH];
@@ -57,8 +80,14 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
   const int gmt = (g.M + TM - 1) / TM;
+  const int gnt = (g.N + TN - 1) / TN;
   const int tile = vkd::xcd_tile(blockIdx.x, gridDim.x);
-  const int m0 = (tile % gmt) * TM, n0 = (tile / gmt) * TN;
+  const int m0 = (tile % gmt) * TM;
+  const int rest = tile / gmt;
+  const int n0 = (rest % gnt) * TN;
+  const int split = rest / gnt;
+  const int nch = (g.K + KC - 1) / KC;
+  const int c_begin = split * nch / g.splits, c_end = (split + 1) * nch / g.splits;
 
   f32x4 acc[2][4];
 #pragma unroll
@@ -70,7 +99,7 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
   const float* arow = As + (wm * 32 + (lane & 15)) * PITCH + kq;
   const float* brow = Bs + (wn * 64 + (lane & 15)) * PITCH + kq;
 
-  for (int k0 = 0; k0 < g.K; k0 += KC) {
+  for (int k0 = c_begin * KC; k0 < c_end * KC; k0 += KC) {
     // stage the chunk: slot f = tid + 512 i is row f/16, float4 f%16 of the
     // chunk (a wave reads four 256-byte row segments).  Loads are never
     // guarded: out-of-range slots read a clamped address and store zeros.
@@ -128,6 +157,22 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
     }
   }
 
+  // split-K: raw sums to this split's slice of the partial buffer
+  if (g.splits > 1) {
+    float* part = g.partial + static_cast<size_t>(split) * g.M * g.N;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
+          const int col = n0 + wn * 64 + u * 16 + (lane & 15);
+          if (row < g.M && col < g.N) part[static_cast<size_t>(row) * g.N + col] = acc[t][u][r];
+        }
+    return;
+  }
+
   // epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile.
   // Parameters and (for the residual) the old values are all loaded, on
   // clamped indices, before the first store.
@@ -162,62 +207,110 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
         const int col = n0 + wn * 64 + u * 16 + (lane & 15);
-        if (row < g.M && col < g.N) {
-          float v = acc[t][u][r] + bias[u];
-          if (g.ls) v = v * ls[u];
-          float* o;
-          if constexpr (LAY == kQkvHnd) {
-            const int embed = g.N / 3;
-            const int which = col >= embed ? (col >= 2 * embed ? 2 : 1) : 0;
-            const int c = col - which * embed;
-            float* base = which == 0 ? g.q_out : (which == 1 ? g.k_out : g.v_out);
-            o = base + (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
-          } else {
-            o = g.out + static_cast<size_t>(row) * g.N + col;
-          }
-          if (EPI == kLinStore) *o = v;
-          if (EPI == kLinGelu) *o = vkd::gelu1<0>(v);
-          if (EPI == kLinGeluErf) *o = vkd::gelu1<1>(v);
-          if (EPI == kLinResidual) *o = old[t][u][r] + v;
-        }
+        if (row < g.M && col < g.N)
+          store_out<EPI, LAY>(g, row, col, acc[t][u][r], bias[u], ls[u],
+                              EPI == kLinResidual ? old[t][u][r] : 0.0f);
       }
+}
+
+// Second pass of a split-K linear: one thread per 4 consecutive outputs of a
+// row; the splits' partial sums are added in split order, then the epilogue
+// of the single-pass kernel is applied.
+template <int EPI, int LAY>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
+  const long long i4 = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  const long long mn = static_cast<long long>(g.M) * g.N;
+  if (i4 * 4 >= mn) return;
+  const size_t e = static_cast<size_t>(i4) * 4;
+  const int row = static_cast<int>(e / g.N), col = static_cast<int>(e % g.N);
+  f32x4 acc = *reinterpret_cast<const f32x4*>(g.partial + e);
+  for (int sp = 1; sp < g.splits; ++sp)
+    acc = acc + *reinterpret_cast<const f32x4*>(g.partial + static_cast<size_t>(sp) * mn + e);
+  f32x4 old = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (EPI == kLinResidual) old = *reinterpret_cast<const f32x4*>(g.out + e);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    store_out<EPI, LAY>(g, row, col + j, acc[j], g.bias[col + j], g.ls ? g.ls[col + j] : 1.0f,
+                        old[j]);
 }
 
 }  // namespace
 
 namespace vk {
 
-int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi) {
+namespace {
+
+// Split count for a tile grid: at least one workgroup per CU when the rows
+// alone leave CUs idle (a single 866-token image), at least two k chunks per
+// split, at most 8 partial slices.
+int choose_splits(const vk_runtime* rt, long long tiles, int K) {
+  const int cus = rt->cu_count > 0 ? rt->cu_count : 256;
+  if (tiles >= cus) return 1;
+  const int nch = (K + KC - 1) / KC;
+  int s = static_cast<int>((static_cast<double>(cus) / static_cast<double>(tiles)) + 0.5);
+  if (s > nch / 2) s = nch / 2;
+  if (s > 8) s = 8;
+  return s < 1 ? 1 : s;
+}
+
+int ensure_splitk(vk_runtime* rt, size_t need) {
+  if (rt->splitk_len >= need) return VK_OK;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  VK_HIP(hipStreamIsCapturing(rt->stream, &st));
+  VK_REQUIRE(st == hipStreamCaptureStatusNone,
+             "linear: the split-K buffer must grow to %zu floats before stream capture "
+             "(run the sequence once eagerly first)", need);
+  size_t len = need > 2 * rt->splitk_len ? need : 2 * rt->splitk_len;
+  if (len < (size_t{8} << 20)) len = size_t{8} << 20;
+  float* p = nullptr;
+  VK_HIP(hipMalloc(reinterpret_cast<void**>(&p), len * sizeof(float)));
+  if (rt->splitk) rt->splitk_retired.push_back(rt->splitk);
+  rt->splitk = p;
+  rt->splitk_len = len;
+  return VK_OK;
+}
+
+template <int EPI, int LAY>
+void launch_pair(vk_runtime* rt, const LinearArgs& g, dim3 grid) {
+  hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY>), grid, dim3(kThreads), 0, rt->stream, g);
+  if (g.splits > 1) {
+    const long long n4 = static_cast<long long>(g.M) * g.N / 4;
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY>), dim3(static_cast<unsigned>((n4 + 255) / 256)),
+                       dim3(256), 0, rt->stream, g);
+  }
+}
+
+}  // namespace
+
+int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   const long long tiles =
-      static_cast<long long>((g.M + TM - 1) / TM) * static_cast<long long>((g.N + TN - 1) / TN);
-  VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "linear: %lld tiles", tiles);
-  const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
+      static_cast<long long>((g0.M + TM - 1) / TM) * static_cast<long long>((g0.N + TN - 1) / TN);
+  LinearArgs g = g0;
+  g.splits = choose_splits(rt, tiles, g.K);
+  g.partial = nullptr;
+  VK_UNSUPPORTED_IF(tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", tiles);
+  if (g.splits > 1) {
+    VK_REQUIRE(g.N % 4 == 0, "linear: split-K needs out_features % 4 == 0");
+    VK_TRY(ensure_splitk(rt, static_cast<size_t>(g.splits) * g.M * g.N));
+    g.partial = rt->splitk;
+  }
+  const dim3 grid(static_cast<unsigned>(tiles * g.splits));
   if (g.q_out) {
     VK_REQUIRE(epi == kLinStore, "linear: the Q|K|V split takes the store epilogue");
-    hipLaunchKernelGGL((linear_wide_kernel<kLinStore, kQkvHnd>), grid, block, 0, rt->stream, g);
+    launch_pair<kLinStore, kQkvHnd>(rt, g, grid);
   } else if (g.a_hnd) {
     if (epi == kLinResidual)
-      hipLaunchKernelGGL((linear_wide_kernel<kLinResidual, kAHnd>), grid, block, 0, rt->stream, g);
+      launch_pair<kLinResidual, kAHnd>(rt, g, grid);
     else if (epi == kLinStore)
-      hipLaunchKernelGGL((linear_wide_kernel<kLinStore, kAHnd>), grid, block, 0, rt->stream, g);
+      launch_pair<kLinStore, kAHnd>(rt, g, grid);
     else
       return set_error(VK_ERR_INVALID, "linear: head-major input takes store or residual");
   } else {
     switch (epi) {
-      case kLinStore:
-        hipLaunchKernelGGL((linear_wide_kernel<kLinStore, kPlain>), grid, block, 0, rt->stream, g);
-        break;
-      case kLinGelu:
-        hipLaunchKernelGGL((linear_wide_kernel<kLinGelu, kPlain>), grid, block, 0, rt->stream, g);
-        break;
-      case kLinGeluErf:
-        hipLaunchKernelGGL((linear_wide_kernel<kLinGeluErf, kPlain>), grid, block, 0, rt->stream,
-                           g);
-        break;
-      default:
-        hipLaunchKernelGGL((linear_wide_kernel<kLinResidual, kPlain>), grid, block, 0, rt->stream,
-                           g);
-        break;
+      case kLinStore: launch_pair<kLinStore, kPlain>(rt, g, grid); break;
+      case kLinGelu: launch_pair<kLinGelu, kPlain>(rt, g, grid); break;
+      case kLinGeluErf: launch_pair<kLinGeluErf, kPlain>(rt, g, grid); break;
+      default: launch_pair<kLinResidual, kPlain>(rt, g, grid); break;
     }
   }
   return check_launch("linear_wide_kernel");

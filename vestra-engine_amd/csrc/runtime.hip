@@ -185,6 +185,8 @@ int vk_runtime_destroy(vk_runtime* rt) {
   VK_TRY(bind(rt));
   (void)hipStreamSynchronize(rt->stream);
   for (auto& kv : rt->rope_tables) (void)hipFree(kv.second.first);
+  if (rt->splitk) (void)hipFree(rt->splitk);
+  for (float* p : rt->splitk_retired) (void)hipFree(p);
   (void)hipStreamDestroy(rt->stream);
   delete rt;
   return VK_OK;
