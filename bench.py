@@ -16,7 +16,10 @@ block (an upper bound of the work; DA3 starts both at layer 0 here).
 value = algorithmic bytes of every launched kernel / measured step time
 (GB/s).  The JSON line also carries us per block (12-view and single-image
 866-token), a per-operation table, the roofline of the dominant kernel and
-the oracle timed on the host cores as the CPU baseline.
+the oracle timed on the host cores as the CPU baseline, and -- beside the
+path -- the fused projection epilogues, the attention core and the whole
+device-resident block (projections and attention included) with their
+F32-MFMA rates.
 """
 import argparse
 import json
@@ -287,6 +290,65 @@ def linear_epilogue_timing(rt, rng, rows, iters):
     return out
 
 
+def full_block_timing(rt, rng, reps=3):
+    """The whole ViT block on the device (vk_vit_block_forward_f32: LN1, QKV
+    storing head-major Q/K/V, Q/K-norm + RoPE, attention, projection + LS +
+    residual, LN2, FC1 + GELU, FC2 + LS + residual), 12 ViT-B blocks with
+    random-init weights, local/global alternation from alt_start 4, captured
+    in one HIP graph: single image (866 tokens) and the 12-view sequence
+    (10,392 rows).  FLOP = the four projections (2*rows*D*(3D + D + 2M)) plus
+    attention (4*64*n^2 per head and sequence)."""
+    import vestra_hip as vh
+    cfg = vh.VitConfig(embed_dim=D, num_heads=H, head_dim=HD, mlp_hidden=M, num_register=NREG,
+                       ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0, rope_start=0,
+                       qknorm_start=0, alt_start=ALT)
+
+    def n(*sh, scale=1.0, shift=0.0):
+        return (shift + scale * rng.standard_normal(sh)).astype(np.float32)
+
+    keep, blocks = [], []
+    for _ in range(DEPTH):
+        vec = {"norm1_gamma": n(D, scale=0.02, shift=1), "norm1_beta": n(D, scale=0.02),
+               "norm2_gamma": n(D, scale=0.02, shift=1), "norm2_beta": n(D, scale=0.02),
+               "qnorm_gamma": n(HD, scale=0.02, shift=1), "qnorm_beta": n(HD, scale=0.02),
+               "knorm_gamma": n(HD, scale=0.02, shift=1), "knorm_beta": n(HD, scale=0.02)}
+        dev = {k: rt.upload_f32(v) for k, v in vec.items()}
+        lin = {"qkv": rt.prepare_linear_f32(D, 3 * D, n(D, 3 * D, scale=0.02),
+                                            n(3 * D, scale=0.02)),
+               "proj": rt.prepare_linear_f32(D, D, n(D, D, scale=0.02), n(D, scale=0.02),
+                                             rng.uniform(0, 0.1, D).astype(np.float32)),
+               "fc1": rt.prepare_linear_f32(D, M, n(D, M, scale=0.02), n(M, scale=0.02)),
+               "fc2": rt.prepare_linear_f32(M, D, n(M, D, scale=0.02), n(D, scale=0.02),
+                                            rng.uniform(0, 0.1, D).astype(np.float32))}
+        keep.append((dev, lin))
+        blocks.append(vh.block_weights_struct(**dev, **lin))
+    camera = rt.upload_f32(n(2 * D, scale=0.02))
+    out = {}
+    for name, views in (("single_image", 1), ("12view", 12)):
+        rows = TPV * views
+        tokens = rt.upload_f32(n(rows, D))
+        ws = rt.block_workspace(rows, D, M)
+
+        def step():
+            for i, w in enumerate(blocks):
+                rt.vit_block_forward_f32(cfg, i, w, tokens, GH, GW, views, camera, ws.struct)
+
+        step()  # builds the RoPE table before capture
+        graph = capture(rt, step)
+        graph.launch()
+        ms = statistics.median(time_loop(rt, graph.launch, 1) for _ in range(reps))
+        flop = 0.0
+        for i in range(DEPTH):
+            glob = i >= ALT and i % 2 == 1
+            seqs, seq_n = (H, rows) if glob else (H * views, TPV)
+            flop += 2.0 * rows * D * (4 * D + 2 * M) + 4.0 * HD * seq_n * seq_n * seqs
+        out[name] = {"rows": rows, "us_per_block": round(ms * 1e3 / DEPTH, 2),
+                     "ms_12_blocks": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 2),
+                     "frac_of_f32_mfma_peak": round(flop / ms / 1e9 / MFMA_F32_PEAK_TFLOPS, 4)}
+        del graph, ws, tokens
+    return out
+
+
 def attention_timing(rt, rng, iters):
     """The attention core (softmax(Q K^T / 8) V, F32 MFMA, online softmax) at
     the path's shapes: a local layer of the 12-view batch (144 sequences of
@@ -429,6 +491,9 @@ def main():
     ap.add_argument("--linear", action="store_true",
                     help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
                          "at the 12-view shape")
+    ap.add_argument("--full-block", action="store_true",
+                    help="whole-block mode: 12 complete ViT-B blocks on the device "
+                         "(projections and attention included), single image and 12 views")
     ap.add_argument("--attention", action="store_true",
                     help="attention mode: the attention core at the local, global and ViT-L "
                          "shapes")
@@ -454,6 +519,9 @@ def main():
             print(json.dumps({"views": views, "rows": rows, "rotate_sets": sets, "ops": table}),
                   flush=True)
             rt.synchronize()
+        return
+    if args.full_block:
+        print(json.dumps({"full_block": full_block_timing(rt, rng)}), flush=True)
         return
     if args.attention:
         print(json.dumps({"attention": attention_timing(rt, rng, args.op_iters)}), flush=True)
@@ -514,6 +582,9 @@ def main():
     gelu = ops12["gelu"]
     log("fused linear epilogues")
     linear = linear_epilogue_timing(rt, rng, model.rows, 10)
+    log("attention and whole blocks")
+    attention = attention_timing(rt, rng, 20)
+    full_block = full_block_timing(rt, rng)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -546,6 +617,8 @@ def main():
         "ops_single_image": ops1,
         "patch_embed": patch,
         "linear_epilogues": linear,
+        "attention": attention,
+        "full_block": full_block,
         "roofline": {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
                      "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
