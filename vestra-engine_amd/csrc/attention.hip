@@ -19,9 +19,16 @@
 //    is exactly the lane's four probabilities of that tile: P never leaves
 //    registers.  O's rows are queries 4(l/16) + r, so the per-query rescale
 //    factors reach them with four shuffles.
-// Q is read once per workgroup, pre-scaled by 1/sqrt(64) = 0.125 (exact).
-// Keys past n are masked to -inf; queries past n are computed on a clamped
-// row and not stored.
+// Scores are kept in the base-2 domain: Q is read once per workgroup and
+// pre-scaled by log2(e)/sqrt(64), so every softmax weight is one v_exp_f32
+// (2^x) of a difference of scores: p = 2^(s' - m') = e^(s - m).
+// Keys past n are masked to -inf (last block only); queries past n are
+// computed on a clamped row and not stored.
+//
+// Staging: K goes to LDS row-major with 128-bit stores (16 lanes fill one
+// 256-byte key row).  V is transposed on the way in; its loads are mapped so
+// that the 64 lanes of a wave hold 16 keys x 4 float4 columns, which makes
+// every transposed 32-bit store of the wave hit 64 distinct banks.
 #include <cmath>
 
 #include "common.h"
@@ -35,7 +42,9 @@ constexpr int QB = 64;  // queries per workgroup
 constexpr int KB = 64;  // keys per block
 constexpr int PITCH = 68;
 constexpr int kThreads = 256;
+constexpr float kQScale = 0.125f * 1.44269504088896341f;  // log2(e) / sqrt(64)
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1, "pitch 4 x odd");
+static_assert(PITCH % 16 == 4, "transposed V stores: 16 (l >> 4) + (l & 15) covers 64 banks");
 
 __device__ __forceinline__ float group_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, 64));
@@ -73,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* __rest
 #pragma unroll
     for (int bd = 0; bd < 4; ++bd) {
       const f32x4 t = *reinterpret_cast<const f32x4*>(qrow + 16 * bd);
-      qf[bd] = t * 0.125f;
+      qf[bd] = t * kQScale;
     }
   }
 
@@ -82,28 +91,33 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* __rest
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;  // statistics of query q0 + c16
 
-  const int skey = tid >> 4, sd = 4 * (tid & 15);  // staging slot: key, d
+  const int skey = tid >> 4, sd = 4 * (tid & 15);  // K staging slot: key, d
+  // V staging slot: key 16 w + (l & 15), float4 columns (l >> 4) + 4 i
+  const int vkey = 16 * wave + (lane & 15), vcol = lane >> 4;
   const float* karow = Ks + c16 * PITCH + 4 * g;
   const float* vtrow = Vt + c16 * PITCH + 4 * g;
 
   for (int k0 = 0; k0 < n; k0 += KB) {
     // stage: slot f = tid + 256 i is key f/16, float4 f%16 of the block
     f32x4 kr[4], vr[4];
+    {
+      const int vk = k0 + vkey < n ? k0 + vkey : n - 1;
+      const float* vrow = v + base + static_cast<size_t>(vk) * HD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = k0 + skey + 16 * i;
-      const int ck = key < n ? key : n - 1;
-      const size_t off = base + static_cast<size_t>(ck) * HD + sd;
-      kr[i] = *reinterpret_cast<const f32x4*>(k + off);
-      vr[i] = *reinterpret_cast<const f32x4*>(v + off);
+      for (int i = 0; i < 4; ++i) {
+        const int key = k0 + skey + 16 * i;
+        const int ck = key < n ? key : n - 1;
+        kr[i] = *reinterpret_cast<const f32x4*>(k + base + static_cast<size_t>(ck) * HD + sd);
+        vr[i] = *reinterpret_cast<const f32x4*>(vrow + 4 * (vcol + 4 * i));
+      }
     }
     __syncthreads();  // the previous block is consumed
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int kk = skey + 16 * i;
-      *reinterpret_cast<f32x4*>(Ks + kk * PITCH + sd) = kr[i];
+      *reinterpret_cast<f32x4*>(Ks + (skey + 16 * i) * PITCH + sd) = kr[i];
+      const int d = 4 * (vcol + 4 * i);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) Vt[(sd + c) * PITCH + kk] = vr[i][c];
+      for (int c = 0; c < 4; ++c) Vt[(d + c) * PITCH + vkey] = vr[i][c];
     }
     __syncthreads();
 
@@ -120,22 +134,26 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* __rest
           s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], qf[bd][j], s[t], 0, 0, 0);
       }
     }
+    if (k0 + KB > n) {  // the last, partial block
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (k0 + 16 * t + 4 * g + r >= n) s[t][r] = -INFINITY;
+    }
     float mb = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (k0 + 16 * t + 4 * g + r >= n) s[t][r] = -INFINITY;
-        mb = fmaxf(mb, s[t][r]);
-      }
+      for (int r = 0; r < 4; ++r) mb = fmaxf(mb, s[t][r]);
     const float m_new = fmaxf(m_run, group_max(mb));
-    const float alpha = expf(m_run - m_new);  // 0 on the first block
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block
     float ps = 0.0f;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        s[t][r] = expf(s[t][r] - m_new);
+        s[t][r] = __builtin_amdgcn_exp2f(s[t][r] - m_new);
         ps += s[t][r];
       }
     l_run = l_run * alpha + group_sum(ps);
