@@ -349,6 +349,125 @@ def full_block_timing(rt, rng, reps=3):
     return out
 
 
+# ViT-L 1008x672: 3,456 patches (48 x 72) + CLS + camera slot, D 1024,
+# 16 heads, MLP 4096, 24 blocks; parameters stored as IEEE binary16.  The
+# alternation start of this shape is not fixed by the reference's tests: 8.
+L_D, L_H, L_M, L_GH, L_GW, L_DEPTH, L_ALT = 1024, 16, 4096, 48, 72, 24, 8
+L_TPV = 1 + NREG + L_GH * L_GW  # 3458
+
+
+def vitl_fused_bytes(rows, plan):
+    """Algorithmic bytes of the ViT-L fused-op sequence, f16 parameter vectors."""
+    import vestra_hip as vh
+    w = 2
+    ln = 2 * rows * L_D * 4 + 2 * L_D * w
+    qk = 4 * L_H * rows * HD * 4 + 4 * HD * w
+    lsln = 4 * rows * L_D * 4 + 3 * L_D * w
+    ls = 3 * rows * L_D * 4 + L_D * w
+    gelu = 2 * rows * L_M * 4
+    total = 0
+    for i, flags in enumerate(plan):
+        if i == L_ALT:
+            total += 2 * L_D * 4
+        if not (flags & vh.VK_BLOCK_SKIP_LN1) or i == L_ALT:
+            total += ln
+        total += qk + lsln + gelu + (lsln if flags & vh.VK_BLOCK_FUSE_NEXT_LN1 else ls)
+    return total
+
+
+def vitl_timing(rt, rng, reps=3):
+    """The ViT-L 1008x672 configuration with F16-stored weights: the 24-block
+    fused-op sequence (parameter vectors in f16, widened in registers) and the
+    24 whole blocks on the device with the projection weights uploaded as
+    F16 and expanded on the device (vk_linear_prepare_w16)."""
+    import vestra_hip as vh
+    rows = L_TPV
+
+    def n(*sh, scale=1.0, shift=0.0):
+        return (shift + scale * rng.standard_normal(sh)).astype(np.float32)
+
+    def h16(a):
+        return rt.upload_f16(a.astype(np.float16))
+
+    cfg = vh.VitConfig(embed_dim=L_D, num_heads=L_H, head_dim=HD, mlp_hidden=L_M,
+                       num_register=NREG, ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0,
+                       rope_start=0, qknorm_start=0, alt_start=L_ALT)
+    vecs = []
+    for _ in range(L_DEPTH):
+        vecs.append({"norm1_gamma": h16(n(L_D, scale=0.02, shift=1)),
+                     "norm1_beta": h16(n(L_D, scale=0.02)),
+                     "qnorm_gamma": h16(n(HD, scale=0.02, shift=1)),
+                     "qnorm_beta": h16(n(HD, scale=0.02)),
+                     "knorm_gamma": h16(n(HD, scale=0.02, shift=1)),
+                     "knorm_beta": h16(n(HD, scale=0.02)),
+                     "norm2_gamma": h16(n(L_D, scale=0.02, shift=1)),
+                     "norm2_beta": h16(n(L_D, scale=0.02))})
+    camera = rt.upload_f32(n(2 * L_D, scale=0.02))
+    out = {"config": "vitl_1008x672_f16_weights", "rows": rows, "blocks": L_DEPTH,
+           "alt_start": L_ALT}
+
+    # fused-op sequence (projections / attention outputs are seeded tensors)
+    lsv = [{"ls1": h16(rng.uniform(0, 0.1, L_D).astype(np.float32)),
+            "ls2": h16(rng.uniform(0, 0.1, L_D).astype(np.float32))} for _ in range(L_DEPTH)]
+    structs = [vh.layer_struct(**v, **l) for v, l in zip(vecs, lsv)]
+    act = {"tokens": rt.upload_f32(n(rows, L_D)), "q": rt.upload_f32(n(rows * L_D)),
+           "k": rt.upload_f32(n(rows * L_D)), "attn_proj": rt.upload_f32(n(rows, L_D)),
+           "hidden": rt.upload_f32(n(rows, L_M)), "mlp_out": rt.upload_f32(n(rows, L_D)),
+           "ln1": rt.alloc_f32(rows * L_D), "ln2": rt.alloc_f32(rows * L_D)}
+    act_struct = vh.activations_struct(**act)
+    plan = block_plan(L_DEPTH, L_ALT)
+
+    def fused_step():
+        for i, flags in enumerate(plan):
+            nxt = structs[i + 1] if i + 1 < L_DEPTH else None
+            rt.vit_block_fused_ops(cfg, i, structs[i], nxt, act_struct, L_GH, L_GW, 1, camera,
+                                   flags)
+
+    fused_step()
+    graph = capture(rt, fused_step)
+    graph.launch()
+    ms = statistics.median(time_loop(rt, graph.launch, 1) for _ in range(reps * 3))
+    nbytes = vitl_fused_bytes(rows, plan)
+    out["fused_ops"] = {"us_per_block": round(ms * 1e3 / L_DEPTH, 2),
+                        "bytes_per_pass": int(nbytes),
+                        "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del graph, act, act_struct
+
+    # whole blocks, weights uploaded as F16
+    keep, blocks = [], []
+    for i in range(L_DEPTH):
+        ls1 = rng.uniform(0, 0.1, L_D).astype(np.float32)
+        ls2 = rng.uniform(0, 0.1, L_D).astype(np.float32)
+        lin = {"qkv": rt.prepare_linear_w16(L_D, 3 * L_D, n(L_D, 3 * L_D, scale=0.02),
+                                            n(3 * L_D, scale=0.02)),
+               "proj": rt.prepare_linear_w16(L_D, L_D, n(L_D, L_D, scale=0.02),
+                                             n(L_D, scale=0.02), ls1),
+               "fc1": rt.prepare_linear_w16(L_D, L_M, n(L_D, L_M, scale=0.02),
+                                            n(L_M, scale=0.02)),
+               "fc2": rt.prepare_linear_w16(L_M, L_D, n(L_M, L_D, scale=0.02),
+                                            n(L_D, scale=0.02), ls2)}
+        keep.append(lin)
+        blocks.append(vh.block_weights_struct(**vecs[i], **lin))
+    tokens = rt.upload_f32(n(rows, L_D))
+    ws = rt.block_workspace(rows, L_D, L_M)
+
+    def block_step():
+        for i, w in enumerate(blocks):
+            rt.vit_block_forward_f32(cfg, i, w, tokens, L_GH, L_GW, 1, camera, ws.struct)
+
+    block_step()
+    graph = capture(rt, block_step)
+    graph.launch()
+    ms = statistics.median(time_loop(rt, graph.launch, 1) for _ in range(reps))
+    flop = L_DEPTH * (2.0 * rows * L_D * (4 * L_D + 2 * L_M) + 4.0 * HD * rows * rows * L_H)
+    out["full_block"] = {"us_per_block": round(ms * 1e3 / L_DEPTH, 2),
+                         "ms_24_blocks": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 2),
+                         "frac_of_f32_mfma_peak": round(flop / ms / 1e9 / MFMA_F32_PEAK_TFLOPS,
+                                                        4)}
+    return out
+
+
 def attention_timing(rt, rng, iters):
     """The attention core (softmax(Q K^T / 8) V, F32 MFMA, online softmax) at
     the path's shapes: a local layer of the 12-view batch (144 sequences of
@@ -494,6 +613,9 @@ def main():
     ap.add_argument("--full-block", action="store_true",
                     help="whole-block mode: 12 complete ViT-B blocks on the device "
                          "(projections and attention included), single image and 12 views")
+    ap.add_argument("--vitl", action="store_true",
+                    help="ViT-L mode: the 1008x672 configuration with F16-stored weights "
+                         "(24-block fused ops and whole blocks)")
     ap.add_argument("--attention", action="store_true",
                     help="attention mode: the attention core at the local, global and ViT-L "
                          "shapes")
@@ -522,6 +644,9 @@ def main():
         return
     if args.full_block:
         print(json.dumps({"full_block": full_block_timing(rt, rng)}), flush=True)
+        return
+    if args.vitl:
+        print(json.dumps({"vitl": vitl_timing(rt, rng)}), flush=True)
         return
     if args.attention:
         print(json.dumps({"attention": attention_timing(rt, rng, args.op_iters)}), flush=True)
@@ -585,6 +710,8 @@ def main():
     log("attention and whole blocks")
     attention = attention_timing(rt, rng, 20)
     full_block = full_block_timing(rt, rng)
+    log("ViT-L 1008x672, F16-stored weights")
+    vitl = vitl_timing(rt, rng)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -619,6 +746,7 @@ def main():
         "linear_epilogues": linear,
         "attention": attention,
         "full_block": full_block,
+        "vitl_1008x672": vitl,
         "roofline": {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
                      "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
