@@ -470,13 +470,14 @@ def vitl_timing(rt, rng, reps=3):
 
 def attention_timing(rt, rng, iters):
     """The attention core (softmax(Q K^T / 8) V, F32 MFMA, online softmax) at
-    the path's shapes: a local layer of the 12-view batch (144 sequences of
-    866 tokens), a global layer (12 heads over the flattened 10,392 rows) and
-    the ViT-L 1008x672 image (16 heads over 3,458 rows).  FLOP counts
+    the path's shapes: one image (12 heads of 866 tokens), a local layer of
+    the 12-view batch (144 sequences of 866 tokens), a global layer (12 heads
+    over the flattened 10,392 rows) and the ViT-L 1008x672 image (16 heads
+    over 3,458 rows).  FLOP counts
     4*n*n*64 per sequence (two n x n x 64 products)."""
     out = {}
-    for name, seqs, n in (("local_12view", 12 * H, TPV), ("global_12view", H, 12 * TPV),
-                          ("vitl_1008x672", 16, 3458)):
+    for name, seqs, n in (("single_image", H, TPV), ("local_12view", 12 * H, TPV),
+                          ("global_12view", H, 12 * TPV), ("vitl_1008x672", 16, 3458)):
         q, k, v = (rt.upload_f32((rng.standard_normal(seqs * n * HD)).astype(np.float32))
                    for _ in range(3))
         o = rt.alloc_f32(seqs * n * HD)

@@ -4,7 +4,9 @@
 // multi-view sequence for global layers), with an online (one-pass) softmax.
 //
 // A 256-thread workgroup (4 waves) owns 64 queries of one sequence; wave w
-// owns queries 16w..16w+15.  Keys and values stream through LDS in blocks of
+// owns queries 16w..16w+15.  Grids of fewer than two such workgroups per CU
+// (a single image's local layer: 12 heads x 14 tiles) use workgroups of 32
+// queries whose two halves split the key blocks (attention_kernel<2, 2>).  Keys and values stream through LDS in blocks of
 // 64: K as [key][d] rows, V transposed as [d][key] rows, both with a pitch of
 // 68 floats (4 x odd: 16-row fragment reads are bank-conflict free).
 //
@@ -38,10 +40,9 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 64;
-constexpr int QB = 64;  // queries per workgroup
 constexpr int KB = 64;  // keys per block
 constexpr int PITCH = 68;
-constexpr int kThreads = 256;
+constexpr int kSlots = KB * HD / 4;  // float4 of one K (or V) block: 1024
 constexpr float kQScale = 0.125f * 1.44269504088896341f;  // log2(e) / sqrt(64)
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1, "pitch 4 x odd");
 static_assert(PITCH % 16 == 4, "transposed V stores: 16 (l >> 4) + (l & 15) covers 64 banks");
@@ -56,22 +57,38 @@ __device__ __forceinline__ float group_sum(float v) {
   return v + __shfl_xor(v, 32, 64);
 }
 
-__global__ __launch_bounds__(kThreads) void attention_kernel(const float* __restrict__ q,
-                                                             const float* __restrict__ k,
-                                                             const float* __restrict__ v,
-                                                             float* __restrict__ out,
-                                                             int sequences, int n) {
-  __shared__ __align__(16) float Ks[KB * PITCH];
-  __shared__ __align__(16) float Vt[HD * PITCH];
+// QG query groups of 16 (one wave each) x KS key splits per workgroup.
+// <4, 1>: 64 queries, every key block, the normal form.  <2, 2>: 32 queries,
+// two halves of 2 waves that take alternate key blocks (each with its own
+// staging buffers) and merge their partial results through LDS at the end
+// -- the form for grids that would leave CUs idle (a single image's local
+// layer: 12 heads x 14 tiles), keeping 4 waves and all four SIMDs per
+// workgroup.
+template <int QG, int KS>
+__global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __restrict__ q,
+                                                                 const float* __restrict__ k,
+                                                                 const float* __restrict__ v,
+                                                                 float* __restrict__ out,
+                                                                 int sequences, int n) {
+  constexpr int kThreads = 64 * QG * KS;
+  constexpr int kHalf = 64 * QG;          // threads of one key split
+  constexpr int QB = 16 * QG;             // queries per workgroup
+  constexpr int kPer = kSlots / kHalf;    // staged float4 of K (and of V) per thread
+  static_assert(KS == 1 || KS == 2, "one or two key splits");
+  __shared__ __align__(16) float smem[KS * 2 * KB * PITCH];
 
   const int tid = threadIdx.x;
   __builtin_assume(tid < kThreads);
   const int wave = tid >> 6, lane = tid & 63;
+  const int half = wave / QG, wq = wave % QG;  // key split, query group
+  const int htid = tid - half * kHalf;         // thread index inside the split
   const int g = lane >> 4, c16 = lane & 15;
+  float* Ks = smem + half * 2 * KB * PITCH;
+  float* Vt = Ks + KB * PITCH;
   const int nqb = (n + QB - 1) / QB;
   // XCD-major numbering: the query blocks of one sequence share an XCD's L2
   const int tile = vkd::xcd_tile(blockIdx.x, gridDim.x);
-  const int seq = tile / nqb, q0 = (tile % nqb) * QB + wave * 16;
+  const int seq = tile / nqb, q0 = (tile % nqb) * QB + wq * 16;
   const size_t base = static_cast<size_t>(seq) * n * HD;
 
   // Q^T fragments (B operand): query q0 + c16, d = 16 bd + 4 g + j
@@ -91,35 +108,48 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* __rest
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;  // statistics of query q0 + c16
 
-  const int skey = tid >> 4, sd = 4 * (tid & 15);  // K staging slot: key, d
-  // V staging slot: key 16 w + (l & 15), float4 columns (l >> 4) + 4 i
-  const int vkey = 16 * wave + (lane & 15), vcol = lane >> 4;
+  // K staging: slot f = htid + kHalf i is key f/16, float4 f%16 (16 lanes
+  // fill one key row).  V staging: slot f -> w' = f/64, key 16 (w' % 4) +
+  // (l & 15), float4 column (l >> 4) + 4 (w' / 4); one wave instruction covers
+  // 16 keys x 4 columns.
+  const int skey = htid >> 4, sd = 4 * (htid & 15);
   const float* karow = Ks + c16 * PITCH + 4 * g;
   const float* vtrow = Vt + c16 * PITCH + 4 * g;
 
-  for (int k0 = 0; k0 < n; k0 += KB) {
-    // stage: slot f = tid + 256 i is key f/16, float4 f%16 of the block
-    f32x4 kr[4], vr[4];
-    {
-      const int vk = k0 + vkey < n ? k0 + vkey : n - 1;
-      const float* vrow = v + base + static_cast<size_t>(vk) * HD;
+  const int nkb = (n + KB - 1) / KB;
+  const int iters = (nkb + KS - 1) / KS;
+  for (int it = 0; it < iters; ++it) {
+    const int k0 = (it * KS + half) * KB;
+    // uniform per split: with two splits the odd half may run out of blocks
+    const bool active = KS == 1 || k0 < n;
+    f32x4 kr[kPer], vr[kPer];
+    if (active) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = k0 + skey + 16 * i;
+      for (int i = 0; i < kPer; ++i) {
+        const int key = k0 + skey + (kHalf / 16) * i;
         const int ck = key < n ? key : n - 1;
         kr[i] = *reinterpret_cast<const f32x4*>(k + base + static_cast<size_t>(ck) * HD + sd);
-        vr[i] = *reinterpret_cast<const f32x4*>(vrow + 4 * (vcol + 4 * i));
+        const int w2 = wq + QG * i;
+        const int vkey = k0 + 16 * (w2 & 3) + (lane & 15);
+        const int cv = vkey < n ? vkey : n - 1;
+        vr[i] = *reinterpret_cast<const f32x4*>(v + base + static_cast<size_t>(cv) * HD +
+                                                4 * ((lane >> 4) + 4 * (w2 >> 2)));
       }
     }
     __syncthreads();  // the previous block is consumed
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<f32x4*>(Ks + (skey + 16 * i) * PITCH + sd) = kr[i];
-      const int d = 4 * (vcol + 4 * i);
+      for (int i = 0; i < kPer; ++i) {
+        *reinterpret_cast<f32x4*>(Ks + (skey + (kHalf / 16) * i) * PITCH + sd) = kr[i];
+        const int w2 = wq + QG * i;
+        const int key = 16 * (w2 & 3) + (lane & 15);
+        const int d = 4 * ((lane >> 4) + 4 * (w2 >> 2));
 #pragma unroll
-      for (int c = 0; c < 4; ++c) Vt[(d + c) * PITCH + vkey] = vr[i][c];
+        for (int c = 0; c < 4; ++c) Vt[(d + c) * PITCH + key] = vr[i][c];
+      }
     }
     __syncthreads();
+    if (!active) continue;
 
     // S^T tiles: s[t][r] = score of query q0 + c16 with key k0 + 16t + 4g + r
     f32x4 s[4];
@@ -179,6 +209,35 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const float* __rest
       }
   }
 
+  if constexpr (KS == 2) {
+    // merge the odd-block half into the even-block half: the waves of one
+    // query group hold the same queries in the same lane layout
+    constexpr int kX = 18;  // o (16), m, l per lane
+    __syncthreads();        // the staging buffers are free
+    float* xr = smem + (wq * 64 + lane) * kX;
+    if (half == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xr[dt * 4 + r] = o[dt][r];
+      xr[16] = m_run;
+      xr[17] = l_run;
+    }
+    __syncthreads();
+    if (half == 1) return;
+    const float m1 = xr[16], l1 = xr[17];
+    const float m = fmaxf(m_run, m1);
+    const float a0 = __builtin_amdgcn_exp2f(m_run - m);  // of query q0 + c16
+    const float a1 = __builtin_amdgcn_exp2f(m1 - m);
+    l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float b0 = __shfl(a0, 4 * g + r, 64), b1 = __shfl(a1, 4 * g + r, 64);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt][r] = o[dt][r] * b0 + xr[dt * 4 + r] * b1;
+    }
+  }
+
   // out[query][d] = O / l, O row 4g + r, column 16 dt + c16
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -223,13 +282,24 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
                "attention: out overlaps an input");
   }
   if (len == 0) return VK_OK;
-  const long long blocks = static_cast<long long>(sequences) * ((n + QB - 1) / QB);
+  // 64-query tiles unless they give fewer than two workgroups per CU; then
+  // 32-query tiles with the keys split over two halves of the workgroup
+  const long long tiles64 = static_cast<long long>(sequences) * ((n + 63) / 64);
+  const bool narrow = tiles64 < 2LL * (rt->cu_count > 0 ? rt->cu_count : 256);
+  const int qb = narrow ? 32 : 64;
+  const long long blocks = static_cast<long long>(sequences) * ((n + qb - 1) / qb);
   VK_UNSUPPORTED_IF(blocks > 0x7fffffffLL, "attention: %lld workgroups", blocks);
-  hipLaunchKernelGGL(attention_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                     rt->stream, static_cast<const float*>(q->ptr),
-                     static_cast<const float*>(k->ptr), static_cast<const float*>(v->ptr),
-                     static_cast<float*>(out->ptr), static_cast<int>(sequences),
-                     static_cast<int>(n));
+  const auto* Q = static_cast<const float*>(q->ptr);
+  const auto* K = static_cast<const float*>(k->ptr);
+  const auto* V = static_cast<const float*>(v->ptr);
+  auto* O = static_cast<float*>(out->ptr);
+  const int S = static_cast<int>(sequences), N = static_cast<int>(n);
+  if (narrow)
+    hipLaunchKernelGGL((attention_kernel<2, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                       0, rt->stream, Q, K, V, O, S, N);
+  else
+    hipLaunchKernelGGL((attention_kernel<4, 1>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                       0, rt->stream, Q, K, V, O, S, N);
   return vk::check_launch("attention_kernel");
 }
 

@@ -243,13 +243,20 @@ namespace {
 // Split count for a tile grid: at least one workgroup per CU when the rows
 // alone leave CUs idle (a single 866-token image), at least two k chunks per
 // split, at most 8 partial slices.
+#ifndef VK_SPLITK_WG_PER_CU
+#define VK_SPLITK_WG_PER_CU 1  // workgroups per CU the split aims at
+#endif
+#ifndef VK_SPLITK_MAX
+#define VK_SPLITK_MAX 8        // most partial slices
+#endif
+
 int choose_splits(const vk_runtime* rt, long long tiles, int K) {
-  const int cus = rt->cu_count > 0 ? rt->cu_count : 256;
+  const int cus = (rt->cu_count > 0 ? rt->cu_count : 256) * VK_SPLITK_WG_PER_CU;
   if (tiles >= cus) return 1;
   const int nch = (K + KC - 1) / KC;
   int s = static_cast<int>((static_cast<double>(cus) / static_cast<double>(tiles)) + 0.5);
   if (s > nch / 2) s = nch / 2;
-  if (s > 8) s = 8;
+  if (s > VK_SPLITK_MAX) s = VK_SPLITK_MAX;
   return s < 1 ? 1 : s;
 }
 
