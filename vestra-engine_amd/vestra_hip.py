@@ -477,7 +477,9 @@ class Runtime:
         ws = self.alloc_u8(need) if need else None
         _check(lib.vk_resize_u8(self.handle, src.handle, sh, sw, dst.handle, dh, dw, mode,
                                 _h(ws)))
-        self._keep = ws  # the workspace must outlive the queued kernels
+        # the workspace lives as long as the result (freeing a tensor waits for
+        # the stream, which a graph capture in progress would not allow)
+        dst._workspace = ws
 
     def preprocess_shape(self, h: int, w: int, image_size: int, patch: int,
                          upper_bound: bool = True):
@@ -496,7 +498,7 @@ class Runtime:
         ws = self.alloc_u8(need) if need else None
         _check(lib.vk_preprocess_resize_u8(self.handle, src.handle, h, w, image_size, patch,
                                            1 if upper_bound else 0, _h(ws), out.handle))
-        self._keep = ws
+        out._workspace = ws
         return out
 
     def normalize_u8_hwc_nchw_f32(self, src: Tensor, h: int, w: int, mean: Sequence[float],
