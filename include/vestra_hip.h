@@ -328,6 +328,18 @@ int vk_linear_run_qkv_hnd_f32(vk_runtime* rt, const vk_linear* lin,
                               const vk_tensor* x, size_t rows, size_t heads,
                               size_t head_dim, vk_tensor* q, vk_tensor* k,
                               vk_tensor* v);
+/* The QKV projection with Q/K-norm + 2D RoPE in its epilogue: bit-identical
+ * to vk_linear_run_qkv_hnd_f32 followed by vk_qk_norm_rope_grid_f32 with
+ * VK_QK_HEADS_OUTER (same arguments; q_gamma..k_beta NULL: RoPE only), and
+ * one pass less over Q and K.  The device path of the QKV run + split +
+ * qk_norm_rope_f32_da3_base of run_tail_device (vit_block.rs:537-557).
+ * rows = view_count * (n_special + gh*gw); head_dim 64. */
+int vk_linear_run_qkv_hnd_norm_rope_f32(
+    vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
+    size_t heads, size_t head_dim, vk_tensor* q, vk_tensor* k, vk_tensor* v,
+    const vk_tensor* q_gamma, const vk_tensor* q_beta, const vk_tensor* k_gamma,
+    const vk_tensor* k_beta, size_t n_special, size_t gh, size_t gw,
+    size_t view_count, int global, float freq, float eps);
 /* The output projection reading the head-major attention output
  * [heads, rows, 64] directly (in_features = heads*64): bit-identical to
  * vk_hnd_to_token_into_f32 followed by vk_linear_run_into_f32 /

@@ -122,3 +122,32 @@ def test_head_major_linears_reject_unqualified_shapes(rt, rng):
     q1, k1, v1 = (rt.alloc_f32(4 * 64) for _ in range(3))
     with pytest.raises(vh.VestraError):
         with_ls.run_qkv_hnd(x64, 4, 1, q1, k1, v1)                  # QKV carries no LayerScale
+
+
+@pytest.mark.parametrize("embed,heads,gh,gw,views,glob,f16,norm", [
+    (768, 12, 24, 36, 1, False, False, True),     # one 504x336 image: split-K path
+    (768, 12, 24, 36, 12, True, False, True),     # 12-view global layer
+    (768, 12, 24, 36, 12, False, False, True),    # 12-view local layer
+    (1024, 16, 4, 8, 2, False, True, True),       # ViT-L, f16 parameters
+    (768, 12, 3, 5, 3, True, False, False),       # RoPE only
+])
+def test_qkv_norm_rope_epilogue_is_the_separate_pass(rt, rng, embed, heads, gh, gw, views, glob,
+                                                     f16, norm):
+    """QKV + Q/K-norm + RoPE in one kernel gives the bits of the QKV projection
+    followed by the Q/K kernel on the head-major layout."""
+    rows = views * (2 + gh * gw)
+    x = rt.upload_f32(normals(rng, rows, embed))
+    lin = rt.prepare_linear_f32(embed, 3 * embed, normals(rng, embed, 3 * embed, scale=0.02),
+                                normals(rng, 3 * embed, scale=0.02))
+    par = [None] * 4
+    if norm:
+        host = [normals(rng, 64, scale=0.02, shift=s) for s in (1, 0, 1, 0)]
+        par = [rt.upload_f16(h.astype(np.float16)) if f16 else rt.upload_f32(h) for h in host]
+    fused = [rt.alloc_f32(rows * embed) for _ in range(3)]
+    lin.run_qkv_hnd_norm_rope(x, rows, heads, *fused, *par, 2, gh, gw, views, glob)
+    sep = [rt.alloc_f32(rows * embed) for _ in range(3)]
+    lin.run_qkv_hnd(x, rows, heads, *sep)
+    rt.qk_norm_rope_grid_f32(sep[0], sep[1], *par, heads, 64, 2, gh, gw, views, glob,
+                             vh.VK_QK_HEADS_OUTER, 100.0, 1e-5)
+    for name, a, b in zip("qkv", fused, sep):
+        assert np.array_equal(a.numpy(), b.numpy()), f"{name} differs from the separate pass"

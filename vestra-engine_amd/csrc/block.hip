@@ -140,7 +140,8 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
 // The QKV projection writes Q, K, V head-major from its epilogue and the
 // output projection reads the attention output head-major, so the
 // reference's split_qkv_hnd / hnd_to_token passes (vit_block.rs:539-541, 560)
-// are not separate launches.  8 launches per block.
+// are not separate launches, and Q/K-norm + RoPE run in the QKV epilogue.
+// 7 launches per block.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -198,24 +199,26 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
     }
   }
 
-  // LN1 -> QKV (head-major Q, K, V)
+  // LN1 -> QKV (head-major Q, K, V) with Q/K-norm + RoPE, gated as in
+  // vk_vit_block_fused_ops (vit_block.rs:835-838); with RoPE on, both run
+  // in the projection's epilogue (the bits of the separate pass)
   VK_TRY(vk_layernorm_into_f32(rt, tokens, w->norm1_gamma, w->norm1_beta, rows, D, cfg->ln_eps,
                                ws->ln));
-  VK_TRY(vk_linear_run_qkv_hnd_f32(rt, w->qkv, ws->ln, rows, H, hd, ws->q, ws->k, ws->v));
-
-  // Q/K-norm + RoPE, gated as in vk_vit_block_fused_ops (vit_block.rs:835-838)
   const bool use_qknorm = cfg->qknorm_start >= 0 &&
                           static_cast<long long>(layer_idx) >= cfg->qknorm_start &&
                           w->qnorm_gamma != nullptr;
   const bool use_rope =
       cfg->rope_start >= 0 && static_cast<long long>(layer_idx) >= cfg->rope_start;
   if (use_rope) {
-    VK_TRY(vk_qk_norm_rope_grid_f32(
-        rt, ws->q, ws->k, use_qknorm ? w->qnorm_gamma : nullptr,
-        use_qknorm ? w->qnorm_beta : nullptr, use_qknorm ? w->knorm_gamma : nullptr,
-        use_qknorm ? w->knorm_beta : nullptr, H, hd, n_special, gh, gw, view_count,
-        global ? 1 : 0, VK_QK_HEADS_OUTER, cfg->rope_freq, cfg->qk_norm_eps));
-  } else if (use_qknorm) {
+    VK_TRY(vk_linear_run_qkv_hnd_norm_rope_f32(
+        rt, w->qkv, ws->ln, rows, H, hd, ws->q, ws->k, ws->v,
+        use_qknorm ? w->qnorm_gamma : nullptr, use_qknorm ? w->qnorm_beta : nullptr,
+        use_qknorm ? w->knorm_gamma : nullptr, use_qknorm ? w->knorm_beta : nullptr, n_special,
+        gh, gw, view_count, global ? 1 : 0, cfg->rope_freq, cfg->qk_norm_eps));
+  } else {
+    VK_TRY(vk_linear_run_qkv_hnd_f32(rt, w->qkv, ws->ln, rows, H, hd, ws->q, ws->k, ws->v));
+  }
+  if (!use_rope && use_qknorm) {
     VK_TRY(vk_layernorm_into_f32(rt, ws->q, w->qnorm_gamma, w->qnorm_beta, rows * H, hd,
                                  cfg->qk_norm_eps, ws->q));
     VK_TRY(vk_layernorm_into_f32(rt, ws->k, w->knorm_gamma, w->knorm_beta, rows * H, hd,

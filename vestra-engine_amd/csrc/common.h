@@ -69,6 +69,34 @@ struct vk_graph {
 // error plumbing
 // ---------------------------------------------------------------------------
 
+namespace vkd {
+
+// Unsigned 32-bit division by a runtime-invariant divisor as a multiply-high
+// and two shifts (Granlund & Montgomery, "Division by invariant integers
+// using multiplication", PLDI 1994, fig. 4.1), exact for every n < 2^32.
+// The divisor data is built on the host and passed to kernels by value.
+struct FastDivU32 {
+  uint32_t d;
+  uint32_t m;
+  uint32_t s1;
+  uint32_t s2;
+};
+
+__host__ __device__ inline FastDivU32 make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;  // l = ceil(log2 d)
+  const unsigned long long m =
+      ((1ull << 32) * ((1ull << l) - d)) / d + 1;  // 2^l - d < 2^31: no overflow
+  FastDivU32 f;
+  f.d = d;
+  f.m = static_cast<uint32_t>(m);
+  f.s1 = l ? 1u : 0u;
+  f.s2 = l ? l - 1 : 0u;
+  return f;
+}
+
+}  // namespace vkd
+
 namespace vk {
 
 int set_error(int code, const char* fmt, ...);
@@ -85,6 +113,22 @@ int check_launch(const char* what);
 // it, so call it before any stream capture that uses the table.
 int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
                int* table_max);
+
+// Q/K-norm + RoPE parameters of the QKV projection's fused epilogue: the
+// row's token index m gives its position (rows are view-major tokens).
+struct QkEpilogue {
+  const void* qg;  // Q/K LayerNorm gamma / beta (f32 or f16), null for RoPE only
+  const void* qb;
+  const void* kg;
+  const void* kb;
+  const float* table;  // cos/sin table (layout below), covers every grid coordinate
+  int table_max;
+  uint32_t n_special;
+  uint32_t global;
+  vkd::FastDivU32 tpv;  // tokens per view
+  vkd::FastDivU32 gw;   // patch grid width
+  float eps;
+};
 
 // F32 linear out[m, n] = epilogue(sum_k x[m, k] W[n, k] + b[n]).
 struct LinearArgs {
@@ -105,6 +149,10 @@ struct LinearArgs {
   // applies the epilogue.
   int splits;
   float* partial;
+  // Q/K LayerNorm + 2D RoPE in the QKV epilogue (q_out set, qkn_mode != 0):
+  // 1 LayerNorm with f32 parameters, 2 with f16 parameters, 3 RoPE only.
+  int qkn_mode;
+  QkEpilogue qkn;
 };
 
 // Epilogues of the linear: v = acc + b (then * ls when the linear has one),
@@ -186,30 +234,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   v = v + __shfl_xor(v, 16, 64);
   v = v + __shfl_xor(v, 32, 64);
   return v;
-}
-
-// Unsigned 32-bit division by a runtime-invariant divisor as a multiply-high
-// and two shifts (Granlund & Montgomery, "Division by invariant integers
-// using multiplication", PLDI 1994, fig. 4.1), exact for every n < 2^32.
-// The divisor data is built on the host and passed to kernels by value.
-struct FastDivU32 {
-  uint32_t d;
-  uint32_t m;
-  uint32_t s1;
-  uint32_t s2;
-};
-
-__host__ __device__ inline FastDivU32 make_fastdiv(uint32_t d) {
-  uint32_t l = 0;
-  while ((1ull << l) < d) ++l;  // l = ceil(log2 d)
-  const unsigned long long m =
-      ((1ull << 32) * ((1ull << l) - d)) / d + 1;  // 2^l - d < 2^31: no overflow
-  FastDivU32 f;
-  f.d = d;
-  f.m = static_cast<uint32_t>(m);
-  f.s1 = l ? 1u : 0u;
-  f.s2 = l ? l - 1 : 0u;
-  return f;
 }
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDivU32& f) {

@@ -23,11 +23,19 @@
 // a float4 of A never crosses a head.  Both are pure address changes: the
 // results are the bits of the linear plus the separate permutation.
 //
+// Q/K-norm + RoPE in the QKV epilogue (QKN != 0): after the last chunk each
+// wave that holds a Q or K head strip writes its 32 x 64 values (acc + b)
+// to LDS and reads them back as the Q/K kernel holds a row -- 16 lanes per
+// 64-wide row, one float4 each -- and applies the same row transform
+// (vkq::qk_row_transform) before storing the row head-major.  The values
+// and the code path are those of the separate pass, so the bits are too.
+//
 // Traffic: a 128 x 128 tile moves (128 + 128) x 4 bytes of operands per k for
 // 2 x 128 x 128 FLOP, 0.031 byte per FLOP from L2 (the 48 x 64 tiles of the
 // narrow kernel need 0.073).  Tiles are numbered XCD-major (xcd_tile), so
 // the workgroups of one XCD share weight columns in that XCD's L2.
 #include "common.h"
+#include "qk_rows.h"
 
 namespace {
 
@@ -70,7 +78,43 @@ __device__ __forceinline__ void store_out(const LinearArgs& g, int row, int col,
   if (EPI == kLinResidual) *o = old + v;
 }
 
-template <int EPI, int LAY>
+// QKN: 0 none; 1 / 2 Q/K LayerNorm (f32 / f16 parameters) + RoPE; 3 RoPE.
+template <int QKN>
+struct QknTraits;
+template <>
+struct QknTraits<1> {
+  typedef float PT;
+  static constexpr bool kNorm = true;
+};
+template <>
+struct QknTraits<2> {
+  typedef uint16_t PT;
+  static constexpr bool kNorm = true;
+};
+template <>
+struct QknTraits<3> {
+  typedef float PT;
+  static constexpr bool kNorm = false;
+};
+
+// Q/K-norm + RoPE of one 64-wide head row held as one float4 per lane of a
+// 16-lane group (lane l: columns 4l..4l+3), for token `row` (clamped to a
+// valid token; rows past M are computed and not stored).
+template <int QKN>
+__device__ __forceinline__ float4 qk_head_row(const LinearArgs& g, float4 v, int l, bool is_k,
+                                              int row) {
+  typedef typename QknTraits<QKN>::PT PT;
+  const int rowc = row < g.M ? row : g.M - 1;
+  int py, px;
+  vkq::grid_position(vkd::fmod_(static_cast<uint32_t>(rowc), g.qkn.tpv), g.qkn.n_special,
+                     g.qkn.global, g.qkn.gw, &py, &px);
+  const PT* gm = static_cast<const PT*>(is_k ? g.qkn.kg : g.qkn.qg);
+  const PT* bt = static_cast<const PT*>(is_k ? g.qkn.kb : g.qkn.qb);
+  return vkq::qk_row_transform<PT, QknTraits<QKN>::kNorm, vkq::kPosGrid>(
+      v, l, gm, bt, py, px, g.qkn.table, g.qkn.table_max, g.qkn.eps);
+}
+
+template <int EPI, int LAY, int QKN = 0>
 __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) {
   __shared__ __align__(16) float As[TM * PITCH];
   __shared__ __align__(16) float Bs[TN * PITCH];
@@ -177,6 +221,40 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
   // Parameters and (for the residual) the old values are all loaded, on
   // clamped indices, before the first store.
   float bias[4], ls[4];
+  if constexpr (QKN != 0) {
+    static_assert(LAY == kQkvHnd && EPI == kLinStore, "Q/K epilogue of the QKV projection");
+    const int col0 = n0 + wn * 64;  // the wave's strip: one head of Q, K or V
+    const int embed = g.N / 3;
+    const int which = col0 < g.N ? col0 / embed : 2;
+    const int g4 = lane >> 4, c16 = lane & 15;
+    float* xs = (wave < 4 ? As : Bs) + (wave & 3) * 32 * PITCH;
+    __syncthreads();  // every wave is done with the last chunk's operands
+    if (which < 2) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float b = g.bias[col0 + u * 16 + c16];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            xs[(t * 16 + 4 * g4 + r) * PITCH + u * 16 + c16] = acc[t][u][r] + b;
+      }
+    }
+    __syncthreads();
+    if (which < 2) {
+      float* dst = (which == 0 ? g.q_out : g.k_out) +
+                   static_cast<size_t>((col0 - which * embed) >> 6) * g.M * 64;
+#pragma unroll 2
+      for (int i = 0; i < 8; ++i) {
+        const int rr = g4 * 8 + i;
+        const int row = m0 + wm * 32 + rr;
+        const float4 v = *reinterpret_cast<const float4*>(xs + rr * PITCH + 4 * c16);
+        const float4 o = qk_head_row<QKN>(g, v, c16, which == 1, row);
+        if (row < g.M) *reinterpret_cast<float4*>(dst + static_cast<size_t>(row) * 64 + 4 * c16) = o;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int col = n0 + wn * 64 + u * 16 + (lane & 15);
@@ -216,16 +294,34 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
 // Second pass of a split-K linear: one thread per 4 consecutive outputs of a
 // row; the splits' partial sums are added in split order, then the epilogue
 // of the single-pass kernel is applied.
-template <int EPI, int LAY>
+template <int EPI, int LAY, int QKN = 0>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
   const long long i4 = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
   const long long mn = static_cast<long long>(g.M) * g.N;
-  if (i4 * 4 >= mn) return;
+  if (i4 * 4 >= mn) return;  // whole 16-lane groups (M*N/4 is a multiple of 16 here)
   const size_t e = static_cast<size_t>(i4) * 4;
   const int row = static_cast<int>(e / g.N), col = static_cast<int>(e % g.N);
   f32x4 acc = *reinterpret_cast<const f32x4*>(g.partial + e);
   for (int sp = 1; sp < g.splits; ++sp)
     acc = acc + *reinterpret_cast<const f32x4*>(g.partial + static_cast<size_t>(sp) * mn + e);
+  if constexpr (QKN != 0) {
+    // 16 consecutive threads hold one 64-wide head row of one token
+    const int embed = g.N / 3;
+    const int which = col / embed;
+    if (which < 2) {
+      const int c = col - which * embed;
+      float4 v;
+      v.x = acc[0] + g.bias[col];
+      v.y = acc[1] + g.bias[col + 1];
+      v.z = acc[2] + g.bias[col + 2];
+      v.w = acc[3] + g.bias[col + 3];
+      const float4 o = qk_head_row<QKN>(g, v, threadIdx.x & 15, which == 1, row);
+      float* dst = (which == 0 ? g.q_out : g.k_out) +
+                   (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
+      *reinterpret_cast<float4*>(dst) = o;
+      return;
+    }
+  }
   f32x4 old = f32x4{0.f, 0.f, 0.f, 0.f};
   if constexpr (EPI == kLinResidual) old = *reinterpret_cast<const f32x4*>(g.out + e);
 #pragma unroll
@@ -277,13 +373,14 @@ int ensure_splitk(vk_runtime* rt, size_t need) {
   return VK_OK;
 }
 
-template <int EPI, int LAY>
+template <int EPI, int LAY, int QKN = 0>
 void launch_pair(vk_runtime* rt, const LinearArgs& g, dim3 grid) {
-  hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY>), grid, dim3(kThreads), 0, rt->stream, g);
+  hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN>), grid, dim3(kThreads), 0, rt->stream, g);
   if (g.splits > 1) {
     const long long n4 = static_cast<long long>(g.M) * g.N / 4;
-    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY>), dim3(static_cast<unsigned>((n4 + 255) / 256)),
-                       dim3(256), 0, rt->stream, g);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN>),
+                       dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, rt->stream,
+                       g);
   }
 }
 
@@ -304,7 +401,13 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   const dim3 grid(static_cast<unsigned>(tiles * g.splits));
   if (g.q_out) {
     VK_REQUIRE(epi == kLinStore, "linear: the Q|K|V split takes the store epilogue");
-    launch_pair<kLinStore, kQkvHnd>(rt, g, grid);
+    switch (g.qkn_mode) {
+      case 0: launch_pair<kLinStore, kQkvHnd>(rt, g, grid); break;
+      case 1: launch_pair<kLinStore, kQkvHnd, 1>(rt, g, grid); break;
+      case 2: launch_pair<kLinStore, kQkvHnd, 2>(rt, g, grid); break;
+      case 3: launch_pair<kLinStore, kQkvHnd, 3>(rt, g, grid); break;
+      default: return set_error(VK_ERR_INVALID, "linear: unknown Q/K epilogue %d", g.qkn_mode);
+    }
   } else if (g.a_hnd) {
     if (epi == kLinResidual)
       launch_pair<kLinResidual, kAHnd>(rt, g, grid);

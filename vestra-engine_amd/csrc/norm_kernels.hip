@@ -20,6 +20,7 @@
 //    product and sum rounded (built with -ffp-contract=off); only the order
 //    of the mean/variance reductions differs (wave tree vs sequential).
 #include "common.h"
+#include "qk_rows.h"
 
 namespace {
 
@@ -118,143 +119,7 @@ __global__ __launch_bounds__(64) void ls_residual_layernorm_rows(
 // ---------------------------------------------------------------------------
 // Q/K LayerNorm (head_dim 64) + 2D RoPE, in place.
 // ---------------------------------------------------------------------------
-enum PosMode { kPosExplicit = 0, kPosGrid = 1 };
-
-struct QkShape {
-  uint32_t rows_per_tensor;  // heads * total tokens; 2 * rows_per_tensor < 2^31
-  int table_max;             // largest position the cos/sin table covers
-  uint32_t n_special;
-  uint32_t global;
-  uint32_t layout;           // vk_qk_layout
-  vkd::FastDivU32 ntok;      // total tokens (view_count * tokens_per_view)
-  vkd::FastDivU32 tpv;       // tokens per view
-  vkd::FastDivU32 per_view;  // heads * tokens per view
-  vkd::FastDivU32 gw;        // patch grid width
-};
-
-// cos/sin of the four frequencies j0..j0+3 for a coordinate outside the
-// table: angle rounded in f32, trig in double, as the host table does.  Only
-// the explicit-position form can meet such a coordinate (grid forms size the
-// table on the host); kept out of line so its double-precision trig does not
-// inflate the register footprint of the streaming path.
-__device__ __noinline__ void rope_cs_slow4(const float* __restrict__ table, int table_max,
-                                           int p, int j0, float4* c, float4* s) {
-  float cv[4], sv[4];
-  for (int u = 0; u < 4; ++u) {
-    const float inv_freq = table[static_cast<size_t>(table_max + 1) * 32 + j0 + u];
-    const float angle = static_cast<float>(p) * inv_freq;
-    cv[u] = static_cast<float>(cos(static_cast<double>(angle)));
-    sv[u] = static_cast<float>(sin(static_cast<double>(angle)));
-  }
-  *c = make_float4(cv[0], cv[1], cv[2], cv[3]);
-  *s = make_float4(sv[0], sv[1], sv[2], sv[3]);
-}
-
-__device__ __forceinline__ float4 swizzle_xor4(float4 v) {
-  // ds_swizzle bit-mask mode: and_mask 0x1f, or_mask 0, xor_mask 4.
-  constexpr int pat = (4 << 10) | 0x1f;
-  float4 r;
-  r.x = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.x), pat));
-  r.y = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.y), pat));
-  r.z = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.z), pat));
-  r.w = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v.w), pat));
-  return r;
-}
-
-// Position (y, x) of Q/K row r (head-major index inside one tensor).  All
-// index math is 32-bit with multiply-shift division by the shape constants.
-template <int POS>
-__device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
-                                                const float* __restrict__ pos_yx, int* py,
-                                                int* px) {
-  uint32_t t;   // index in the position sequence
-  uint32_t lt;  // index inside its view
-  if (sh.layout == VK_QK_HEADS_OUTER) {
-    t = vkd::fmod_(r, sh.ntok);
-    lt = vkd::fmod_(t, sh.tpv);
-  } else {
-    const uint32_t v = vkd::fdiv(r, sh.per_view);
-    lt = vkd::fmod_(r, sh.tpv);
-    t = v * sh.tpv.d + lt;
-  }
-  *py = 0;
-  *px = 0;
-  if (POS == kPosExplicit) {
-    // the reference's f32 device encoding, truncated like `value as i64`
-    *py = static_cast<int>(pos_yx[2 * static_cast<size_t>(t)]);
-    *px = static_cast<int>(pos_yx[2 * static_cast<size_t>(t) + 1]);
-  } else if (lt >= sh.n_special) {
-    if (sh.global) {
-      *py = 1;
-      *px = 1;
-    } else {
-      const uint32_t p = lt - sh.n_special;
-      const uint32_t row = vkd::fdiv(p, sh.gw);
-      *py = static_cast<int>(row) + 1;
-      *px = static_cast<int>(p - row * sh.gw.d) + 1;
-    }
-  }
-}
-
-// LayerNorm of one 64-wide row held as one float4 per lane of a 16-lane DPP
-// row, then its 2D rotation.
-template <typename PT, bool HAS_NORM, int POS>
-__device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
-                                                   const PT* __restrict__ b, int py, int px,
-                                                   const float* __restrict__ table,
-                                                   int table_max, float eps) {
-  if (HAS_NORM) {
-    float s = v.x;
-    s += v.y;
-    s += v.z;
-    s += v.w;
-    s = vkd::row16_sum(s);
-    const float mean = s / 64.0f;
-    float d, sq;
-    d = v.x - mean; sq = d * d;
-    d = v.y - mean; sq += d * d;
-    d = v.z - mean; sq += d * d;
-    d = v.w - mean; sq += d * d;
-    sq = vkd::row16_sum(sq);
-    const float var = sq / 64.0f;
-    const float inv = 1.0f / sqrtf(var + eps);
-    const float4 gv = Param<PT>::load4(g, l);
-    const float4 bv = Param<PT>::load4(b, l);
-    v.x = (v.x - mean) * inv * gv.x + bv.x;
-    v.y = (v.y - mean) * inv * gv.y + bv.y;
-    v.z = (v.z - mean) * inv * gv.z + bv.z;
-    v.w = (v.w - mean) * inv * gv.w + bv.w;
-  }
-  // RoPE.  Lanes 0-7 hold the y half (elements 0..31), lanes 8-15 the x half.
-  // Inside a half, lanes with bit 2 clear hold elements j (j < 16) and rotate
-  // against the lane 4 above, which holds element j + 16.
-  const int coord = (l < 8) ? py : px;
-  const int j0 = (l & 3) * 4;
-  float4 c, s;
-  if (POS == kPosGrid || (coord >= 0 && coord <= table_max)) {
-    const float* e = table + static_cast<size_t>(coord) * 32;
-    c = *reinterpret_cast<const float4*>(e + j0);
-    s = *reinterpret_cast<const float4*>(e + 16 + j0);
-  } else {
-    rope_cs_slow4(table, table_max, coord, j0, &c, &s);
-  }
-  const float4 p = swizzle_xor4(v);
-  float4 o;
-  if ((l & 4) == 0) {
-    // out[j] = x[j]*cos - x[j+16]*sin
-    o.x = v.x * c.x + (-p.x) * s.x;
-    o.y = v.y * c.y + (-p.y) * s.y;
-    o.z = v.z * c.z + (-p.z) * s.z;
-    o.w = v.w * c.w + (-p.w) * s.w;
-  } else {
-    // out[j+16] = x[j+16]*cos + x[j]*sin
-    o.x = v.x * c.x + p.x * s.x;
-    o.y = v.y * c.y + p.y * s.y;
-    o.z = v.z * c.z + p.z * s.z;
-    o.w = v.w * c.w + p.w * s.w;
-  }
-  return o;
-}
+using namespace vkq;
 
 // Each 16-lane group owns kQkRowsPerGroup consecutive rows of the flattened
 // [Q rows | K rows] index space; both rows' loads are issued before either

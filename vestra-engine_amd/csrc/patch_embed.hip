@@ -1044,6 +1044,71 @@ int vk_linear_run_qkv_hnd_f32(vk_runtime* rt, const vk_linear* lin, const vk_ten
   return vk::launch_linear_wide(rt, g, kLinStore);
 }
 
+int vk_linear_run_qkv_hnd_norm_rope_f32(vk_runtime* rt, const vk_linear* lin,
+                                        const vk_tensor* x, size_t rows, size_t heads,
+                                        size_t head_dim, vk_tensor* q, vk_tensor* k,
+                                        vk_tensor* v, const vk_tensor* q_gamma,
+                                        const vk_tensor* q_beta, const vk_tensor* k_gamma,
+                                        const vk_tensor* k_beta, size_t n_special, size_t gh,
+                                        size_t gw, size_t view_count, int global, float freq,
+                                        float eps) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && q && k && v, "null argument");
+  VK_UNSUPPORTED_IF(head_dim != 64, "qkv norm_rope: head_dim=%zu (qualified: 64)", head_dim);
+  VK_REQUIRE(view_count > 0 && gw > 0, "view_count and gw must be > 0");
+  VK_REQUIRE(rows == view_count * (n_special + gh * gw),
+             "qkv norm_rope: rows=%zu, expected view_count*(n_special+gh*gw)=%zu", rows,
+             view_count * (n_special + gh * gw));
+  const bool any = q_gamma || q_beta || k_gamma || k_beta;
+  const bool all = q_gamma && q_beta && k_gamma && k_beta;
+  VK_REQUIRE(!any || all, "q/k norm parameters must be all present or all null");
+  if (all) {
+    for (const vk_tensor* t : {q_gamma, q_beta, k_gamma, k_beta})
+      VK_REQUIRE((t->dtype == VK_F32 || t->dtype == VK_F16) && t->dtype == q_gamma->dtype &&
+                     t->len == head_dim,
+                 "q/k norm parameters must be f32 or f16 vectors of 64 sharing one dtype");
+  }
+  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "qkv norm_rope: rows=%zu too large", rows);
+  // Q|K|V projection checks (and nothing to do for zero rows)
+  if (rows == 0) return vk_linear_run_qkv_hnd_f32(rt, lin, x, rows, heads, head_dim, q, k, v);
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_head_layout(lin, x, heads, head_dim));
+  VK_REQUIRE(lin->out_features == 3 * heads * head_dim,
+             "linear_run_qkv_hnd: out_features=%zu, expected 3*heads*head_dim=%zu",
+             lin->out_features, 3 * heads * head_dim);
+  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_qkv_hnd: the linear carries a LayerScale");
+  const size_t part = rows * heads * head_dim;
+  for (const vk_tensor* t : {q, k, v})
+    VK_REQUIRE(t->dtype == VK_F32 && t->len == part, "q, k, v must be f32 [rows*heads*64=%zu]",
+               part);
+  VK_REQUIRE(tensors_disjoint(x, q) && tensors_disjoint(x, k) && tensors_disjoint(x, v) &&
+                 tensors_disjoint(q, k) && tensors_disjoint(q, v) && tensors_disjoint(k, v),
+             "linear_run_qkv_hnd: tensors overlap");
+  // the grid's largest coordinate is max(gh, gw) + 1: the table covers it
+  const size_t max_coord = (gh > gw ? gh : gw) + 1;
+  VK_UNSUPPORTED_IF(max_coord > (1u << 22), "patch grid %zux%zu too large", gh, gw);
+  const float* table = nullptr;
+  int table_max = 0;
+  VK_TRY(vk::rope_table(rt, freq, 64, static_cast<int>(max_coord), &table, &table_max));
+  LinearArgs g = linear_args(lin, x, rows, nullptr);
+  g.q_out = static_cast<float*>(q->ptr);
+  g.k_out = static_cast<float*>(k->ptr);
+  g.v_out = static_cast<float*>(v->ptr);
+  g.qkn_mode = !all ? 3 : (q_gamma->dtype == VK_F16 ? 2 : 1);
+  g.qkn.qg = all ? q_gamma->ptr : nullptr;
+  g.qkn.qb = all ? q_beta->ptr : nullptr;
+  g.qkn.kg = all ? k_gamma->ptr : nullptr;
+  g.qkn.kb = all ? k_beta->ptr : nullptr;
+  g.qkn.table = table;
+  g.qkn.table_max = table_max;
+  g.qkn.n_special = static_cast<uint32_t>(n_special);
+  g.qkn.global = global ? 1u : 0u;
+  g.qkn.tpv = vkd::make_fastdiv(static_cast<uint32_t>(n_special + gh * gw));
+  g.qkn.gw = vkd::make_fastdiv(static_cast<uint32_t>(gw));
+  g.qkn.eps = eps;
+  return vk::launch_linear_wide(rt, g, kLinStore);
+}
+
 static int run_hnd(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd, size_t rows,
                    size_t heads, size_t head_dim, vk_tensor* out, int epi, const char* what) {
   VK_TRY(vk::bind(rt));

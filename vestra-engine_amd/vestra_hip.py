@@ -150,6 +150,9 @@ _SIGS = {
     "vk_linear_run_gelu_erf_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_residual_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_qkv_hnd_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp], _i),
+    "vk_linear_run_qkv_hnd_norm_rope_f32": (
+        [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _i,
+         _f, _f], _i),
     "vk_linear_run_hnd_into_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_linear_run_hnd_residual_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_split_qkv_hnd_f32": ([_vp, _vp, _sz, _sz, _sz, _pp, _pp, _pp], _i),
@@ -284,6 +287,18 @@ class Linear:
         """Projection of a head-major input [heads, rows, 64]."""
         _check(lib.vk_linear_run_hnd_into_f32(self.rt.handle, self.handle, hnd.handle, rows,
                                               heads, head_dim, out.handle))
+
+    def run_qkv_hnd_norm_rope(self, x: Tensor, rows: int, heads: int, q: Tensor, k: Tensor,
+                              v: Tensor, q_gamma: Optional[Tensor], q_beta: Optional[Tensor],
+                              k_gamma: Optional[Tensor], k_beta: Optional[Tensor],
+                              n_special: int, gh: int, gw: int, view_count: int,
+                              global_layer: bool, freq: float = 100.0,
+                              eps: float = 1e-5) -> None:
+        """QKV projection storing head-major Q, K, V with Q/K-norm + RoPE fused."""
+        _check(lib.vk_linear_run_qkv_hnd_norm_rope_f32(
+            self.rt.handle, self.handle, x.handle, rows, heads, 64, q.handle, k.handle, v.handle,
+            _h(q_gamma), _h(q_beta), _h(k_gamma), _h(k_beta), n_special, gh, gw, view_count,
+            1 if global_layer else 0, freq, eps))
 
     def run_hnd_residual(self, hnd: Tensor, rows: int, heads: int, residual: Tensor,
                          head_dim: int = 64) -> None:
