@@ -176,3 +176,42 @@ def test_block_forward_errors(rt, rng):
     with pytest.raises(vh.VestraError):
         rt.vit_block_forward_f32(cfg, 0, swapped, rt.alloc_f32(rows * D), 2, 3, 1, None,
                                  ws.struct)                      # projection shapes
+
+
+def test_block_forward_graph_replays(rt, rng):
+    """Two whole blocks (one split-K single view of 4x6 patches, so every
+    projection takes the two-pass path) captured into a HIP graph after one
+    eager pass: every replay, with eager work and synchronisation between
+    replays, gives the bits of the eager sequence."""
+    import gc
+    D, H, M, gh, gw, views = 768, 12, 3072, 4, 6, 1
+    cfg = vh.VitConfig(**config(D, H, M, alt=1))
+    rows = (2 + gh * gw) * views
+    devs = [DeviceBlock(rt, make_params(rng, D, M), D, M) for _ in range(2)]
+    x0 = normals(rng, rows, D)
+    cam = rt.upload_f32(normals(rng, 2 * D))
+    tokens, ws = rt.upload_f32(x0), rt.block_workspace(rows, D, M)
+
+    def step():
+        for layer, dev in enumerate(devs):
+            rt.vit_block_forward_f32(cfg, layer, dev.struct, tokens, gh, gw, views, cam, ws.struct)
+
+    step()  # eager: RoPE table and split-K buffer exist before capture
+    want = tokens.numpy()
+    rt.synchronize()
+    gc.disable()
+    try:
+        rt.begin_capture()
+        step()
+        graph = rt.end_capture()
+    finally:
+        gc.enable()
+    for _ in range(3):
+        tokens.write(x0)
+        graph.launch()
+        rt.synchronize()
+        assert np.array_equal(tokens.numpy(), want)
+        scratch = rt.upload_f32(normals(rng, rows, D))  # eager work between replays
+        rt.layernorm_into_f32(scratch, devs[0].vec["norm1_gamma"], devs[0].vec["norm1_beta"],
+                              rows, D, 1e-6, scratch)
+        rt.synchronize()
