@@ -598,6 +598,27 @@ int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
                              size_t view_count, const vk_tensor* camera,
                              const vk_vit_block_workspace* ws);
 
+/* The backbone's block loop on the device: Backbone::forward /
+ * forward_multi_view_ordered (backbone.rs:390-532, 688-877) over `depth`
+ * blocks (blocks[layer], vk_vit_block_forward_f32 each) on the view-major
+ * tokens [view_count * (1+num_register+gh*gw), D], in place.  At each
+ * out_layers[i] (in the caller's order) the capture of vk_capture_f32 with
+ * the final vit.norm (norm_gamma/beta, cfg->ln_eps) fills feats[i]
+ * [views, gh*gw, W] and cams[i] [views, W] (W = 2D with cat_token, else D);
+ * captures at global layers pair the stream with local_x, the snapshot of
+ * the last local layer (backbone.rs:816-830, 832-834).  local_x [rows*D] is
+ * needed only when cat_token and some out layer is global (else NULL). */
+int vk_backbone_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
+                            size_t depth, const vk_vit_block_weights* blocks,
+                            vk_tensor* tokens, size_t gh, size_t gw,
+                            size_t view_count, const vk_tensor* camera,
+                            const vk_tensor* norm_gamma,
+                            const vk_tensor* norm_beta, int cat_token,
+                            const int* out_layers, size_t n_out,
+                            vk_tensor* const* feats, vk_tensor* const* cams,
+                            const vk_vit_block_workspace* ws,
+                            vk_tensor* local_x);
+
 /* ------------------------------------------------------------------ */
 /* timing and graphs                                                    */
 /* ------------------------------------------------------------------ */

@@ -488,3 +488,30 @@ def preprocess_resize_u8(img_hwc, image_size: int, patch: int, upper_bound: bool
     lib.ora_preprocess_resize_u8(_p(img), h, w, image_size, patch, 1 if upper_bound else 0,
                                  _p(out))
     return out
+
+
+def backbone_forward(tokens, blocks: list, cfg: dict, gh: int, gw: int, view_count: int,
+                     camera, norm_gamma, norm_beta, cat_token: bool, out_layers):
+    """Backbone::forward_multi_view_ordered (backbone.rs:688-877) on the
+    view-major token rows: block_forward per layer, the snapshot local_x
+    after every local layer, post_process_capture at each out layer in the
+    caller's order (global layers pair the stream with local_x).  Returns
+    (tokens, [(feat, cam) per out layer])."""
+    D = cfg["embed_dim"]
+    n = 1 + cfg["num_register"] + gh * gw
+    alt = cfg["alt_start"]
+    x = _f32(tokens).reshape(n * view_count, D).copy()
+    local_x = x.copy()
+    out = [None] * len(out_layers)
+    for layer, p in enumerate(blocks):
+        x = block_forward(x, p, cfg, layer, gh, gw, view_count, camera)["tokens"]
+        glob = alt >= 0 and layer >= alt and layer % 2 == 1
+        for i, want in enumerate(out_layers):
+            if want == layer:
+                out[i] = capture(local_x if glob else x, x, n, 1 + cfg["num_register"], D,
+                                 view_count, norm_gamma, norm_beta, cfg["ln_eps"], cat_token)
+        if not glob:
+            local_x = x.copy()
+    if any(o is None for o in out):
+        raise ValueError("an out layer was never reached")
+    return x, out

@@ -119,3 +119,33 @@ def block_f64(tokens, p, cfg, layer, gh, gw, views, camera=None):
     return {"tokens": x, "q": q, "k": k, "v": v, "attn": attn, "ln2": ln2, "hidden": hidden}
 
 
+
+
+def backbone_f64(tokens, blocks, cfg, gh, gw, views, camera, norm_gamma, norm_beta, cat,
+                 out_layers):
+    """float64 twin of the backbone block loop with its captures
+    (backbone.rs:688-877, 1139-1179)."""
+    D = cfg["embed_dim"]
+    ns = 1 + cfg["num_register"]
+    n = ns + gh * gw
+    x = tokens.astype(np.float64).reshape(n * views, D)
+    local = x.copy()
+    out = [None] * len(out_layers)
+    for layer, p in enumerate(blocks):
+        x = block_f64(x, p, cfg, layer, gh, gw, views, camera)["tokens"]
+        glob = is_global(cfg, layer)
+        for i, want in enumerate(out_layers):
+            if want != layer:
+                continue
+            xv = x.reshape(views, n, D)
+            lv = (local if glob else x).reshape(views, n, D)
+            normed = _ln64(xv[:, ns:], norm_gamma.astype(np.float64),
+                           norm_beta.astype(np.float64), cfg["ln_eps"])
+            if cat:
+                out[i] = (np.concatenate([lv[:, ns:], normed], axis=2),
+                          np.concatenate([lv[:, 0], xv[:, 0]], axis=1))
+            else:
+                out[i] = (normed, xv[:, 0].copy())
+        if not glob:
+            local = x.copy()
+    return x, out

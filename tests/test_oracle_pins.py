@@ -593,3 +593,38 @@ def test_resize_area_matches_exact_box_integral(rng):
     exact = np.einsum("yi,xj,ijc->yxc", box(sh, dh), box(sw, dw), img)
     got = oracle.resize_u8(img.astype(np.uint8), dh, dw, "area").astype(np.float64)
     assert np.max(np.abs(got - np.rint(exact))) <= 1.0
+
+
+# ---------------------------------------------------------------- backbone loop
+def test_backbone_captures_follow_the_reference_rules(rng):
+    """backbone.rs:1287-1372: captures in the requested (not execution) order,
+    widths 2*embed (cat_token) or embed, n_patch rows, finite, distinct per
+    layer; global layers pair the stream with the snapshot of the last local
+    layer (backbone.rs:816-830); matches the float64 twin."""
+    from block_twin import backbone_f64, config, make_params, normals
+    D, H, M, gh, gw, views = 64, 1, 128, 2, 2, 2
+    cfg = config(D, H, M, alt=2)
+    blocks = [make_params(rng, D, M) for _ in range(6)]
+    n = 2 + gh * gw
+    x0, cam = normals(rng, views * n, D), normals(rng, 2 * D)
+    ng, nb = normals(rng, D, scale=0.02, shift=1), normals(rng, D, scale=0.02)
+    outs = [3, 1, 5]
+    x, caps = oracle.backbone_forward(x0, blocks, cfg, gh, gw, views, cam, ng, nb, True, outs)
+    for feat, c in caps:
+        assert feat.shape == (views, gh * gw, 2 * D) and c.shape == (views, 2 * D)
+        assert np.isfinite(feat).all() and np.isfinite(c).all()
+    assert not np.array_equal(caps[0][0], caps[1][0])
+    assert not np.array_equal(caps[1][0], caps[2][0])
+    # layer 3 is global: its local half is the stream after layer 2
+    x2 = x0.reshape(-1, D)
+    for layer in range(3):
+        x2 = oracle.block_forward(x2, blocks[layer], cfg, layer, gh, gw, views, cam)["tokens"]
+    assert np.array_equal(caps[0][0][:, :, :D], x2.reshape(views, n, D)[:, 2:])
+    # the float64 twin
+    x64, caps64 = backbone_f64(x0, blocks, cfg, gh, gw, views, cam, ng, nb, True, outs)
+    assert np.max(np.abs(x - x64)) < 1e-5
+    for (f, c), (f64, c64) in zip(caps, caps64):
+        assert np.max(np.abs(f - f64)) < 2e-5 and np.max(np.abs(c - c64)) < 1e-5
+    # without cat_token: single width, the camera row of the stream
+    _, caps1 = oracle.backbone_forward(x0, blocks, cfg, gh, gw, views, cam, ng, nb, False, [4])
+    assert caps1[0][0].shape == (views, gh * gw, D) and caps1[0][1].shape == (views, D)

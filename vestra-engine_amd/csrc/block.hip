@@ -240,3 +240,61 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
   VK_TRY(vk_linear_run_residual_f32(rt, w->fc2, ws->hidden, rows, tokens));
   return VK_OK;
 }
+
+// ---------------------------------------------------------------------------
+// The backbone's block loop on the device (Backbone::forward and
+// forward_multi_view_ordered, backbone.rs:390-532, 688-877): every block on
+// the view-major residual stream, the pre-alternation snapshot local_x kept
+// after each local layer, and the capture (final LayerNorm + cat) at each
+// requested layer, in the order the caller lists them.
+// ---------------------------------------------------------------------------
+extern "C" int vk_backbone_forward_f32(vk_runtime* rt, const vk_vit_config* cfg, size_t depth,
+                                       const vk_vit_block_weights* blocks, vk_tensor* tokens,
+                                       size_t gh, size_t gw, size_t view_count,
+                                       const vk_tensor* camera, const vk_tensor* norm_gamma,
+                                       const vk_tensor* norm_beta, int cat_token,
+                                       const int* out_layers, size_t n_out,
+                                       vk_tensor* const* feats, vk_tensor* const* cams,
+                                       const vk_vit_block_workspace* ws, vk_tensor* local_x) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(cfg && blocks && tokens && ws, "null argument");
+  VK_REQUIRE(n_out == 0 || (out_layers && feats && cams), "null capture arrays");
+  VK_REQUIRE(view_count > 0, "empty view count");
+  const size_t D = cfg->embed_dim;
+  const size_t n_special = 1 + cfg->num_register;
+  const size_t n = n_special + gh * gw;
+  const size_t rows = n * view_count;
+  const size_t width = cat_token ? 2 * D : D;
+  VK_TRY(check_len(tokens, rows * D, "tokens"));
+  // every requested layer must be reached (backbone.rs:1085-1095 panics otherwise)
+  bool any_global_capture = false;
+  for (size_t i = 0; i < n_out; ++i) {
+    VK_REQUIRE(out_layers[i] >= 0 && static_cast<size_t>(out_layers[i]) < depth,
+               "out layer %d was never reached (depth %zu)", out_layers[i], depth);
+    VK_REQUIRE(feats[i] && cams[i], "null capture tensor for out layer %d", out_layers[i]);
+    VK_TRY(check_len(feats[i], view_count * (n - n_special) * width, "capture feat"));
+    VK_TRY(check_len(cams[i], view_count * width, "capture cam"));
+    any_global_capture = any_global_capture ||
+                         layer_uses_global(cfg, static_cast<size_t>(out_layers[i]));
+  }
+  // the snapshot is read only by captures at global layers with cat_token
+  const bool keep_local = cat_token && any_global_capture;
+  if (keep_local) VK_TRY(check_len(local_x, rows * D, "local_x"));
+  if (keep_local) VK_TRY(vk_copy_segment_into_f32(rt, local_x, 0, tokens, 0, rows * D));
+  for (size_t layer = 0; layer < depth; ++layer) {
+    VK_TRY(vk_vit_block_forward_f32(rt, cfg, layer, &blocks[layer], tokens, gh, gw, view_count,
+                                    camera, ws));
+    const bool global = layer_uses_global(cfg, layer);
+    for (size_t i = 0; i < n_out; ++i) {
+      if (static_cast<size_t>(out_layers[i]) != layer) continue;
+      // local layers capture against the current stream, global ones against
+      // the snapshot of the last local layer (backbone.rs:816-830)
+      const vk_tensor* local = cat_token ? (global ? local_x : tokens) : nullptr;
+      VK_TRY(vk_capture_f32(rt, local, tokens, n, n_special, D, view_count, norm_gamma,
+                            norm_beta, cfg->ln_eps, cat_token, feats[i], cams[i]));
+    }
+    if (keep_local && !global)
+      VK_TRY(vk_copy_segment_into_f32(rt, local_x, 0, tokens, 0, rows * D));
+  }
+  return VK_OK;
+}

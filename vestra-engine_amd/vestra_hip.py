@@ -178,6 +178,10 @@ _SIGS = {
     "vk_vit_block_forward_f32": (
         [_vp, C.POINTER(VitConfig), _sz, C.POINTER(VitBlockWeights), _vp, _sz, _sz, _sz, _vp,
          C.POINTER(VitBlockWorkspace)], _i),
+    "vk_backbone_forward_f32": (
+        [_vp, C.POINTER(VitConfig), _sz, C.POINTER(VitBlockWeights), _vp, _sz, _sz, _sz, _vp,
+         _vp, _vp, _i, C.POINTER(C.c_int), _sz, C.POINTER(_vp), C.POINTER(_vp),
+         C.POINTER(VitBlockWorkspace), _vp], _i),
     "vk_event_create": ([_vp, _pp], _i),
     "vk_event_destroy": ([_vp], _i),
     "vk_event_record": ([_vp, _vp], _i),
@@ -702,6 +706,24 @@ class Runtime:
         _check(lib.vk_vit_block_forward_f32(self.handle, C.byref(cfg), layer_idx,
                                             C.byref(weights), tokens.handle, gh, gw, view_count,
                                             _h(camera), C.byref(ws)))
+
+    def backbone_forward_f32(self, cfg: VitConfig, blocks: Sequence[VitBlockWeights],
+                             tokens: Tensor, gh: int, gw: int, view_count: int,
+                             camera: Optional[Tensor], norm_gamma: Tensor, norm_beta: Tensor,
+                             cat_token: bool, out_layers: Sequence[int],
+                             feats: Sequence[Tensor], cams: Sequence[Tensor],
+                             ws: "BlockWorkspace", local_x: Optional[Tensor]) -> None:
+        """Backbone::forward_multi_view_ordered: all blocks + captures on the device."""
+        arr = (VitBlockWeights * len(blocks))(*blocks)
+        n = len(out_layers)
+        layers = (C.c_int * max(n, 1))(*out_layers)
+        fa = (_vp * max(n, 1))(*[f.handle.value for f in feats])
+        ca = (_vp * max(n, 1))(*[c.handle.value for c in cams])
+        _check(lib.vk_backbone_forward_f32(self.handle, C.byref(cfg), len(blocks), arr,
+                                           tokens.handle, gh, gw, view_count, _h(camera),
+                                           norm_gamma.handle, norm_beta.handle,
+                                           1 if cat_token else 0, layers, n, fa, ca,
+                                           C.byref(ws.struct), _h(local_x)))
 
     def block_workspace(self, rows: int, embed: int, mlp: int) -> "BlockWorkspace":
         return BlockWorkspace(self, rows, embed, mlp)
