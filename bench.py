@@ -349,6 +349,98 @@ def full_block_timing(rt, rng, reps=3):
     return out
 
 
+OUT_LAYERS = [2, 5, 8, 11]  # the DA3-Base capture layers of the reference's config tests
+
+
+def pipeline_timing(rt, rng, reps=3):
+    """The image-to-head-input path on the device, per frame: a 427x640 u8
+    camera frame resized and patch-snapped to 336x504 (area resampling,
+    vk_preprocess_resize_u8), the fused patch embedding with the bicubic
+    position table (built once and cached, as PosEmbedCache does), the 12
+    ViT-B blocks with captures at layers 2, 5, 8, 11 (vk_backbone_forward_f32,
+    cat_token) and the head's LayerNorm + token -> CHW hand-off of each
+    capture (vk_token_to_chw_f32).  One frame, and 12 frames as one
+    multi-view pass.  Frames are device-resident u8 at the start; the whole
+    pass is one HIP graph."""
+    import vestra_hip as vh
+
+    def n(*sh, scale=1.0, shift=0.0):
+        return (shift + scale * rng.standard_normal(sh)).astype(np.float32)
+
+    fh, fw = 427, 640
+    oh, ow = rt.preprocess_shape(fh, fw, 504, 14)
+    gh, gw = oh // 14, ow // 14
+    assert (gh, gw) == (GH, GW)
+    cfg = vh.VitConfig(embed_dim=D, num_heads=H, head_dim=HD, mlp_hidden=M, num_register=NREG,
+                       ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0, rope_start=0,
+                       qknorm_start=0, alt_start=ALT)
+    keep, blocks = [], []
+    for _ in range(DEPTH):
+        vec = {"norm1_gamma": n(D, scale=0.02, shift=1), "norm1_beta": n(D, scale=0.02),
+               "norm2_gamma": n(D, scale=0.02, shift=1), "norm2_beta": n(D, scale=0.02),
+               "qnorm_gamma": n(HD, scale=0.02, shift=1), "qnorm_beta": n(HD, scale=0.02),
+               "knorm_gamma": n(HD, scale=0.02, shift=1), "knorm_beta": n(HD, scale=0.02)}
+        dev = {k: rt.upload_f32(v) for k, v in vec.items()}
+        lin = {"qkv": rt.prepare_linear_f32(D, 3 * D, n(D, 3 * D, scale=0.02),
+                                            n(3 * D, scale=0.02)),
+               "proj": rt.prepare_linear_f32(D, D, n(D, D, scale=0.02), n(D, scale=0.02),
+                                             rng.uniform(0, 0.1, D).astype(np.float32)),
+               "fc1": rt.prepare_linear_f32(D, M, n(D, M, scale=0.02), n(M, scale=0.02)),
+               "fc2": rt.prepare_linear_f32(M, D, n(M, D, scale=0.02), n(D, scale=0.02),
+                                            rng.uniform(0, 0.1, D).astype(np.float32))}
+        keep.append((dev, lin))
+        blocks.append(vh.block_weights_struct(**dev, **lin))
+    patch = rt.prepare_linear_oihw_f32(588, D, n(D, 3, 14, 14, scale=0.02), n(D, scale=0.02))
+    cls, reg = rt.upload_f32(n(D, scale=0.02)), rt.upload_f32(n(D, scale=0.02))
+    pos = rt.pos_embed_bicubic_f32(rt.upload_f32(n(37 * 37 + 1, D, scale=0.02)), 37, D, gh, gw)
+    camera = rt.upload_f32(n(2 * D, scale=0.02))
+    vit_ng, vit_nb = rt.upload_f32(n(D, scale=0.02, shift=1)), rt.upload_f32(n(D, scale=0.02))
+    head_ng = rt.upload_f32(n(2 * D, scale=0.02, shift=1))
+    head_nb = rt.upload_f32(n(2 * D, scale=0.02))
+    mean, std = [0.485, 0.456, 0.406], [0.229, 0.224, 0.225]
+    n_patch = gh * gw
+    out = {"frame": f"{fh}x{fw} u8 -> {oh}x{ow}", "blocks": DEPTH, "out_layers": OUT_LAYERS}
+    for name, views in (("single_image", 1), ("12view", 12)):
+        rows = TPV * views
+        frames = [rt.upload_u8(rng.integers(0, 256, (fh, fw, 3), dtype=np.uint8))
+                  for _ in range(views)]
+        resized = [rt.alloc_u8(oh * ow * 3) for _ in range(views)]
+        tokens = rt.alloc_f32(rows * D)
+        token_views = [tokens.view(v * TPV * D, TPV * D) for v in range(views)]
+        ws = rt.block_workspace(rows, D, M)
+        local = rt.alloc_f32(rows * D)
+        feats = [rt.alloc_f32(views * n_patch * 2 * D) for _ in OUT_LAYERS]
+        cams = [rt.alloc_f32(views * 2 * D) for _ in OUT_LAYERS]
+        chw = [rt.alloc_f32(n_patch * 2 * D) for _ in range(views * len(OUT_LAYERS))]
+        feat_views = [[f.view(v * n_patch * 2 * D, n_patch * 2 * D) for v in range(views)]
+                      for f in feats]
+        pre_ws = [rt.alloc_u8(int(vh.lib.vk_preprocess_workspace_bytes(fh, fw, 504, 14, 1)))
+                  for _ in range(views)]
+
+        def step():
+            for v in range(views):
+                vh._check(vh.lib.vk_preprocess_resize_u8(rt.handle, frames[v].handle, fh, fw, 504,
+                                                         14, 1, pre_ws[v].handle,
+                                                         resized[v].handle))
+                rt.patch_embed_u8(resized[v], oh, ow, 14, mean, std, patch, cls, reg, NREG, pos,
+                                  token_views[v])
+            rt.backbone_forward_f32(cfg, blocks, tokens, gh, gw, views, camera, vit_ng, vit_nb,
+                                    True, OUT_LAYERS, feats, cams, ws, local)
+            for i in range(len(OUT_LAYERS)):
+                for v in range(views):
+                    rt.token_to_chw_f32(feat_views[i][v], n_patch, 2 * D, head_ng, head_nb, 1e-5,
+                                        chw[i * views + v])
+
+        step()
+        graph = capture(rt, step)
+        graph.launch()
+        ms = statistics.median(time_loop(rt, graph.launch, 1) for _ in range(reps))
+        out[name] = {"views": views, "ms_per_pass": round(ms, 3),
+                     "ms_per_frame": round(ms / views, 3)}
+        del graph
+    return out
+
+
 # ViT-L 1008x672: 3,456 patches (48 x 72) + CLS + camera slot, D 1024,
 # 16 heads, MLP 4096, 24 blocks; parameters stored as IEEE binary16.  The
 # alternation start of this shape is not fixed by the reference's tests: 8.
@@ -614,6 +706,9 @@ def main():
     ap.add_argument("--full-block", action="store_true",
                     help="whole-block mode: 12 complete ViT-B blocks on the device "
                          "(projections and attention included), single image and 12 views")
+    ap.add_argument("--pipeline", action="store_true",
+                    help="pipeline mode: frame -> preprocess -> patch embedding -> 12 blocks "
+                         "with captures -> head hand-off, one frame and 12 frames")
     ap.add_argument("--vitl", action="store_true",
                     help="ViT-L mode: the 1008x672 configuration with F16-stored weights "
                          "(24-block fused ops and whole blocks)")
@@ -645,6 +740,9 @@ def main():
         return
     if args.full_block:
         print(json.dumps({"full_block": full_block_timing(rt, rng)}), flush=True)
+        return
+    if args.pipeline:
+        print(json.dumps({"pipeline": pipeline_timing(rt, rng)}), flush=True)
         return
     if args.vitl:
         print(json.dumps({"vitl": vitl_timing(rt, rng)}), flush=True)
@@ -713,6 +811,8 @@ def main():
     full_block = full_block_timing(rt, rng)
     log("ViT-L 1008x672, F16-stored weights")
     vitl = vitl_timing(rt, rng)
+    log("frame-to-head-input pipeline")
+    pipeline = pipeline_timing(rt, rng)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -748,6 +848,7 @@ def main():
         "attention": attention,
         "full_block": full_block,
         "vitl_1008x672": vitl,
+        "pipeline": pipeline,
         "roofline": {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
                      "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),

@@ -228,6 +228,18 @@ class Tensor:
     def device_ptr(self) -> int:
         return int(lib.vk_tensor_device_ptr(self.handle) or 0)
 
+    def view(self, offset: int, length: int) -> "Tensor":
+        """Non-owning f32 view of elements [offset, offset + length); keeps
+        this tensor alive while the view lives."""
+        if offset < 0 or length < 0 or offset + length > len(self):
+            raise VestraError(VK_ERR_INVALID, "view out of range")
+        out = C.c_void_p()
+        _check(lib.vk_tensor_wrap(self.rt.handle, 0, self.device_ptr + 4 * offset, length,
+                                  C.byref(out)))
+        t = Tensor(self.rt, out)
+        t._base = self
+        return t
+
     def numpy(self) -> np.ndarray:
         return self.rt.download_f32(self)
 
