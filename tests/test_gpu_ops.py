@@ -257,3 +257,43 @@ def test_rope_positions_bit_exact(rt):
     for args in ((2, 24, 36, 12, False), (2, 24, 36, 12, True), (1, 3, 5, 2, False)):
         got = rt.rope_positions_f32(*args).numpy().reshape(-1, 2)
         assert np.array_equal(got, oracle.rope_positions(*args))
+
+
+def test_rope_table_growth_keeps_captured_graphs_valid(rt, rng):
+    """A grid wider than the default table (1,100 patches) grows the runtime's
+    cos/sin table; a graph captured before the growth still reads the table
+    it was captured with (kept alive until the runtime ends), and the wide
+    grid's rotation matches the oracle bit for bit."""
+    import gc
+    heads, n_special = 2, 2
+    small = (3, 5)
+    n = n_special + small[0] * small[1]
+    q, k = normals(rng, heads, n, 64), normals(rng, heads, n, 64)
+    tq, tk = rt.upload_f32(q), rt.upload_f32(k)
+
+    def small_step():
+        rt.qk_norm_rope_grid_f32(tq, tk, None, None, None, None, heads, 64, n_special, *small, 1,
+                                 False, vh.VK_QK_HEADS_OUTER)
+
+    small_step()
+    want = tq.numpy()
+    rt.synchronize()
+    gc.disable()
+    try:
+        rt.begin_capture()
+        small_step()
+        graph = rt.end_capture()
+    finally:
+        gc.enable()
+    gh, gw = 1, 1100
+    nw = n_special + gh * gw
+    qw, kw = normals(rng, heads, nw, 64), normals(rng, heads, nw, 64)
+    twq, twk = rt.upload_f32(qw), rt.upload_f32(kw)
+    rt.qk_norm_rope_grid_f32(twq, twk, None, None, None, None, heads, 64, n_special, gh, gw, 1,
+                             False, vh.VK_QK_HEADS_OUTER)
+    pos = oracle.rope_positions(n_special, gh, gw, 1, False).astype(np.int64)
+    assert np.array_equal(twq.numpy().reshape(heads, nw, 64), oracle.rope2d(qw, heads, nw, 64, pos))
+    tq.write(q)
+    graph.launch()
+    rt.synchronize()
+    assert np.array_equal(tq.numpy(), want)

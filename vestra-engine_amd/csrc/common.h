@@ -26,11 +26,13 @@ struct vk_runtime {
   // position the table covers.
   std::map<std::pair<uint32_t, int>, std::pair<float*, int>> rope_tables;
   // Partial sums of split-K linears (f32).  Grown only outside stream
-  // capture; a replaced buffer is kept until the runtime is destroyed, since
-  // graphs captured earlier may still name it.
+  // capture.
   float* splitk = nullptr;
   size_t splitk_len = 0;
-  std::vector<float*> splitk_retired;
+  // Replaced device buffers (split-K partials, smaller RoPE tables): graphs
+  // captured earlier may still name them, so they live until the runtime
+  // is destroyed.
+  std::vector<void*> retired;
 };
 
 struct vk_tensor {

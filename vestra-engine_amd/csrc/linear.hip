@@ -367,7 +367,7 @@ int ensure_splitk(vk_runtime* rt, size_t need) {
   if (len < (size_t{8} << 20)) len = size_t{8} << 20;
   float* p = nullptr;
   VK_HIP(hipMalloc(reinterpret_cast<void**>(&p), len * sizeof(float)));
-  if (rt->splitk) rt->splitk_retired.push_back(rt->splitk);
+  if (rt->splitk) rt->retired.push_back(rt->splitk);
   rt->splitk = p;
   rt->splitk_len = len;
   return VK_OK;

@@ -93,6 +93,11 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const 
   }
   for (int j = 0; j < quarter; ++j) host[entries * 32 + j] = inv_freq[j];
   VK_TRY(bind(rt));
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  VK_HIP(hipStreamIsCapturing(rt->stream, &st));
+  VK_REQUIRE(st == hipStreamCaptureStatusNone,
+             "RoPE table for positions up to %d must be built before stream capture "
+             "(run the sequence once eagerly first)", min_max_pos);
   float* dev = nullptr;
   VK_HIP(hipMalloc(&dev, host.size() * sizeof(float)));
   hipError_t e = hipMemcpy(dev, host.data(), host.size() * sizeof(float),
@@ -102,9 +107,9 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const 
     return hip_fail(e, "hipMemcpy(rope table)");
   }
   if (it != rt->rope_tables.end()) {
-    // the smaller table may still be read by queued kernels
-    (void)hipStreamSynchronize(rt->stream);
-    (void)hipFree(it->second.first);
+    // the smaller table may still be read by queued kernels or named by a
+    // graph captured earlier: keep it until the runtime is destroyed
+    rt->retired.push_back(it->second.first);
   }
   rt->rope_tables[key] = std::make_pair(dev, max_pos);
   *out = dev;
@@ -186,7 +191,7 @@ int vk_runtime_destroy(vk_runtime* rt) {
   (void)hipStreamSynchronize(rt->stream);
   for (auto& kv : rt->rope_tables) (void)hipFree(kv.second.first);
   if (rt->splitk) (void)hipFree(rt->splitk);
-  for (float* p : rt->splitk_retired) (void)hipFree(p);
+  for (void* p : rt->retired) (void)hipFree(p);
   (void)hipStreamDestroy(rt->stream);
   delete rt;
   return VK_OK;
