@@ -8,12 +8,15 @@
 //    or LN(x); the camera/CLS row 0 goes to cam.  One wave per patch row
 //    (plus one per view for the camera row), the row held in registers as
 //    in the block LayerNorm; one launch covers all views.
-//  * token_chw_rows: token_major_to_chw_with_optional_layernorm
-//    (dpt_head.rs:260-301).  A 256-thread workgroup owns 64 tokens: the four
-//    waves compute the 64 rows' mean and 1/std (one wave per row, registers),
-//    then the rows are streamed again in 64-channel chunks, normalised and
-//    transposed through a [64][65] LDS tile so both the row reads and the
-//    channel-major writes are contiguous 256-byte runs.
+//  * chw_row_stats + chw_tiles: token_major_to_chw_with_optional_layernorm
+//    (dpt_head.rs:260-301).  One image's hand-off is a few hundred tokens,
+//    too few rows to fill the chip if a workgroup owned whole rows, so the
+//    LayerNorm statistics come first (one wave per row, mean and 1/std into
+//    the runtime's work buffer) and the transpose is then tiled over
+//    (64 tokens x 64 channels): each tile is read as 64 contiguous 256-byte
+//    row pieces, normalised, turned through a [64][65] LDS tile and written
+//    as 64 contiguous 256-byte channel pieces.  A 864-token, 1536-channel
+//    hand-off is 14 x 24 = 336 workgroups.
 //
 // Row statistics and the per-element formula are vkd::row_mean_inv and
 // vkd::ln_apply4, shared with the block LayerNorm: a captured or handed-off
@@ -82,66 +85,72 @@ __global__ __launch_bounds__(64) void capture_rows(const float* __restrict__ loc
   }
 }
 
-constexpr int kChwTok = 64;  // tokens per workgroup
-constexpr int kChwCh = 64;   // channels per transposed chunk
+constexpr int kChwTok = 64;  // tokens per tile
+constexpr int kChwCh = 64;   // channels per tile
 
-template <int NV, typename PT, bool EXACT, bool NORM>
-__global__ __launch_bounds__(256) void token_chw_rows(const float* __restrict__ tok,
-                                                      const PT* __restrict__ gamma,
-                                                      const PT* __restrict__ beta,
-                                                      float* __restrict__ out, int n_tok, int C,
-                                                      float eps) {
-  __shared__ float mean_s[kChwTok], inv_s[kChwTok];
+// stats[2 t] = mean, stats[2 t + 1] = 1/std of token row t; wave per row.
+template <int NV, bool EXACT>
+__global__ __launch_bounds__(256) void chw_row_stats(const float* __restrict__ tok,
+                                                     float* __restrict__ stats, int n_tok, int C,
+                                                     float eps) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= n_tok) return;
+  const int nvec = C >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(tok + static_cast<size_t>(t) * C);
+  float4 vv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    vv[i] = (EXACT || c < nvec) ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float mean, inv;
+  vkd::row_mean_inv<NV, EXACT>(vv, lane, C, eps, &mean, &inv);
+  if (lane == 0) *reinterpret_cast<float2*>(stats + 2 * static_cast<size_t>(t)) =
+      make_float2(mean, inv);
+}
+
+// One (64-token x 64-channel) tile per workgroup; blockIdx.x = token tile,
+// blockIdx.y = channel tile.
+template <typename PT, bool NORM>
+__global__ __launch_bounds__(256) void chw_tiles(const float* __restrict__ tok,
+                                                 const float* __restrict__ stats,
+                                                 const PT* __restrict__ gamma,
+                                                 const PT* __restrict__ beta,
+                                                 float* __restrict__ out, int n_tok, int C) {
   __shared__ float tile[kChwCh][kChwTok + 1];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int t0 = blockIdx.x * kChwTok;
-  const int nvec = C >> 2;
-  if (NORM) {
-    for (int rr = wave; rr < kChwTok && t0 + rr < n_tok; rr += 4) {
-      const float4* xr = reinterpret_cast<const float4*>(tok + static_cast<size_t>(t0 + rr) * C);
-      float4 vv[NV];
+  const int c0 = blockIdx.y * kChwCh;
+  // 64 tokens x 16 float4: slot s = tid + 256 j -> token s/16, float4 s%16.
+  // LDS bank of tile[4 c4 + k][rr] is (4 c4 + rr) mod 64: one wave's 64
+  // lanes (16 c4 x 4 rr) hit 64 distinct banks.
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = lane + i * 64;
-        vv[i] = (EXACT || c < nvec) ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < 4; ++j) {
+    const int s = tid + 256 * j;
+    const int rr = s >> 4, c4 = s & 15;
+    const int t = t0 + rr, c = c0 + 4 * c4;
+    if (t < n_tok && c < C) {
+      float4 xv = *reinterpret_cast<const float4*>(tok + static_cast<size_t>(t) * C + c);
+      if (NORM) {
+        const float2 st = *reinterpret_cast<const float2*>(stats + 2 * static_cast<size_t>(t));
+        xv = vkd::ln_apply4(xv, st.x, st.y, Param<PT>::load4(gamma, c >> 2),
+                            Param<PT>::load4(beta, c >> 2));
       }
-      float mean, inv;
-      vkd::row_mean_inv<NV, EXACT>(vv, lane, C, eps, &mean, &inv);
-      if (lane == 0) {
-        mean_s[rr] = mean;
-        inv_s[rr] = inv;
-      }
+      tile[4 * c4 + 0][rr] = xv.x;
+      tile[4 * c4 + 1][rr] = xv.y;
+      tile[4 * c4 + 2][rr] = xv.z;
+      tile[4 * c4 + 3][rr] = xv.w;
     }
-    __syncthreads();
   }
-  for (int c0 = 0; c0 < C; c0 += kChwCh) {
-    // 64 tokens x 16 float4: slot s = tid + 256 j -> token s/16, float4 s%16
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int s = tid + 256 * j;
-      const int rr = s >> 4, c4 = s & 15;
-      const int t = t0 + rr, c = c0 + 4 * c4;
-      if (t < n_tok && c < C) {
-        float4 xv = *reinterpret_cast<const float4*>(tok + static_cast<size_t>(t) * C + c);
-        if (NORM)
-          xv = vkd::ln_apply4(xv, mean_s[rr], inv_s[rr], Param<PT>::load4(gamma, c >> 2),
-                              Param<PT>::load4(beta, c >> 2));
-        tile[4 * c4 + 0][rr] = xv.x;
-        tile[4 * c4 + 1][rr] = xv.y;
-        tile[4 * c4 + 2][rr] = xv.z;
-        tile[4 * c4 + 3][rr] = xv.w;
-      }
-    }
-    __syncthreads();
-    // wave w writes channel rows 16w..16w+15 of the chunk, 64 tokens each
+  __syncthreads();
+  // wave w writes channel rows 16w..16w+15 of the tile, 64 tokens each
 #pragma unroll 4
-    for (int j = 0; j < 16; ++j) {
-      const int cc = wave * 16 + j;
-      const int c = c0 + cc, t = t0 + lane;
-      if (c < C && t < n_tok) out[static_cast<size_t>(c) * n_tok + t] = tile[cc][lane];
-    }
-    __syncthreads();
+  for (int j = 0; j < 16; ++j) {
+    const int cc = wave * 16 + j;
+    const int c = c0 + cc, t = t0 + lane;
+    if (c < C && t < n_tok) out[static_cast<size_t>(c) * n_tok + t] = tile[cc][lane];
   }
 }
 
@@ -194,24 +203,33 @@ int launch_capture(vk_runtime* rt, int nv, bool exact, const float* lx, const fl
 template <typename PT, bool NORM>
 int launch_chw(vk_runtime* rt, int nv, bool exact, const float* tok, const void* g,
                const void* b, float* out, int n_tok, int C, float eps) {
-  const dim3 grid(static_cast<unsigned>((n_tok + kChwTok - 1) / kChwTok)), block(256);
-  auto G = static_cast<const PT*>(g);
-  auto B = static_cast<const PT*>(b);
-#define VK_CHW_CASE(N)                                                                         \
+  const float* stats = nullptr;
+  if (NORM) {
+    VK_TRY(vk::ensure_work(rt, 2 * static_cast<size_t>(n_tok), "token_to_chw"));
+    float* st = rt->work;
+    const dim3 sgrid(static_cast<unsigned>((n_tok + 3) / 4)), sblock(256);
+#define VK_STAT_CASE(N)                                                                        \
   case N:                                                                                      \
     if (exact)                                                                                 \
-      hipLaunchKernelGGL((token_chw_rows<N, PT, true, NORM>), grid, block, 0, rt->stream, tok, G, B, out, n_tok, C, eps); \
+      hipLaunchKernelGGL((chw_row_stats<N, true>), sgrid, sblock, 0, rt->stream, tok, st, n_tok, C, eps); \
     else                                                                                       \
-      hipLaunchKernelGGL((token_chw_rows<N, PT, false, NORM>), grid, block, 0, rt->stream, tok, G, B, out, n_tok, C, eps); \
+      hipLaunchKernelGGL((chw_row_stats<N, false>), sgrid, sblock, 0, rt->stream, tok, st, n_tok, C, eps); \
     break;
-  switch (nv) {
-    VK_CHW_CASE(1) VK_CHW_CASE(2) VK_CHW_CASE(3) VK_CHW_CASE(4) VK_CHW_CASE(6) VK_CHW_CASE(8)
-    VK_CHW_CASE(12)
-    default:
-      return vk::set_error(VK_ERR_UNSUPPORTED, "token_to_chw: no instance for c=%d", C);
+    switch (nv) {
+      VK_STAT_CASE(1) VK_STAT_CASE(2) VK_STAT_CASE(3) VK_STAT_CASE(4) VK_STAT_CASE(6)
+      VK_STAT_CASE(8) VK_STAT_CASE(12)
+      default:
+        return vk::set_error(VK_ERR_UNSUPPORTED, "token_to_chw: no instance for c=%d", C);
+    }
+#undef VK_STAT_CASE
+    VK_TRY(vk::check_launch("chw_row_stats"));
+    stats = st;
   }
-#undef VK_CHW_CASE
-  return vk::check_launch("token_chw_rows");
+  const dim3 grid(static_cast<unsigned>((n_tok + kChwTok - 1) / kChwTok),
+                  static_cast<unsigned>((C + kChwCh - 1) / kChwCh));
+  hipLaunchKernelGGL((chw_tiles<PT, NORM>), grid, dim3(256), 0, rt->stream, tok, stats,
+                     static_cast<const PT*>(g), static_cast<const PT*>(b), out, n_tok, C);
+  return vk::check_launch("chw_tiles");
 }
 
 }  // namespace

@@ -25,11 +25,14 @@ struct vk_runtime {
   // head_dim): device pointer (owned by the runtime) and the largest
   // position the table covers.
   std::map<std::pair<uint32_t, int>, std::pair<float*, int>> rope_tables;
-  // Partial sums of split-K linears (f32).  Grown only outside stream
+  // Work buffer (f32) of launches that hand intermediate values from one
+  // kernel to the next on the runtime's stream: split-K partial sums, the
+  // row statistics of the token -> CHW hand-off.  Every user is ordered on
+  // `stream`, so one buffer serves all of them.  Grown only outside stream
   // capture.
-  float* splitk = nullptr;
-  size_t splitk_len = 0;
-  // Replaced device buffers (split-K partials, smaller RoPE tables): graphs
+  float* work = nullptr;
+  size_t work_len = 0;
+  // Replaced device buffers (work buffers, smaller RoPE tables): graphs
   // captured earlier may still name them, so they live until the runtime
   // is destroyed.
   std::vector<void*> retired;
@@ -115,6 +118,11 @@ int check_launch(const char* what);
 // it, so call it before any stream capture that uses the table.
 int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
                int* table_max);
+// Makes rt->work hold at least `floats` floats (at least 8 Mi once
+// allocated, doubling on growth).  Growth is refused during stream capture:
+// run the sequence once eagerly first.  The buffer it replaces is retired,
+// not freed.
+int ensure_work(vk_runtime* rt, size_t floats, const char* who);
 
 // Q/K-norm + RoPE parameters of the QKV projection's fused epilogue: the
 // row's token index m gives its position (rows are view-major tokens).

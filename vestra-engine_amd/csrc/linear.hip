@@ -356,23 +356,6 @@ int choose_splits(const vk_runtime* rt, long long tiles, int K) {
   return s < 1 ? 1 : s;
 }
 
-int ensure_splitk(vk_runtime* rt, size_t need) {
-  if (rt->splitk_len >= need) return VK_OK;
-  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  VK_HIP(hipStreamIsCapturing(rt->stream, &st));
-  VK_REQUIRE(st == hipStreamCaptureStatusNone,
-             "linear: the split-K buffer must grow to %zu floats before stream capture "
-             "(run the sequence once eagerly first)", need);
-  size_t len = need > 2 * rt->splitk_len ? need : 2 * rt->splitk_len;
-  if (len < (size_t{8} << 20)) len = size_t{8} << 20;
-  float* p = nullptr;
-  VK_HIP(hipMalloc(reinterpret_cast<void**>(&p), len * sizeof(float)));
-  if (rt->splitk) rt->retired.push_back(rt->splitk);
-  rt->splitk = p;
-  rt->splitk_len = len;
-  return VK_OK;
-}
-
 template <int EPI, int LAY, int QKN = 0>
 void launch_pair(vk_runtime* rt, const LinearArgs& g, dim3 grid) {
   hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN>), grid, dim3(kThreads), 0, rt->stream, g);
@@ -395,8 +378,8 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   VK_UNSUPPORTED_IF(tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", tiles);
   if (g.splits > 1) {
     VK_REQUIRE(g.N % 4 == 0, "linear: split-K needs out_features % 4 == 0");
-    VK_TRY(ensure_splitk(rt, static_cast<size_t>(g.splits) * g.M * g.N));
-    g.partial = rt->splitk;
+    VK_TRY(vk::ensure_work(rt, static_cast<size_t>(g.splits) * g.M * g.N, "linear (split-K)"));
+    g.partial = rt->work;
   }
   const dim3 grid(static_cast<unsigned>(tiles * g.splits));
   if (g.q_out) {

@@ -117,6 +117,24 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const 
   return VK_OK;
 }
 
+int ensure_work(vk_runtime* rt, size_t floats, const char* who) {
+  if (rt->work_len >= floats) return VK_OK;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  VK_HIP(hipStreamIsCapturing(rt->stream, &st));
+  VK_REQUIRE(st == hipStreamCaptureStatusNone,
+             "%s: the work buffer must grow to %zu floats before stream capture "
+             "(run the sequence once eagerly first)", who, floats);
+  size_t len = floats > 2 * rt->work_len ? floats : 2 * rt->work_len;
+  if (len < (size_t{8} << 20)) len = size_t{8} << 20;
+  float* p = nullptr;
+  VK_HIP(hipMalloc(reinterpret_cast<void**>(&p), len * sizeof(float)));
+  // queued kernels or graphs captured earlier may still name the old one
+  if (rt->work) rt->retired.push_back(rt->work);
+  rt->work = p;
+  rt->work_len = len;
+  return VK_OK;
+}
+
 static int new_tensor(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** out) {
   VK_REQUIRE(out != nullptr, "null output handle");
   VK_REQUIRE(dtype == VK_F32 || dtype == VK_F16 || dtype == VK_U8,
@@ -190,7 +208,7 @@ int vk_runtime_destroy(vk_runtime* rt) {
   VK_TRY(bind(rt));
   (void)hipStreamSynchronize(rt->stream);
   for (auto& kv : rt->rope_tables) (void)hipFree(kv.second.first);
-  if (rt->splitk) (void)hipFree(rt->splitk);
+  if (rt->work) (void)hipFree(rt->work);
   for (void* p : rt->retired) (void)hipFree(p);
   (void)hipStreamDestroy(rt->stream);
   delete rt;
