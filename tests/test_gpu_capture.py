@@ -111,3 +111,67 @@ def test_capture_and_chw_errors(rt, rng):
     with pytest.raises(vh.VestraError):
         rt.token_to_chw_f32(t, 8, 16, None, None, 1e-5, t)        # aliasing
     rt.token_to_chw_f32(rt.alloc_f32(0), 0, 16, None, None, 1e-5, rt.alloc_f32(0))
+
+
+def test_chw_work_buffer_capture_rules(rng):
+    """The hand-off's row statistics live in the runtime's work buffer:
+    the first use inside a stream capture is refused (the buffer cannot be
+    allocated there), a graph captured after an eager call replays
+    correctly, and it still does after a larger call has replaced the
+    buffer (the old one is kept until the runtime ends)."""
+    import gc
+    rt = vh.Runtime(0)  # fresh runtime: no work buffer yet
+    _work_buffer_case(rt, rng)
+    gc.collect()  # every tensor and graph of the case is gone
+    rt.close()    # (left open when the case fails: its tensors may live on)
+
+
+def _work_buffer_case(rt, rng):
+    import gc
+    n_tok, c = 100, 768
+    tok = normals(rng, n_tok, c)
+    g, b = _params(rng, c, False)
+    td, gd, bd = rt.upload_f32(tok), rt.upload_f32(g), rt.upload_f32(b)
+    out = rt.alloc_f32(n_tok * c)
+
+    def step():
+        rt.token_to_chw_f32(td, n_tok, c, gd, bd, 1e-5, out)
+
+    rt.synchronize()
+    gc.disable()
+    try:
+        rt.begin_capture()
+        with pytest.raises(vh.VestraError, match="before stream capture"):
+            step()
+        rt.end_capture()
+    finally:
+        gc.enable()
+    step()
+    want = out.numpy()
+    ln = rt.alloc_f32(n_tok * c)
+    rt.layernorm_into_f32(td, gd, bd, n_tok, c, 1e-5, ln)
+    assert np.array_equal(want.reshape(c, n_tok), ln.numpy().reshape(n_tok, c).T)
+    rt.synchronize()
+    gc.disable()
+    try:
+        rt.begin_capture()
+        step()
+        graph = rt.end_capture()
+    finally:
+        gc.enable()
+    # 4.5 M tokens x 4 channels: 9 M floats of statistics, more than the
+    # first allocation (8 Mi floats), so the buffer is replaced
+    nb, cb = 4_500_000, 4
+    big = normals(rng, nb, cb)
+    gb, bb = _params(rng, cb, False)
+    big_d, gbd, bbd = rt.upload_f32(big), rt.upload_f32(gb), rt.upload_f32(bb)
+    big_out = rt.alloc_f32(nb * cb)
+    rt.token_to_chw_f32(big_d, nb, cb, gbd, bbd, 1e-5, big_out)
+    big_ln = rt.alloc_f32(nb * cb)
+    rt.layernorm_into_f32(big_d, gbd, bbd, nb, cb, 1e-5, big_ln)
+    assert np.array_equal(big_out.numpy().reshape(cb, nb), big_ln.numpy().reshape(nb, cb).T)
+    for _ in range(3):
+        out.write(np.zeros(n_tok * c, np.float32))
+        graph.launch()
+        rt.synchronize()
+        assert np.array_equal(out.numpy(), want)

@@ -336,24 +336,45 @@ namespace vk {
 
 namespace {
 
-// Split count for a tile grid: at least one workgroup per CU when the rows
-// alone leave CUs idle (a single 866-token image), at least two k chunks per
-// split, at most 8 partial slices.
-#ifndef VK_SPLITK_WG_PER_CU
-#define VK_SPLITK_WG_PER_CU 1  // workgroups per CU the split aims at
-#endif
+// Split count for a tile grid, from a cost model fitted to split sweeps of
+// the ViT-B and ViT-L projections at 866 and 3,458 rows.  Workgroups are
+// dealt round-robin to the CUs, so the busiest CU runs ceil(tiles * s / CUs)
+// workgroups of up to ceil(chunks / s) K chunks each, about 5.5 us per
+// chunk; a split adds its partial sums (s x M x N floats written, then read
+// by the sum pass, at about 5.5 TB/s) and the sum pass's launch (about 2 us).
+// The cheapest count wins, the smallest on ties; at least two chunks per
+// split, at most VK_SPLITK_MAX slices and VK_SPLITK_MAX_FLOATS floats of
+// partial sums.  One 866-token ViT-B image: QKV 2, projection 6, FC1 3,
+// FC2 6; 10,392 rows: 1 for all four.
 #ifndef VK_SPLITK_MAX
-#define VK_SPLITK_MAX 8        // most partial slices
+#define VK_SPLITK_MAX 8  // most partial slices
+#endif
+#ifndef VK_SPLITK_MAX_FLOATS
+#define VK_SPLITK_MAX_FLOATS (1LL << 26)  // 256 MB of partial sums
 #endif
 
-int choose_splits(const vk_runtime* rt, long long tiles, int K) {
-  const int cus = (rt->cu_count > 0 ? rt->cu_count : 256) * VK_SPLITK_WG_PER_CU;
-  if (tiles >= cus) return 1;
+int choose_splits(const vk_runtime* rt, long long tiles, int M, int N, int K) {
+  constexpr double kChunkUs = 5.5, kBytesPerUs = 5.5e6, kSumLaunchUs = 2.0;
+  const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
   const int nch = (K + KC - 1) / KC;
-  int s = static_cast<int>((static_cast<double>(cus) / static_cast<double>(tiles)) + 0.5);
-  if (s > nch / 2) s = nch / 2;
-  if (s > VK_SPLITK_MAX) s = VK_SPLITK_MAX;
-  return s < 1 ? 1 : s;
+  const long long mn = static_cast<long long>(M) * N;
+  auto cost = [&](int sp) {
+    const long long load = (tiles * sp + cus - 1) / cus * ((nch + sp - 1) / sp);
+    double us = kChunkUs * static_cast<double>(load);
+    if (sp > 1) us += 8.0 * static_cast<double>(sp * mn) / kBytesPerUs + kSumLaunchUs;
+    return us;
+  };
+  int best = 1;
+  double best_us = cost(1);
+  for (int sp = 2; sp <= VK_SPLITK_MAX && 2 * sp <= nch && sp * mn <= VK_SPLITK_MAX_FLOATS;
+       ++sp) {
+    const double us = cost(sp);
+    if (us < best_us) {
+      best = sp;
+      best_us = us;
+    }
+  }
+  return best;
 }
 
 template <int EPI, int LAY, int QKN = 0>
@@ -373,7 +394,7 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   const long long tiles =
       static_cast<long long>((g0.M + TM - 1) / TM) * static_cast<long long>((g0.N + TN - 1) / TN);
   LinearArgs g = g0;
-  g.splits = choose_splits(rt, tiles, g.K);
+  g.splits = choose_splits(rt, tiles, g.M, g.N, g.K);
   g.partial = nullptr;
   VK_UNSUPPORTED_IF(tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", tiles);
   if (g.splits > 1) {
