@@ -325,6 +325,24 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// Raw buffer loads: a buffer resource (base address and byte size, held in
+// scalar registers) plus a 32-bit per-lane byte offset and a uniform byte
+// offset, with no 64-bit address arithmetic per load.  Reads at or past
+// `bytes` return zeros.  Third descriptor word: the gfx9-family raw-buffer
+// format (32-bit data, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ float4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t lane_off,
+                                               uint32_t uniform_off) {
+  typedef int i32x4_t __attribute__((ext_vector_type(4)));
+  const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+      r, static_cast<int>(lane_off), static_cast<int>(uniform_off), 0);
+  return __builtin_bit_cast(float4, v);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on
 // XCD i % 8), and each XCD has its own L2.  Renumber so that an XCD's
 // workgroups are consecutive tiles t of an N-major order (t -> m = t % gm,

@@ -143,45 +143,26 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
   const float* arow = As + (wm * 32 + (lane & 15)) * PITCH + kq;
   const float* brow = Bs + (wn * 64 + (lane & 15)) * PITCH + kq;
 
-  for (int k0 = c_begin * KC; k0 < c_end * KC; k0 += KC) {
-    // stage the chunk: slot f = tid + 512 i is row f/16, float4 f%16 of the
-    // chunk (a wave reads four 256-byte row segments).  Loads are never
-    // guarded: out-of-range slots read a clamped address and store zeros.
-    float4 ra[kVec], rb[kVec];
-    bool oka[kVec], okb[kVec];
+  // Staging slot i of a thread: row r_i = tid/16 + 32 i of the A and B
+  // tiles, float4 column c = 4 (tid % 16) of the chunk (a wave reads four
+  // 256-byte row segments).  Rows past M or N read a clamped, valid row:
+  // row i of A only reaches output row i and row j of B output column j, so
+  // their values never reach a stored output.
+  const int c_ld = 4 * (tid & 15);
+  uint32_t a_off[kVec], b_off[kVec];  // byte offsets, the same for every chunk
+  int s_off[kVec];                    // LDS float offsets
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      const int f = tid + kThreads * i;
-      const int r = f >> 4, c = 4 * (f & 15);
-      const int gm = m0 + r, gn = n0 + r, gk = k0 + c;
-      oka[i] = gm < g.M && gk < g.K;
-      okb[i] = gn < g.N && gk < g.Kp;
-      const int cm = gm < g.M ? gm : g.M - 1;
-      const int cn = gn < g.N ? gn : g.N - 1;
-      const int ck = gk < g.K ? gk : g.K - 4;
-      const size_t ia = LAY == kAHnd
-                            ? (static_cast<size_t>(ck >> 6) * g.M + cm) * 64 + (ck & 63)
-                            : static_cast<size_t>(cm) * g.K + ck;
-      ra[i] = *reinterpret_cast<const float4*>(g.x + ia);
-      rb[i] = *reinterpret_cast<const float4*>(g.wnk + static_cast<size_t>(cn) * g.Kp +
-                                                (gk < g.Kp ? gk : g.Kp - 4));
-    }
-    __syncthreads();  // every wave is done reading the previous chunk
-#pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      const int f = tid + kThreads * i;
-      const int r = f >> 4, c = 4 * (f & 15);
-      // component selects: a select of whole float4 values becomes a select
-      // of their addresses, which puts the staging arrays in scratch memory
-      const bool a_on = oka[i], b_on = okb[i];
-      *reinterpret_cast<float4*>(As + r * PITCH + c) =
-          make_float4(a_on ? ra[i].x : 0.f, a_on ? ra[i].y : 0.f, a_on ? ra[i].z : 0.f,
-                      a_on ? ra[i].w : 0.f);
-      *reinterpret_cast<float4*>(Bs + r * PITCH + c) =
-          make_float4(b_on ? rb[i].x : 0.f, b_on ? rb[i].y : 0.f, b_on ? rb[i].z : 0.f,
-                      b_on ? rb[i].w : 0.f);
-    }
-    __syncthreads();
+  for (int i = 0; i < kVec; ++i) {
+    const int r = (tid >> 4) + (kThreads / 16) * i;
+    const int gm = m0 + r, gn = n0 + r;
+    const uint32_t cm = static_cast<uint32_t>(gm < g.M ? gm : g.M - 1);
+    const uint32_t cn = static_cast<uint32_t>(gn < g.N ? gn : g.N - 1);
+    a_off[i] = 4u * (LAY == kAHnd ? cm * 64u + c_ld : cm * static_cast<uint32_t>(g.K) + c_ld);
+    b_off[i] = 4u * (cn * static_cast<uint32_t>(g.Kp) + c_ld);
+    s_off[i] = r * PITCH + c_ld;
+  }
+
+  auto mma_chunk = [&]() {
 #pragma unroll
     for (int b = 0; b < KC / 16; ++b) {
       f32x4 a[2], w[4];
@@ -199,6 +180,72 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
           for (int u = 0; u < 4; ++u)
             acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][j], w[u][j], acc[t][u], 0, 0, 0);
     }
+  };
+
+  // Whole chunks (k0 + 64 <= K): buffer loads of the lane's fixed offset
+  // plus the chunk's uniform offset, with no per-chunk address arithmetic or
+  // selects.
+  const int full = g.K / KC;
+  const int c_full = c_end < full ? c_end : full;
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      vkd::buffer_rsrc(g.x, 4u * static_cast<uint32_t>(g.M) * static_cast<uint32_t>(g.K));
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      vkd::buffer_rsrc(g.wnk, 4u * static_cast<uint32_t>(g.N) * static_cast<uint32_t>(g.Kp));
+  for (int ch = c_begin; ch < c_full; ++ch) {
+    const uint32_t k0 = static_cast<uint32_t>(ch) * KC;
+    const uint32_t a_chunk =
+        4u * (LAY == kAHnd ? static_cast<uint32_t>(ch) * static_cast<uint32_t>(g.M) * 64u : k0);
+    float4 ra[kVec], rb[kVec];
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      ra[i] = vkd::buffer_load4(a_rsrc, a_off[i], a_chunk);
+      rb[i] = vkd::buffer_load4(b_rsrc, b_off[i], 4u * k0);
+    }
+    __syncthreads();  // every wave is done reading the previous chunk
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      *reinterpret_cast<float4*>(As + s_off[i]) = ra[i];
+      *reinterpret_cast<float4*>(Bs + s_off[i]) = rb[i];
+    }
+    __syncthreads();
+    mma_chunk();
+  }
+
+  // The last, partial chunk (K % 64 != 0): k past K reads a clamped address
+  // and stores zeros (A past K, B past its zero padding Kp).
+  if (c_end > full && c_begin <= full) {
+    const int k0 = full * KC;
+    const int gk = k0 + c_ld;
+    const bool ka = gk < g.K, kb = gk < g.Kp;
+    const int ck = ka ? gk : g.K - 4;
+    const int ckb = kb ? gk : g.Kp - 4;
+    float4 ra[kVec], rb[kVec];
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      const int r = (tid >> 4) + (kThreads / 16) * i;
+      const int gm = m0 + r, gn = n0 + r;
+      const int cm = gm < g.M ? gm : g.M - 1;
+      const int cn = gn < g.N ? gn : g.N - 1;
+      const size_t ia = LAY == kAHnd
+                            ? (static_cast<size_t>(ck >> 6) * g.M + cm) * 64 + (ck & 63)
+                            : static_cast<size_t>(cm) * g.K + ck;
+      ra[i] = *reinterpret_cast<const float4*>(g.x + ia);
+      rb[i] = *reinterpret_cast<const float4*>(g.wnk + static_cast<size_t>(cn) * g.Kp + ckb);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      // component selects: a select of whole float4 values becomes a select
+      // of their addresses, which puts the staging arrays in scratch memory
+      *reinterpret_cast<float4*>(As + s_off[i]) =
+          make_float4(ka ? ra[i].x : 0.f, ka ? ra[i].y : 0.f, ka ? ra[i].z : 0.f,
+                      ka ? ra[i].w : 0.f);
+      *reinterpret_cast<float4*>(Bs + s_off[i]) =
+          make_float4(kb ? rb[i].x : 0.f, kb ? rb[i].y : 0.f, kb ? rb[i].z : 0.f,
+                      kb ? rb[i].w : 0.f);
+    }
+    __syncthreads();
+    mma_chunk();
   }
 
   // split-K: raw sums to this split's slice of the partial buffer
@@ -397,6 +444,9 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   g.splits = choose_splits(rt, tiles, g.M, g.N, g.K);
   g.partial = nullptr;
   VK_UNSUPPORTED_IF(tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", tiles);
+  // the staging loads address A and B rows with 32-bit byte offsets
+  VK_UNSUPPORTED_IF(4LL * g.M * g.K >= (1LL << 32) || 4LL * g.N * g.Kp >= (1LL << 32),
+                    "linear: operands of 4 GiB or more (M=%d, N=%d, K=%d)", g.M, g.N, g.K);
   if (g.splits > 1) {
     VK_REQUIRE(g.N % 4 == 0, "linear: split-K needs out_features % 4 == 0");
     VK_TRY(vk::ensure_work(rt, static_cast<size_t>(g.splits) * g.M * g.N, "linear (split-K)"));
