@@ -115,6 +115,21 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
   const int skey = htid >> 4, sd = 4 * (htid & 15);
   const float* karow = Ks + c16 * PITCH + 4 * g;
   const float* vtrow = Vt + c16 * PITCH + 4 * g;
+  // Whole key blocks load through buffer resources: the lane's byte offset
+  // inside a block is fixed, the block's offset is uniform, so the loads
+  // carry no per-block vector address arithmetic.  (The kernel's tensors
+  // are under 4 GiB, checked at launch.)
+  const uint32_t bytes = 4u * static_cast<uint32_t>(sequences) * static_cast<uint32_t>(n) * HD;
+  const __amdgpu_buffer_rsrc_t k_rsrc = vkd::buffer_rsrc(k, bytes);
+  const __amdgpu_buffer_rsrc_t v_rsrc = vkd::buffer_rsrc(v, bytes);
+  uint32_t k_off[kPer], v_off[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    k_off[i] = 4u * static_cast<uint32_t>((skey + (kHalf / 16) * i) * HD + sd);
+    const int w2 = wq + QG * i;
+    v_off[i] = 4u * static_cast<uint32_t>((16 * (w2 & 3) + (lane & 15)) * HD +
+                                          4 * ((lane >> 4) + 4 * (w2 >> 2)));
+  }
 
   const int nkb = (n + KB - 1) / KB;
   const int iters = (nkb + KS - 1) / KS;
@@ -123,7 +138,17 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
     // uniform per split: with two splits the odd half may run out of blocks
     const bool active = KS == 1 || k0 < n;
     f32x4 kr[kPer], vr[kPer];
-    if (active) {
+    if (active && k0 + KB <= n) {
+      const uint32_t blk = 4u * (static_cast<uint32_t>(seq) * static_cast<uint32_t>(n) +
+                                 static_cast<uint32_t>(k0)) * HD;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const float4 a = vkd::buffer_load4(k_rsrc, k_off[i], blk);
+        const float4 b = vkd::buffer_load4(v_rsrc, v_off[i], blk);
+        kr[i] = f32x4{a.x, a.y, a.z, a.w};
+        vr[i] = f32x4{b.x, b.y, b.z, b.w};
+      }
+    } else if (active) {  // the last, partial block: keys past n read key n - 1
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
         const int key = k0 + skey + (kHalf / 16) * i;
@@ -190,12 +215,15 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
     m_run = m_new;
 
     // rescale O: row 4g + r belongs to query q0 + 4g + r, whose factor sits
-    // in lane 4g + r
+    // in lane 4g + r.  Skipped when every factor of the wave is exactly 1 (no
+    // row maximum grew): multiplying by 1 changes no bits.
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * g + r, 64);
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * g + r, 64);
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt][r] *= ar;
+        for (int dt = 0; dt < 4; ++dt) o[dt][r] *= ar;
+      }
     }
     // O += P V: A = the lane's probabilities of key tile t, B = V^T rows
 #pragma unroll
@@ -271,6 +299,7 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
   VK_UNSUPPORTED_IF(head_dim != HD, "attention: head_dim=%zu (qualified: 64)", head_dim);
   VK_UNSUPPORTED_IF(n > 0x7fffffffULL || sequences > 0x7fffffffULL, "attention: too large");
   const size_t len = sequences * n * HD;
+  VK_UNSUPPORTED_IF(len >= (size_t{1} << 30), "attention: tensors of 4 GiB or more");
   VK_TRY(check_qkv(q, len, "q"));
   VK_TRY(check_qkv(k, len, "k"));
   VK_TRY(check_qkv(v, len, "v"));
