@@ -44,14 +44,13 @@ using namespace vk::linear_epilogue;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int TM = 128;
-constexpr int TN = 128;
+constexpr int TN = 128;  // tile width; the tile height TM is 128 or 64 (template)
 constexpr int KC = 64;
 constexpr int PITCH = 68;
-constexpr int kThreads = 512;
-constexpr int kVec = TM * KC / 4 / kThreads;  // float4 of A (and of B) per thread a chunk: 4
-static_assert(TM == TN && TM * KC / 4 % kThreads == 0, "staging slots divide evenly");
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1 && PITCH >= KC, "pitch 4 x odd");
+
+// Threads of a TM x 128 tile: one wave per 32 x 64 strip.
+constexpr int threads_for(int tm) { return 4 * tm; }
 
 enum Layout { kPlain = 0, kQkvHnd = 1, kAHnd = 2 };
 
@@ -114,8 +113,14 @@ __device__ __forceinline__ float4 qk_head_row(const LinearArgs& g, float4 v, int
       v, l, gm, bt, py, px, g.qkn.table, g.qkn.table_max, g.qkn.eps);
 }
 
-template <int EPI, int LAY, int QKN = 0>
-__global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) {
+template <int EPI, int LAY, int QKN, int TM>
+__global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wide_kernel(
+    LinearArgs g) {
+  constexpr int kThreads = threads_for(TM);
+  constexpr int kVA = TM * KC / 4 / kThreads;  // float4 of A per thread a chunk: 4
+  constexpr int kVB = TN * KC / 4 / kThreads;  // float4 of B: 4 (TM 128) or 8 (TM 64)
+  static_assert(TM == 128 || TM == 64, "tile heights 128 and 64");
+  static_assert(kVA * kThreads * 4 == TM * KC && kVB * kThreads * 4 == TN * KC, "slots");
   __shared__ __align__(16) float As[TM * PITCH];
   __shared__ __align__(16) float Bs[TN * PITCH];
 
@@ -143,23 +148,25 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
   const float* arow = As + (wm * 32 + (lane & 15)) * PITCH + kq;
   const float* brow = Bs + (wn * 64 + (lane & 15)) * PITCH + kq;
 
-  // Staging slot i of a thread: row r_i = tid/16 + 32 i of the A and B
-  // tiles, float4 column c = 4 (tid % 16) of the chunk (a wave reads four
-  // 256-byte row segments).  Rows past M or N read a clamped, valid row:
-  // row i of A only reaches output row i and row j of B output column j, so
-  // their values never reach a stored output.
+  // Staging slot i of a thread: row r_i = tid/16 + (threads/16) i of the A
+  // (or B) tile, float4 column c = 4 (tid % 16) of the chunk (a wave reads
+  // four 256-byte row segments).  Rows past M or N read a clamped, valid
+  // row: row i of A only reaches output row i and row j of B output column
+  // j, so their values never reach a stored output.
   const int c_ld = 4 * (tid & 15);
-  uint32_t a_off[kVec], b_off[kVec];  // byte offsets, the same for every chunk
-  int s_off[kVec];                    // LDS float offsets
+  uint32_t a_off[kVA], b_off[kVB];  // byte offsets, the same for every chunk
+  auto slot_row = [&](int i) { return (tid >> 4) + (kThreads / 16) * i; };
 #pragma unroll
-  for (int i = 0; i < kVec; ++i) {
-    const int r = (tid >> 4) + (kThreads / 16) * i;
-    const int gm = m0 + r, gn = n0 + r;
+  for (int i = 0; i < kVA; ++i) {
+    const int gm = m0 + slot_row(i);
     const uint32_t cm = static_cast<uint32_t>(gm < g.M ? gm : g.M - 1);
-    const uint32_t cn = static_cast<uint32_t>(gn < g.N ? gn : g.N - 1);
     a_off[i] = 4u * (LAY == kAHnd ? cm * 64u + c_ld : cm * static_cast<uint32_t>(g.K) + c_ld);
+  }
+#pragma unroll
+  for (int i = 0; i < kVB; ++i) {
+    const int gn = n0 + slot_row(i);
+    const uint32_t cn = static_cast<uint32_t>(gn < g.N ? gn : g.N - 1);
     b_off[i] = 4u * (cn * static_cast<uint32_t>(g.Kp) + c_ld);
-    s_off[i] = r * PITCH + c_ld;
   }
 
   auto mma_chunk = [&]() {
@@ -195,18 +202,18 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
     const uint32_t k0 = static_cast<uint32_t>(ch) * KC;
     const uint32_t a_chunk =
         4u * (LAY == kAHnd ? static_cast<uint32_t>(ch) * static_cast<uint32_t>(g.M) * 64u : k0);
-    float4 ra[kVec], rb[kVec];
+    float4 ra[kVA], rb[kVB];
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      ra[i] = vkd::buffer_load4(a_rsrc, a_off[i], a_chunk);
-      rb[i] = vkd::buffer_load4(b_rsrc, b_off[i], 4u * k0);
-    }
+    for (int i = 0; i < kVA; ++i) ra[i] = vkd::buffer_load4(a_rsrc, a_off[i], a_chunk);
+#pragma unroll
+    for (int i = 0; i < kVB; ++i) rb[i] = vkd::buffer_load4(b_rsrc, b_off[i], 4u * k0);
     __syncthreads();  // every wave is done reading the previous chunk
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      *reinterpret_cast<float4*>(As + s_off[i]) = ra[i];
-      *reinterpret_cast<float4*>(Bs + s_off[i]) = rb[i];
-    }
+    for (int i = 0; i < kVA; ++i)
+      *reinterpret_cast<float4*>(As + slot_row(i) * PITCH + c_ld) = ra[i];
+#pragma unroll
+    for (int i = 0; i < kVB; ++i)
+      *reinterpret_cast<float4*>(Bs + slot_row(i) * PITCH + c_ld) = rb[i];
     __syncthreads();
     mma_chunk();
   }
@@ -219,31 +226,35 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
     const bool ka = gk < g.K, kb = gk < g.Kp;
     const int ck = ka ? gk : g.K - 4;
     const int ckb = kb ? gk : g.Kp - 4;
-    float4 ra[kVec], rb[kVec];
+    float4 ra[kVA], rb[kVB];
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      const int r = (tid >> 4) + (kThreads / 16) * i;
-      const int gm = m0 + r, gn = n0 + r;
+    for (int i = 0; i < kVA; ++i) {
+      const int gm = m0 + slot_row(i);
       const int cm = gm < g.M ? gm : g.M - 1;
-      const int cn = gn < g.N ? gn : g.N - 1;
       const size_t ia = LAY == kAHnd
                             ? (static_cast<size_t>(ck >> 6) * g.M + cm) * 64 + (ck & 63)
                             : static_cast<size_t>(cm) * g.K + ck;
       ra[i] = *reinterpret_cast<const float4*>(g.x + ia);
+    }
+#pragma unroll
+    for (int i = 0; i < kVB; ++i) {
+      const int gn = n0 + slot_row(i);
+      const int cn = gn < g.N ? gn : g.N - 1;
       rb[i] = *reinterpret_cast<const float4*>(g.wnk + static_cast<size_t>(cn) * g.Kp + ckb);
     }
     __syncthreads();
+    // component selects: a select of whole float4 values becomes a select
+    // of their addresses, which puts the staging arrays in scratch memory
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      // component selects: a select of whole float4 values becomes a select
-      // of their addresses, which puts the staging arrays in scratch memory
-      *reinterpret_cast<float4*>(As + s_off[i]) =
+    for (int i = 0; i < kVA; ++i)
+      *reinterpret_cast<float4*>(As + slot_row(i) * PITCH + c_ld) =
           make_float4(ka ? ra[i].x : 0.f, ka ? ra[i].y : 0.f, ka ? ra[i].z : 0.f,
                       ka ? ra[i].w : 0.f);
-      *reinterpret_cast<float4*>(Bs + s_off[i]) =
+#pragma unroll
+    for (int i = 0; i < kVB; ++i)
+      *reinterpret_cast<float4*>(Bs + slot_row(i) * PITCH + c_ld) =
           make_float4(kb ? rb[i].x : 0.f, kb ? rb[i].y : 0.f, kb ? rb[i].z : 0.f,
                       kb ? rb[i].w : 0.f);
-    }
     __syncthreads();
     mma_chunk();
   }
@@ -274,7 +285,9 @@ __global__ __launch_bounds__(kThreads, 2) void linear_wide_kernel(LinearArgs g) 
     const int embed = g.N / 3;
     const int which = col0 < g.N ? col0 / embed : 2;
     const int g4 = lane >> 4, c16 = lane & 15;
-    float* xs = (wave < 4 ? As : Bs) + (wave & 3) * 32 * PITCH;
+    // a 32-row staging region per wave: the A tile holds TM / 32 of them,
+    // the B tile the rest
+    float* xs = wave < TM / 32 ? As + wave * 32 * PITCH : Bs + (wave - TM / 32) * 32 * PITCH;
     __syncthreads();  // every wave is done with the last chunk's operands
     if (which < 2) {
 #pragma unroll
@@ -383,50 +396,73 @@ namespace vk {
 
 namespace {
 
-// Split count for a tile grid, from a cost model fitted to split sweeps of
+// Tile height and split count, from a cost model fitted to split sweeps of
 // the ViT-B and ViT-L projections at 866 and 3,458 rows.  Workgroups are
 // dealt round-robin to the CUs, so the busiest CU runs ceil(tiles * s / CUs)
 // workgroups of up to ceil(chunks / s) K chunks each, about 5.5 us per
-// chunk; a split adds its partial sums (s x M x N floats written, then read
-// by the sum pass, at about 5.5 TB/s) and the sum pass's launch (about 2 us).
-// The cheapest count wins, the smallest on ties; at least two chunks per
-// split, at most VK_SPLITK_MAX slices and VK_SPLITK_MAX_FLOATS floats of
-// partial sums.  One 866-token ViT-B image: QKV 2, projection 6, FC1 3,
-// FC2 6; 10,392 rows: 1 for all four.
+// chunk of a 128-row tile and 0.6 of that for a 64-row tile (half the
+// MFMAs, more operand traffic per MFMA: 3.0-3.5 against 4.8-6.2 us
+// measured at one to two workgroups per CU); a split adds its
+// partial sums (s x M x N floats written, then read by the sum pass, at
+// about 5.5 TB/s) and the sum pass's launch (about 2 us).  The cheapest plan
+// wins; on ties the 128-row tile, then the smaller count.  At least two
+// chunks per split, at most VK_SPLITK_MAX slices and VK_SPLITK_MAX_FLOATS
+// floats of partial sums.  One 866-token ViT-B image: QKV 64 rows unsplit,
+// projection 64 rows x 3, FC1 128 x 3, FC2 128 x 6; 3,458 and 10,392 rows
+// keep 128-row tiles.
 #ifndef VK_SPLITK_MAX
 #define VK_SPLITK_MAX 8  // most partial slices
 #endif
 #ifndef VK_SPLITK_MAX_FLOATS
 #define VK_SPLITK_MAX_FLOATS (1LL << 26)  // 256 MB of partial sums
 #endif
+#ifndef VK_LINEAR_TILES
+#define VK_LINEAR_TILES 3  // bit 0: 128-row tiles allowed, bit 1: 64-row tiles allowed
+#endif
 
-int choose_splits(const vk_runtime* rt, long long tiles, int M, int N, int K) {
+struct Plan {
+  int tm;
+  int splits;
+  long long tiles;
+};
+
+long long tile_count(int tm, int M, int N) {
+  return static_cast<long long>((M + tm - 1) / tm) * static_cast<long long>((N + TN - 1) / TN);
+}
+
+Plan choose_plan(const vk_runtime* rt, int M, int N, int K) {
   constexpr double kChunkUs = 5.5, kBytesPerUs = 5.5e6, kSumLaunchUs = 2.0;
   const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
   const int nch = (K + KC - 1) / KC;
   const long long mn = static_cast<long long>(M) * N;
-  auto cost = [&](int sp) {
-    const long long load = (tiles * sp + cus - 1) / cus * ((nch + sp - 1) / sp);
-    double us = kChunkUs * static_cast<double>(load);
-    if (sp > 1) us += 8.0 * static_cast<double>(sp * mn) / kBytesPerUs + kSumLaunchUs;
-    return us;
-  };
-  int best = 1;
-  double best_us = cost(1);
-  for (int sp = 2; sp <= VK_SPLITK_MAX && 2 * sp <= nch && sp * mn <= VK_SPLITK_MAX_FLOATS;
-       ++sp) {
-    const double us = cost(sp);
-    if (us < best_us) {
-      best = sp;
-      best_us = us;
+  Plan best{0, 1, 0};
+  double best_us = 0.0;
+  for (int tm : {128, 64}) {
+    if (!(VK_LINEAR_TILES & (tm == 128 ? 1 : 2))) continue;
+    const long long tiles = tile_count(tm, M, N);
+    for (int sp = 1; sp == 1 || (sp <= VK_SPLITK_MAX && 2 * sp <= nch &&
+                                 sp * mn <= VK_SPLITK_MAX_FLOATS);
+         ++sp) {
+      const long long load = (tiles * sp + cus - 1) / cus * ((nch + sp - 1) / sp);
+      double us = kChunkUs * (tm == 128 ? 1.0 : 0.6) * static_cast<double>(load);
+      if (sp > 1) us += 8.0 * static_cast<double>(sp * mn) / kBytesPerUs + kSumLaunchUs;
+      if (best.tm == 0 || us < best_us) {
+        best = Plan{tm, sp, tiles};
+        best_us = us;
+      }
     }
   }
   return best;
 }
 
 template <int EPI, int LAY, int QKN = 0>
-void launch_pair(vk_runtime* rt, const LinearArgs& g, dim3 grid) {
-  hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN>), grid, dim3(kThreads), 0, rt->stream, g);
+void launch_pair(vk_runtime* rt, const LinearArgs& g, int tm, dim3 grid) {
+  if (tm == 128)
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 128>), grid, dim3(threads_for(128)), 0,
+                       rt->stream, g);
+  else
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64>), grid, dim3(threads_for(64)), 0,
+                       rt->stream, g);
   if (g.splits > 1) {
     const long long n4 = static_cast<long long>(g.M) * g.N / 4;
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN>),
@@ -438,12 +474,12 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, dim3 grid) {
 }  // namespace
 
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
-  const long long tiles =
-      static_cast<long long>((g0.M + TM - 1) / TM) * static_cast<long long>((g0.N + TN - 1) / TN);
   LinearArgs g = g0;
-  g.splits = choose_splits(rt, tiles, g.M, g.N, g.K);
+  const Plan plan = choose_plan(rt, g.M, g.N, g.K);
+  const int tm = plan.tm;
+  g.splits = plan.splits;
   g.partial = nullptr;
-  VK_UNSUPPORTED_IF(tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", tiles);
+  VK_UNSUPPORTED_IF(plan.tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", plan.tiles);
   // the staging loads address A and B rows with 32-bit byte offsets
   VK_UNSUPPORTED_IF(4LL * g.M * g.K >= (1LL << 32) || 4LL * g.N * g.Kp >= (1LL << 32),
                     "linear: operands of 4 GiB or more (M=%d, N=%d, K=%d)", g.M, g.N, g.K);
@@ -452,29 +488,29 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
     VK_TRY(vk::ensure_work(rt, static_cast<size_t>(g.splits) * g.M * g.N, "linear (split-K)"));
     g.partial = rt->work;
   }
-  const dim3 grid(static_cast<unsigned>(tiles * g.splits));
+  const dim3 grid(static_cast<unsigned>(plan.tiles * g.splits));
   if (g.q_out) {
     VK_REQUIRE(epi == kLinStore, "linear: the Q|K|V split takes the store epilogue");
     switch (g.qkn_mode) {
-      case 0: launch_pair<kLinStore, kQkvHnd>(rt, g, grid); break;
-      case 1: launch_pair<kLinStore, kQkvHnd, 1>(rt, g, grid); break;
-      case 2: launch_pair<kLinStore, kQkvHnd, 2>(rt, g, grid); break;
-      case 3: launch_pair<kLinStore, kQkvHnd, 3>(rt, g, grid); break;
+      case 0: launch_pair<kLinStore, kQkvHnd>(rt, g, tm, grid); break;
+      case 1: launch_pair<kLinStore, kQkvHnd, 1>(rt, g, tm, grid); break;
+      case 2: launch_pair<kLinStore, kQkvHnd, 2>(rt, g, tm, grid); break;
+      case 3: launch_pair<kLinStore, kQkvHnd, 3>(rt, g, tm, grid); break;
       default: return set_error(VK_ERR_INVALID, "linear: unknown Q/K epilogue %d", g.qkn_mode);
     }
   } else if (g.a_hnd) {
     if (epi == kLinResidual)
-      launch_pair<kLinResidual, kAHnd>(rt, g, grid);
+      launch_pair<kLinResidual, kAHnd>(rt, g, tm, grid);
     else if (epi == kLinStore)
-      launch_pair<kLinStore, kAHnd>(rt, g, grid);
+      launch_pair<kLinStore, kAHnd>(rt, g, tm, grid);
     else
       return set_error(VK_ERR_INVALID, "linear: head-major input takes store or residual");
   } else {
     switch (epi) {
-      case kLinStore: launch_pair<kLinStore, kPlain>(rt, g, grid); break;
-      case kLinGelu: launch_pair<kLinGelu, kPlain>(rt, g, grid); break;
-      case kLinGeluErf: launch_pair<kLinGeluErf, kPlain>(rt, g, grid); break;
-      default: launch_pair<kLinResidual, kPlain>(rt, g, grid); break;
+      case kLinStore: launch_pair<kLinStore, kPlain>(rt, g, tm, grid); break;
+      case kLinGelu: launch_pair<kLinGelu, kPlain>(rt, g, tm, grid); break;
+      case kLinGeluErf: launch_pair<kLinGeluErf, kPlain>(rt, g, tm, grid); break;
+      default: launch_pair<kLinResidual, kPlain>(rt, g, tm, grid); break;
     }
   }
   return check_launch("linear_wide_kernel");
