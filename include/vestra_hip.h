@@ -76,6 +76,11 @@ int vk_abi_version(void);
 
 /* CudaRuntime::new(device) (engine.rs:284-385 enable_cuda_*). */
 int vk_runtime_create(int device, vk_runtime** out);
+/* Waits for the runtime's queued work and retires the handle: it takes no
+ * new work (calls on it fail).  Tensors, linears and events created on it
+ * may still be destroyed afterwards; the stream and the runtime's own
+ * buffers are released with the last of them.  Graphs captured on it must
+ * not be launched afterwards. */
 int vk_runtime_destroy(vk_runtime* rt);
 /* Blocks until all work queued on the runtime's stream has finished. */
 int vk_runtime_synchronize(vk_runtime* rt);

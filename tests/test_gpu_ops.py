@@ -297,3 +297,29 @@ def test_rope_table_growth_keeps_captured_graphs_valid(rt, rng):
     graph.launch()
     rt.synchronize()
     assert np.array_equal(tq.numpy(), want)
+
+
+def test_runtime_destroy_before_its_objects(rng):
+    """Objects may outlive their runtime's handle: after vk_runtime_destroy
+    the handle takes no new work, and the tensors, linears and events made
+    on it are still destroyed cleanly (the runtime goes with the last)."""
+    import ctypes
+    import gc
+    rt = vh.Runtime(0)
+    h = rt.handle
+    x = rng.standard_normal(4096).astype(np.float32)
+    t = rt.upload_f32(x)
+    assert np.array_equal(t.numpy(), x)
+    lin = rt.prepare_linear_f32(16, 8, rng.standard_normal((16, 8)).astype(np.float32),
+                                np.zeros(8, np.float32))
+    ev = rt.event()
+    ev.record()
+    rt.close()
+    out = ctypes.c_void_p()
+    with pytest.raises(vh.VestraError, match="destroyed"):
+        vh._check(vh.lib.vk_tensor_alloc(h, vh.VK_F32, 4, ctypes.byref(out)))
+    with pytest.raises(vh.VestraError, match="destroyed"):
+        vh._check(vh.lib.vk_runtime_synchronize(h))
+    t.free()
+    del lin, ev
+    gc.collect()  # the last object releases the runtime

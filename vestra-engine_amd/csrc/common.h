@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -18,6 +19,14 @@
 // ---------------------------------------------------------------------------
 
 struct vk_runtime {
+  // Handles that keep the runtime alive: the runtime handle itself plus
+  // every tensor, linear and event created on it.  vk_runtime_destroy drops
+  // the first; the stream and the runtime's buffers are released when the
+  // last one goes, so objects destroyed after their runtime stay valid to
+  // destroy.
+  std::atomic<int> refs{1};
+  // vk_runtime_destroy was called: the handle takes no new work.
+  bool destroyed = false;
   int device = 0;
   hipStream_t stream = nullptr;
   int cu_count = 0;
@@ -108,8 +117,15 @@ int set_error(int code, const char* fmt, ...);
 void clear_error();
 int hip_fail(hipError_t e, const char* what);
 size_t dtype_size(vk_dtype d);
-// Ensures the calling thread's current device is the runtime's device.
+// Ensures the calling thread's current device is the runtime's device;
+// fails for a destroyed runtime.
 int bind(vk_runtime* rt);
+// The same without the destroyed check: releasing objects of a destroyed
+// runtime.
+int bind_device(vk_runtime* rt);
+// Reference counting of the runtime by the objects created on it.
+void retain(vk_runtime* rt);
+void release(vk_runtime* rt);
 // Launch check: turns a failed launch into a status.
 int check_launch(const char* what);
 // Device cos/sin table for the 2D RoPE (layout below) covering at least

@@ -599,6 +599,7 @@ int make_linear(vk_runtime* rt, size_t in, size_t out, const std::vector<float>&
                 const float* bias, const float* ls, vk_linear** res) {
   auto* lin = new vk_linear;
   lin->rt = rt;
+  vk::retain(rt);
   lin->in_features = in;
   lin->out_features = out;
   lin->k_pitch = (in + kKAlign - 1) / kKAlign * kKAlign;
@@ -785,6 +786,7 @@ int make_linear_stored(vk_runtime* rt, size_t in, size_t out, int src_kind, bool
                        vk_linear** res) {
   auto* lin = new vk_linear;
   lin->rt = rt;
+  vk::retain(rt);
   lin->in_features = in;
   lin->out_features = out;
   lin->k_pitch = (in + kKAlign - 1) / kKAlign * kKAlign;
@@ -952,13 +954,15 @@ int vk_linear_prepare_oihw_f32(vk_runtime* rt, size_t in_features, size_t out_fe
 
 int vk_linear_destroy(vk_linear* lin) {
   if (!lin) return VK_OK;
-  if (lin->rt) (void)vk::bind(lin->rt);
-  if (lin->rt) (void)hipStreamSynchronize(lin->rt->stream);
+  vk_runtime* rt = lin->rt;
+  if (rt) (void)vk::bind_device(rt);
+  if (rt) (void)hipStreamSynchronize(rt->stream);
   if (lin->weight_nk) (void)hipFree(lin->weight_nk);
   if (lin->weight_patch) (void)hipFree(lin->weight_patch);
   if (lin->bias) (void)hipFree(lin->bias);
   if (lin->ls_gamma) (void)hipFree(lin->ls_gamma);
   delete lin;
+  vk::release(rt);
   return VK_OK;
 }
 

@@ -43,6 +43,12 @@ size_t dtype_size(vk_dtype d) {
 
 int bind(vk_runtime* rt) {
   VK_REQUIRE(rt != nullptr, "null runtime");
+  VK_REQUIRE(!rt->destroyed, "runtime was destroyed");
+  return bind_device(rt);
+}
+
+int bind_device(vk_runtime* rt) {
+  VK_REQUIRE(rt != nullptr, "null runtime");
   int cur = -1;
   VK_HIP(hipGetDevice(&cur));
   if (cur != rt->device) VK_HIP(hipSetDevice(rt->device));
@@ -117,6 +123,21 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const 
   return VK_OK;
 }
 
+void retain(vk_runtime* rt) {
+  if (rt) rt->refs.fetch_add(1, std::memory_order_relaxed);
+}
+
+void release(vk_runtime* rt) {
+  if (!rt || rt->refs.fetch_sub(1, std::memory_order_acq_rel) != 1) return;
+  (void)bind_device(rt);
+  (void)hipStreamSynchronize(rt->stream);
+  for (auto& kv : rt->rope_tables) (void)hipFree(kv.second.first);
+  if (rt->work) (void)hipFree(rt->work);
+  for (void* p : rt->retired) (void)hipFree(p);
+  (void)hipStreamDestroy(rt->stream);
+  delete rt;
+}
+
 int ensure_work(vk_runtime* rt, size_t floats, const char* who) {
   if (rt->work_len >= floats) return VK_OK;
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
@@ -144,6 +165,7 @@ static int new_tensor(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** ou
   if (len > 0) VK_HIP(hipMalloc(&p, len * dtype_size(dtype)));
   auto* t = new vk_tensor;
   t->rt = rt;
+  retain(rt);
   t->ptr = p;
   t->len = len;
   t->dtype = dtype;
@@ -205,13 +227,10 @@ int vk_runtime_create(int device, vk_runtime** out) {
 
 int vk_runtime_destroy(vk_runtime* rt) {
   if (!rt) return VK_OK;
-  VK_TRY(bind(rt));
+  VK_TRY(bind(rt));  // also refuses a second destroy of a runtime still alive
   (void)hipStreamSynchronize(rt->stream);
-  for (auto& kv : rt->rope_tables) (void)hipFree(kv.second.first);
-  if (rt->work) (void)hipFree(rt->work);
-  for (void* p : rt->retired) (void)hipFree(p);
-  (void)hipStreamDestroy(rt->stream);
-  delete rt;
+  rt->destroyed = true;
+  release(rt);
   return VK_OK;
 }
 
@@ -234,8 +253,10 @@ int vk_tensor_wrap(vk_runtime* rt, vk_dtype dtype, void* device_ptr, size_t len,
   VK_REQUIRE(rt != nullptr && out != nullptr, "null runtime or output handle");
   VK_REQUIRE(device_ptr != nullptr || len == 0, "null device pointer");
   VK_REQUIRE(dtype_size(dtype) != 0, "unknown dtype %d", static_cast<int>(dtype));
+  VK_REQUIRE(!rt->destroyed, "runtime was destroyed");
   auto* t = new vk_tensor;
   t->rt = rt;
+  retain(rt);
   t->ptr = device_ptr;
   t->len = len;
   t->dtype = dtype;
@@ -246,13 +267,17 @@ int vk_tensor_wrap(vk_runtime* rt, vk_dtype dtype, void* device_ptr, size_t len,
 
 int vk_tensor_destroy(vk_tensor* t) {
   if (!t) return VK_OK;
+  vk_runtime* rt = t->rt;
+  hipError_t e = hipSuccess;
   if (t->owned && t->ptr) {
-    VK_TRY(bind(t->rt));
+    VK_TRY(bind_device(rt));
     // Stream-ordered: pending kernels that read the buffer finish first.
-    (void)hipStreamSynchronize(t->rt->stream);
-    VK_HIP(hipFree(t->ptr));
+    (void)hipStreamSynchronize(rt->stream);
+    e = hipFree(t->ptr);
   }
   delete t;
+  release(rt);
+  if (e != hipSuccess) return hip_fail(e, "hipFree");
   return VK_OK;
 }
 
@@ -374,14 +399,17 @@ int vk_event_create(vk_runtime* rt, vk_event** out) {
     delete e;
     return hip_fail(err, "hipEventCreate");
   }
+  retain(rt);
   *out = e;
   return VK_OK;
 }
 
 int vk_event_destroy(vk_event* ev) {
   if (!ev) return VK_OK;
-  (void)hipEventDestroy(ev->ev);
+  vk_runtime* rt = ev->rt;
+  if (bind_device(rt) == VK_OK) (void)hipEventDestroy(ev->ev);
   delete ev;
+  release(rt);
   return VK_OK;
 }
 
