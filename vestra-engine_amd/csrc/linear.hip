@@ -54,27 +54,37 @@ constexpr int threads_for(int tm) { return 4 * tm; }
 
 enum Layout { kPlain = 0, kQkvHnd = 1, kAHnd = 2 };
 
-// One output element: v = acc + b (then * ls), each step rounded, through
-// the epilogue into the output layout.
-template <int EPI, int LAY>
-__device__ __forceinline__ void store_out(const LinearArgs& g, int row, int col, float acc,
-                                          float bias, float ls, float old) {
+// One output value: v = acc + b (then * ls), each step rounded, through the
+// epilogue.
+template <int EPI>
+__device__ __forceinline__ float epi_value(const LinearArgs& g, float acc, float bias, float ls,
+                                           float old) {
   float v = acc + bias;
   if (g.ls) v = v * ls;
-  float* o;
+  if (EPI == kLinGelu) return vkd::gelu1<0>(v);
+  if (EPI == kLinGeluErf) return vkd::gelu1<1>(v);
+  if (EPI == kLinResidual) return old + v;
+  return v;
+}
+
+// Address of output element (row, col) in the output layout.
+template <int LAY>
+__device__ __forceinline__ float* out_addr(const LinearArgs& g, int row, int col) {
   if constexpr (LAY == kQkvHnd) {
     const int embed = g.N / 3;
     const int which = col >= embed ? (col >= 2 * embed ? 2 : 1) : 0;
     const int c = col - which * embed;
     float* base = which == 0 ? g.q_out : (which == 1 ? g.k_out : g.v_out);
-    o = base + (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
+    return base + (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
   } else {
-    o = g.out + static_cast<size_t>(row) * g.N + col;
+    return g.out + static_cast<size_t>(row) * g.N + col;
   }
-  if (EPI == kLinStore) *o = v;
-  if (EPI == kLinGelu) *o = vkd::gelu1<0>(v);
-  if (EPI == kLinGeluErf) *o = vkd::gelu1<1>(v);
-  if (EPI == kLinResidual) *o = old + v;
+}
+
+template <int EPI, int LAY>
+__device__ __forceinline__ void store_out(const LinearArgs& g, int row, int col, float acc,
+                                          float bias, float ls, float old) {
+  *out_addr<LAY>(g, row, col) = epi_value<EPI>(g, acc, bias, ls, old);
 }
 
 // QKN: 0 none; 1 / 2 Q/K LayerNorm (f32 / f16 parameters) + RoPE; 3 RoPE.
@@ -315,40 +325,47 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
       return;
     }
   }
+  // Per 16-column strip u: bias, LayerScale and the address of the column
+  // at row 0 (row r adds r x the row stride), computed once; a tile inside
+  // the matrix stores without bounds checks.
+  const bool interior = m0 + TM <= g.M && n0 + TN <= g.N;
+  const size_t rs = LAY == kQkvHnd ? 64 : static_cast<size_t>(g.N);
+  float* cptr[4];
+  bool cok[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int col = n0 + wn * 64 + u * 16 + (lane & 15);
-    const int cc = col < g.N ? col : g.N - 1;
+    cok[u] = col < g.N;
+    const int cc = cok[u] ? col : g.N - 1;
     bias[u] = g.bias[cc];
     ls[u] = g.ls ? g.ls[cc] : 1.0f;
+    cptr[u] = out_addr<LAY>(g, 0, cc);
   }
   float old[2][4][4];
   if constexpr (EPI == kLinResidual) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
+        const size_t cr = static_cast<size_t>(row < g.M ? row : g.M - 1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
-          const int col = n0 + wn * 64 + u * 16 + (lane & 15);
-          const int cr = row < g.M ? row : g.M - 1;
-          const int cc = col < g.N ? col : g.N - 1;
-          old[t][u][r] = g.out[static_cast<size_t>(cr) * g.N + cc];
-        }
+        for (int u = 0; u < 4; ++u) old[t][u][r] = cptr[u][cr * rs];
+      }
   }
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
+      const bool rok = row < g.M;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
-        const int col = n0 + wn * 64 + u * 16 + (lane & 15);
-        if (row < g.M && col < g.N)
-          store_out<EPI, LAY>(g, row, col, acc[t][u][r], bias[u], ls[u],
-                              EPI == kLinResidual ? old[t][u][r] : 0.0f);
+      for (int u = 0; u < 4; ++u) {
+        const float val = epi_value<EPI>(g, acc[t][u][r], bias[u], ls[u],
+                                         EPI == kLinResidual ? old[t][u][r] : 0.0f);
+        if (interior || (rok && cok[u])) cptr[u][static_cast<size_t>(row) * rs] = val;
       }
+    }
 }
 
 // Second pass of a split-K linear: one thread per 4 consecutive outputs of a
