@@ -5,10 +5,12 @@
 //
 // A 256-thread workgroup (4 waves) owns 64 queries of one sequence; wave w
 // owns queries 16w..16w+15.  Grids of fewer than two such workgroups per CU
-// (a single image's local layer: 12 heads x 14 tiles) use workgroups of 32
-// queries whose two halves split the key blocks (attention_kernel<2, 2>).  Keys and values stream through LDS in blocks of
-// 64: K as [key][d] rows, V transposed as [d][key] rows, both with a pitch of
-// 68 floats (4 x odd: 16-row fragment reads are bank-conflict free).
+// (a single image's layer: 12 heads x 14 tiles) split each tile's key
+// blocks over several workgroups and merge the partial results in a second
+// pass (attention_kernel<true>, attention_merge_kernel).  Keys and values
+// stream through LDS in blocks of 64: K as [key][d] rows, V transposed as
+// [d][key] rows, both with a pitch of 68 floats (4 x odd: 16-row fragment
+// reads are bank-conflict free).
 //
 // Per key block a wave runs 128 v_mfma_f32_16x16x4_f32:
 //  * S^T = K Q^T (A = K, B = Q^T).  The transposed product leaves, in lane l,
@@ -57,37 +59,38 @@ __device__ __forceinline__ float group_sum(float v) {
   return v + __shfl_xor(v, 32, 64);
 }
 
-// QG query groups of 16 (one wave each) x KS key splits per workgroup.
-// <4, 1>: 64 queries, every key block, the normal form.  <2, 2>: 32 queries,
-// two halves of 2 waves that take alternate key blocks (each with its own
-// staging buffers) and merge their partial results through LDS at the end
-// -- the form for grids that would leave CUs idle (a single image's local
-// layer: 12 heads x 14 tiles), keeping 4 waves and all four SIMDs per
-// workgroup.
-template <int QG, int KS>
-__global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __restrict__ q,
-                                                                 const float* __restrict__ k,
-                                                                 const float* __restrict__ v,
-                                                                 float* __restrict__ out,
-                                                                 int sequences, int n) {
-  constexpr int kThreads = 64 * QG * KS;
-  constexpr int kHalf = 64 * QG;          // threads of one key split
+// Four query groups of 16 (one wave each) per workgroup: 64 queries over
+// every key block.  PART: grids of fewer than two workgroups per CU (a
+// single image's layer: 12 heads x 14 query tiles) split the key blocks of
+// each query tile into `splits` contiguous runs, one workgroup each; a run
+// writes its O (scaled to its own running max), the max and the sum to
+// `part` ([splits][rows][64], then [splits][rows][2]) and
+// attention_merge_kernel combines them in split order.
+template <bool PART>
+__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q,
+                                                        const float* __restrict__ k,
+                                                        const float* __restrict__ v,
+                                                        float* __restrict__ out, int sequences,
+                                                        int n, int splits,
+                                                        float* __restrict__ part) {
+  constexpr int QG = 4;                   // query groups (waves)
+  constexpr int kThreads = 64 * QG;
   constexpr int QB = 16 * QG;             // queries per workgroup
-  constexpr int kPer = kSlots / kHalf;    // staged float4 of K (and of V) per thread
-  static_assert(KS == 1 || KS == 2, "one or two key splits");
-  __shared__ __align__(16) float smem[KS * 2 * KB * PITCH];
+  constexpr int kPer = kSlots / kThreads; // staged float4 of K (and of V) per thread
+  __shared__ __align__(16) float smem[2 * KB * PITCH];
 
   const int tid = threadIdx.x;
   __builtin_assume(tid < kThreads);
   const int wave = tid >> 6, lane = tid & 63;
-  const int half = wave / QG, wq = wave % QG;  // key split, query group
-  const int htid = tid - half * kHalf;         // thread index inside the split
+  const int wq = wave;  // query group
   const int g = lane >> 4, c16 = lane & 15;
-  float* Ks = smem + half * 2 * KB * PITCH;
+  float* Ks = smem;
   float* Vt = Ks + KB * PITCH;
   const int nqb = (n + QB - 1) / QB;
   // XCD-major numbering: the query blocks of one sequence share an XCD's L2
-  const int tile = vkd::xcd_tile(blockIdx.x, gridDim.x);
+  const int tile_all = vkd::xcd_tile(blockIdx.x, gridDim.x);
+  const int split = PART ? tile_all % splits : 0;
+  const int tile = PART ? tile_all / splits : tile_all;
   const int seq = tile / nqb, q0 = (tile % nqb) * QB + wq * 16;
   const size_t base = static_cast<size_t>(seq) * n * HD;
 
@@ -108,11 +111,11 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;  // statistics of query q0 + c16
 
-  // K staging: slot f = htid + kHalf i is key f/16, float4 f%16 (16 lanes
-  // fill one key row).  V staging: slot f -> w' = f/64, key 16 (w' % 4) +
-  // (l & 15), float4 column (l >> 4) + 4 (w' / 4); one wave instruction covers
-  // 16 keys x 4 columns.
-  const int skey = htid >> 4, sd = 4 * (htid & 15);
+  // K staging: slot f = tid + 256 i is key f/16, float4 f%16 (16 lanes fill
+  // one key row).  V staging: slot f -> w' = f/64, key 16 (w' % 4) + (l & 15),
+  // float4 column (l >> 4) + 4 (w' / 4); one wave instruction covers 16 keys
+  // x 4 columns.
+  const int skey = tid >> 4, sd = 4 * (tid & 15);
   const float* karow = Ks + c16 * PITCH + 4 * g;
   const float* vtrow = Vt + c16 * PITCH + 4 * g;
   // Whole key blocks load through buffer resources: the lane's byte offset
@@ -125,20 +128,19 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
   uint32_t k_off[kPer], v_off[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    k_off[i] = 4u * static_cast<uint32_t>((skey + (kHalf / 16) * i) * HD + sd);
+    k_off[i] = 4u * static_cast<uint32_t>((skey + (kThreads / 16) * i) * HD + sd);
     const int w2 = wq + QG * i;
     v_off[i] = 4u * static_cast<uint32_t>((16 * (w2 & 3) + (lane & 15)) * HD +
                                           4 * ((lane >> 4) + 4 * (w2 >> 2)));
   }
 
   const int nkb = (n + KB - 1) / KB;
-  const int iters = (nkb + KS - 1) / KS;
-  for (int it = 0; it < iters; ++it) {
-    const int k0 = (it * KS + half) * KB;
-    // uniform per split: with two splits the odd half may run out of blocks
-    const bool active = KS == 1 || k0 < n;
+  const int kb_begin = PART ? split * nkb / splits : 0;
+  const int kb_end = PART ? (split + 1) * nkb / splits : nkb;
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int k0 = kb * KB;
     f32x4 kr[kPer], vr[kPer];
-    if (active && k0 + KB <= n) {
+    if (k0 + KB <= n) {
       const uint32_t blk = 4u * (static_cast<uint32_t>(seq) * static_cast<uint32_t>(n) +
                                  static_cast<uint32_t>(k0)) * HD;
 #pragma unroll
@@ -148,10 +150,10 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
         kr[i] = f32x4{a.x, a.y, a.z, a.w};
         vr[i] = f32x4{b.x, b.y, b.z, b.w};
       }
-    } else if (active) {  // the last, partial block: keys past n read key n - 1
+    } else {  // the last, partial block: keys past n read key n - 1
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
-        const int key = k0 + skey + (kHalf / 16) * i;
+        const int key = k0 + skey + (kThreads / 16) * i;
         const int ck = key < n ? key : n - 1;
         kr[i] = *reinterpret_cast<const f32x4*>(k + base + static_cast<size_t>(ck) * HD + sd);
         const int w2 = wq + QG * i;
@@ -162,19 +164,16 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
       }
     }
     __syncthreads();  // the previous block is consumed
-    if (active) {
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        *reinterpret_cast<f32x4*>(Ks + (skey + (kHalf / 16) * i) * PITCH + sd) = kr[i];
-        const int w2 = wq + QG * i;
-        const int key = 16 * (w2 & 3) + (lane & 15);
-        const int d = 4 * ((lane >> 4) + 4 * (w2 >> 2));
+    for (int i = 0; i < kPer; ++i) {
+      *reinterpret_cast<f32x4*>(Ks + (skey + (kThreads / 16) * i) * PITCH + sd) = kr[i];
+      const int w2 = wq + QG * i;
+      const int key = 16 * (w2 & 3) + (lane & 15);
+      const int d = 4 * ((lane >> 4) + 4 * (w2 >> 2));
 #pragma unroll
-        for (int c = 0; c < 4; ++c) Vt[(d + c) * PITCH + key] = vr[i][c];
-      }
+      for (int c = 0; c < 4; ++c) Vt[(d + c) * PITCH + key] = vr[i][c];
     }
     __syncthreads();
-    if (!active) continue;
 
     // S^T tiles: s[t][r] = score of query q0 + c16 with key k0 + 16t + 4g + r
     f32x4 s[4];
@@ -237,33 +236,24 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
       }
   }
 
-  if constexpr (KS == 2) {
-    // merge the odd-block half into the even-block half: the waves of one
-    // query group hold the same queries in the same lane layout
-    constexpr int kX = 18;  // o (16), m, l per lane
-    __syncthreads();        // the staging buffers are free
-    float* xr = smem + (wq * 64 + lane) * kX;
-    if (half == 1) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xr[dt * 4 + r] = o[dt][r];
-      xr[16] = m_run;
-      xr[17] = l_run;
-    }
-    __syncthreads();
-    if (half == 1) return;
-    const float m1 = xr[16], l1 = xr[17];
-    const float m = fmaxf(m_run, m1);
-    const float a0 = __builtin_amdgcn_exp2f(m_run - m);  // of query q0 + c16
-    const float a1 = __builtin_amdgcn_exp2f(m1 - m);
-    l_run = l_run * a0 + l1 * a1;
+  if constexpr (PART) {
+    // this split's O (rescaled to its own running max), max and sum
+    const size_t rows = static_cast<size_t>(sequences) * n;
+    float* po = part + (static_cast<size_t>(split) * rows + static_cast<size_t>(seq) * n) * HD;
+    float* pml = part + static_cast<size_t>(splits) * rows * HD +
+                 (static_cast<size_t>(split) * rows + static_cast<size_t>(seq) * n) * 2;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float b0 = __shfl(a0, 4 * g + r, 64), b1 = __shfl(a1, 4 * g + r, 64);
+      const int qi = q0 + 4 * g + r;
+      if (qi < n) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt][r] = o[dt][r] * b0 + xr[dt * 4 + r] * b1;
+        for (int dt = 0; dt < 4; ++dt) po[static_cast<size_t>(qi) * HD + 16 * dt + c16] = o[dt][r];
+      }
     }
+    if (g == 0 && q0 + c16 < n)
+      *reinterpret_cast<float2*>(pml + 2 * static_cast<size_t>(q0 + c16)) =
+          make_float2(m_run, l_run);
+    return;
   }
 
   // out[query][d] = O / l, O row 4g + r, column 16 dt + c16
@@ -277,6 +267,30 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_kernel(const float* __
       for (int dt = 0; dt < 4; ++dt) orow[16 * dt] = o[dt][r] / lr;
     }
   }
+}
+
+// Combines the key splits of the PART form: 16 threads per query row, one
+// float4 of O each; the splits' weights 2^(m_s - m) and sums are taken in
+// split order.
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float* __restrict__ part,
+                                                              float* __restrict__ out,
+                                                              long long rows, int splits) {
+  const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  const long long row = idx >> 4;
+  const int c4 = static_cast<int>(idx & 15);
+  if (row >= rows) return;
+  const float* ml = part + static_cast<size_t>(splits) * rows * HD;
+  float m = -INFINITY;
+  for (int sp = 0; sp < splits; ++sp) m = fmaxf(m, ml[2 * (sp * rows + row)]);
+  float l = 0.0f;
+  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < splits; ++sp) {
+    const float w = __builtin_amdgcn_exp2f(ml[2 * (sp * rows + row)] - m);
+    l = l + ml[2 * (sp * rows + row) + 1] * w;
+    o = o + *reinterpret_cast<const f32x4*>(part + (sp * rows + row) * HD + 4 * c4) * w;
+  }
+  *reinterpret_cast<f32x4*>(out + row * HD + 4 * c4) =
+      f32x4{o[0] / l, o[1] / l, o[2] / l, o[3] / l};
 }
 
 int check_qkv(const vk_tensor* t, size_t len, const char* what) {
@@ -311,24 +325,40 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
                "attention: out overlaps an input");
   }
   if (len == 0) return VK_OK;
-  // 64-query tiles unless they give fewer than two workgroups per CU; then
-  // 32-query tiles with the keys split over two halves of the workgroup
+  // 64-query tiles; when they give fewer than two workgroups per CU the key
+  // blocks of each tile are split over about two workgroups per CU (at least
+  // two key blocks per split), the partial results merged by a second pass
+  const int cus = rt->cu_count > 0 ? rt->cu_count : 256;
   const long long tiles64 = static_cast<long long>(sequences) * ((n + 63) / 64);
-  const bool narrow = tiles64 < 2LL * (rt->cu_count > 0 ? rt->cu_count : 256);
-  const int qb = narrow ? 32 : 64;
-  const long long blocks = static_cast<long long>(sequences) * ((n + qb - 1) / qb);
+  const int nkb = static_cast<int>((n + KB - 1) / KB);
+  int splits = 1;
+  if (tiles64 < 2LL * cus) {
+    splits = static_cast<int>((2.0 * cus) / static_cast<double>(tiles64) + 0.5);
+    if (splits > nkb / 2) splits = nkb / 2;
+    if (splits > 8) splits = 8;
+    if (splits < 1) splits = 1;
+  }
+  const long long blocks = tiles64 * splits;
   VK_UNSUPPORTED_IF(blocks > 0x7fffffffLL, "attention: %lld workgroups", blocks);
   const auto* Q = static_cast<const float*>(q->ptr);
   const auto* K = static_cast<const float*>(k->ptr);
   const auto* V = static_cast<const float*>(v->ptr);
   auto* O = static_cast<float*>(out->ptr);
   const int S = static_cast<int>(sequences), N = static_cast<int>(n);
-  if (narrow)
-    hipLaunchKernelGGL((attention_kernel<2, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256),
-                       0, rt->stream, Q, K, V, O, S, N);
-  else
-    hipLaunchKernelGGL((attention_kernel<4, 1>), dim3(static_cast<unsigned>(blocks)), dim3(256),
-                       0, rt->stream, Q, K, V, O, S, N);
+  if (splits > 1) {
+    const size_t rows = sequences * n;
+    VK_TRY(vk::ensure_work(rt, static_cast<size_t>(splits) * rows * (HD + 2), "attention"));
+    float* part = rt->work;
+    hipLaunchKernelGGL((attention_kernel<true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, rt->stream, Q, K, V, O, S, N, splits, part);
+    VK_TRY(vk::check_launch("attention_kernel"));
+    const long long threads = static_cast<long long>(rows) * 16;
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                       dim3(256), 0, rt->stream, part, O, static_cast<long long>(rows), splits);
+    return vk::check_launch("attention_merge_kernel");
+  }
+  hipLaunchKernelGGL((attention_kernel<false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     rt->stream, Q, K, V, O, S, N, 1, nullptr);
   return vk::check_launch("attention_kernel");
 }
 
