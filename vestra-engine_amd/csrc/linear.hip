@@ -44,7 +44,8 @@ using namespace vk::linear_epilogue;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int TN = 128;  // tile width; the tile height TM is 128 or 64 (template)
+// Tiles are TM x TN (TM 128 or 64, TN 128 or 64, template parameters); a
+// wave owns a 32-row x TN/2-column strip.
 constexpr int KC = 64;
 constexpr int PITCH = 68;
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1 && PITCH >= KC, "pitch 4 x odd");
@@ -123,12 +124,16 @@ __device__ __forceinline__ float4 qk_head_row(const LinearArgs& g, float4 v, int
       v, l, gm, bt, py, px, g.qkn.table, g.qkn.table_max, g.qkn.eps);
 }
 
-template <int EPI, int LAY, int QKN, int TM>
-__global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wide_kernel(
-    LinearArgs g) {
+template <int EPI, int LAY, int QKN, int TM, int TN>
+__global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4))
+    void linear_wide_kernel(LinearArgs g) {
+  constexpr int WN = TN / 2;  // columns of a wave's strip
+  constexpr int NU = WN / 16; // 16-column MFMA tiles per strip
+  static_assert(TN == 128 || TN == 64, "tile widths 128 and 64");
+  static_assert(QKN == 0 || TN == 128, "the Q/K epilogue takes 64-column head strips");
   constexpr int kThreads = threads_for(TM);
   constexpr int kVA = TM * KC / 4 / kThreads;  // float4 of A per thread a chunk: 4
-  constexpr int kVB = TN * KC / 4 / kThreads;  // float4 of B: 4 (TM 128) or 8 (TM 64)
+  constexpr int kVB = TN * KC / 4 / kThreads;  // float4 of B: TN / TM x 4
   static_assert(TM == 128 || TM == 64, "tile heights 128 and 64");
   static_assert(kVA * kThreads * 4 == TM * KC && kVB * kThreads * 4 == TN * KC, "slots");
   __shared__ __align__(16) float As[TM * PITCH];
@@ -148,15 +153,15 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
   const int nch = (g.K + KC - 1) / KC;
   const int c_begin = split * nch / g.splits, c_end = (split + 1) * nch / g.splits;
 
-  f32x4 acc[2][4];
+  f32x4 acc[2][NU];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NU; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kq = 4 * (lane >> 4);
   const float* arow = As + (wm * 32 + (lane & 15)) * PITCH + kq;
-  const float* brow = Bs + (wn * 64 + (lane & 15)) * PITCH + kq;
+  const float* brow = Bs + (wn * WN + (lane & 15)) * PITCH + kq;
 
   // Staging slot i of a thread: row r_i = tid/16 + (threads/16) i of the A
   // (or B) tile, float4 column c = 4 (tid % 16) of the chunk (a wave reads
@@ -182,19 +187,19 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
   auto mma_chunk = [&]() {
 #pragma unroll
     for (int b = 0; b < KC / 16; ++b) {
-      f32x4 a[2], w[4];
+      f32x4 a[2], w[NU];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         a[t] = *reinterpret_cast<const f32x4*>(arow + t * 16 * PITCH + 16 * b);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < NU; ++u)
         w[u] = *reinterpret_cast<const f32x4*>(brow + u * 16 * PITCH + 16 * b);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+          for (int u = 0; u < NU; ++u)
             acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][j], w[u][j], acc[t][u], 0, 0, 0);
     }
   };
@@ -275,11 +280,11 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
-          const int col = n0 + wn * 64 + u * 16 + (lane & 15);
+          const int col = n0 + wn * WN + u * 16 + (lane & 15);
           if (row < g.M && col < g.N) part[static_cast<size_t>(row) * g.N + col] = acc[t][u][r];
         }
     return;
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
   // epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile.
   // Parameters and (for the residual) the old values are all loaded, on
   // clamped indices, before the first store.
-  float bias[4], ls[4];
+  float bias[NU], ls[NU];
   if constexpr (QKN != 0) {
     static_assert(LAY == kQkvHnd && EPI == kLinStore, "Q/K epilogue of the QKV projection");
     const int col0 = n0 + wn * 64;  // the wave's strip: one head of Q, K or V
@@ -330,18 +335,18 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
   // the matrix stores without bounds checks.
   const bool interior = m0 + TM <= g.M && n0 + TN <= g.N;
   const size_t rs = LAY == kQkvHnd ? 64 : static_cast<size_t>(g.N);
-  float* cptr[4];
-  bool cok[4];
+  float* cptr[NU];
+  bool cok[NU];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int col = n0 + wn * 64 + u * 16 + (lane & 15);
+  for (int u = 0; u < NU; ++u) {
+    const int col = n0 + wn * WN + u * 16 + (lane & 15);
     cok[u] = col < g.N;
     const int cc = cok[u] ? col : g.N - 1;
     bias[u] = g.bias[cc];
     ls[u] = g.ls ? g.ls[cc] : 1.0f;
     cptr[u] = out_addr<LAY>(g, 0, cc);
   }
-  float old[2][4][4];
+  float old[2][NU][4];
   if constexpr (EPI == kLinResidual) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -350,7 +355,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
         const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
         const size_t cr = static_cast<size_t>(row < g.M ? row : g.M - 1);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) old[t][u][r] = cptr[u][cr * rs];
+        for (int u = 0; u < NU; ++u) old[t][u][r] = cptr[u][cr * rs];
       }
   }
 #pragma unroll
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : 3) void linear_wid
       const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
       const bool rok = row < g.M;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < NU; ++u) {
         const float val = epi_value<EPI>(g, acc[t][u][r], bias[u], ls[u],
                                          EPI == kLinResidual ? old[t][u][r] : 0.0f);
         if (interior || (rok && cok[u])) cptr[u][static_cast<size_t>(row) * rs] = val;
@@ -413,20 +418,21 @@ namespace vk {
 
 namespace {
 
-// Tile height and split count, from a cost model fitted to split sweeps of
+// Tile shape and split count, from a cost model fitted to plan sweeps of
 // the ViT-B and ViT-L projections at 866 and 3,458 rows.  Workgroups are
 // dealt round-robin to the CUs, so the busiest CU runs ceil(tiles * s / CUs)
-// workgroups of up to ceil(chunks / s) K chunks each, about 5.5 us per
-// chunk of a 128-row tile and 0.6 of that for a 64-row tile (half the
-// MFMAs, more operand traffic per MFMA: 3.0-3.5 against 4.8-6.2 us
-// measured at one to two workgroups per CU); a split adds its
+// workgroups of up to ceil(chunks / s) K chunks each: about 5.5 us per
+// chunk of a 128 x 128 tile, 0.6 of that for 64 x 128 and 0.28 for 64 x 64
+// (a quarter of the MFMAs, more operand staging per MFMA, and more
+// workgroups per CU to hide it: 1.0-1.5 us measured).  A split adds its
 // partial sums (s x M x N floats written, then read by the sum pass, at
 // about 5.5 TB/s) and the sum pass's launch (about 2 us).  The cheapest plan
-// wins; on ties the 128-row tile, then the smaller count.  At least two
+// wins; on ties the larger tile, then the smaller count.  At least two
 // chunks per split, at most VK_SPLITK_MAX slices and VK_SPLITK_MAX_FLOATS
-// floats of partial sums.  One 866-token ViT-B image: QKV 64 rows unsplit,
-// projection 64 rows x 3, FC1 128 x 3, FC2 128 x 6; 3,458 and 10,392 rows
-// keep 128-row tiles.
+// floats of partial sums.  One 866-token ViT-B image: QKV and FC1 64 x 64
+// unsplit, projection 64 x 64 x 3, FC2 128 x 128 x 6; ViT-L at 3,458 rows:
+// FC1 64 x 64, the others 128 x 128 (FC2 x 8); 10,392 rows: 128 x 128
+// unsplit.
 #ifndef VK_SPLITK_MAX
 #define VK_SPLITK_MAX 8  // most partial slices
 #endif
@@ -434,37 +440,43 @@ namespace {
 #define VK_SPLITK_MAX_FLOATS (1LL << 26)  // 256 MB of partial sums
 #endif
 #ifndef VK_LINEAR_TILES
-#define VK_LINEAR_TILES 3  // bit 0: 128-row tiles allowed, bit 1: 64-row tiles allowed
+#define VK_LINEAR_TILES 7  // allowed tiles: bit 0 128x128, bit 1 64x128, bit 2 64x64
 #endif
 
 struct Plan {
-  int tm;
+  int tm, tn;
   int splits;
   long long tiles;
 };
 
-long long tile_count(int tm, int M, int N) {
-  return static_cast<long long>((M + tm - 1) / tm) * static_cast<long long>((N + TN - 1) / TN);
+long long tile_count(int tm, int tn, int M, int N) {
+  return static_cast<long long>((M + tm - 1) / tm) * static_cast<long long>((N + tn - 1) / tn);
 }
 
 Plan choose_plan(const vk_runtime* rt, int M, int N, int K) {
   constexpr double kChunkUs = 5.5, kBytesPerUs = 5.5e6, kSumLaunchUs = 2.0;
+  // tile shape, cost of one of its K chunks relative to a 128 x 128 chunk
+  struct Shape {
+    int tm, tn, bit;
+    double cost;
+  };
+  constexpr Shape kShapes[] = {{128, 128, 1, 1.0}, {64, 128, 2, 0.6}, {64, 64, 4, 0.28}};
   const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
   const int nch = (K + KC - 1) / KC;
   const long long mn = static_cast<long long>(M) * N;
-  Plan best{0, 1, 0};
+  Plan best{0, 0, 1, 0};
   double best_us = 0.0;
-  for (int tm : {128, 64}) {
-    if (!(VK_LINEAR_TILES & (tm == 128 ? 1 : 2))) continue;
-    const long long tiles = tile_count(tm, M, N);
+  for (const Shape& sh : kShapes) {
+    if (!(VK_LINEAR_TILES & sh.bit)) continue;
+    const long long tiles = tile_count(sh.tm, sh.tn, M, N);
     for (int sp = 1; sp == 1 || (sp <= VK_SPLITK_MAX && 2 * sp <= nch &&
                                  sp * mn <= VK_SPLITK_MAX_FLOATS);
          ++sp) {
       const long long load = (tiles * sp + cus - 1) / cus * ((nch + sp - 1) / sp);
-      double us = kChunkUs * (tm == 128 ? 1.0 : 0.6) * static_cast<double>(load);
+      double us = kChunkUs * sh.cost * static_cast<double>(load);
       if (sp > 1) us += 8.0 * static_cast<double>(sp * mn) / kBytesPerUs + kSumLaunchUs;
       if (best.tm == 0 || us < best_us) {
-        best = Plan{tm, sp, tiles};
+        best = Plan{sh.tm, sh.tn, sp, tiles};
         best_us = us;
       }
     }
@@ -473,13 +485,16 @@ Plan choose_plan(const vk_runtime* rt, int M, int N, int K) {
 }
 
 template <int EPI, int LAY, int QKN = 0>
-void launch_pair(vk_runtime* rt, const LinearArgs& g, int tm, dim3 grid) {
-  if (tm == 128)
-    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 128>), grid, dim3(threads_for(128)), 0,
-                       rt->stream, g);
-  else
-    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64>), grid, dim3(threads_for(64)), 0,
-                       rt->stream, g);
+void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 grid) {
+  if (plan.tm == 128)
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 128, 128>), grid,
+                       dim3(threads_for(128)), 0, rt->stream, g);
+  else if (plan.tn == 128)
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 128>), grid, dim3(threads_for(64)),
+                       0, rt->stream, g);
+  else if constexpr (QKN == 0)
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 64>), grid, dim3(threads_for(64)),
+                       0, rt->stream, g);
   if (g.splits > 1) {
     const long long n4 = static_cast<long long>(g.M) * g.N / 4;
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN>),
@@ -492,8 +507,13 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, int tm, dim3 grid) {
 
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   LinearArgs g = g0;
-  const Plan plan = choose_plan(rt, g.M, g.N, g.K);
-  const int tm = plan.tm;
+  // An output element's bits depend on the split count only, so the plan
+  // depends on (M, N, K) alone and every layout and epilogue of one shape
+  // gives the same bits.  The Q/K epilogue works on whole 64-column head
+  // strips: a 64-wide tile becomes 64 x 128 with the same split count.
+  Plan plan = choose_plan(rt, g.M, g.N, g.K);
+  if (g.q_out != nullptr && g.qkn_mode != 0 && plan.tn != 128)
+    plan = Plan{64, 128, plan.splits, tile_count(64, 128, g.M, g.N)};
   g.splits = plan.splits;
   g.partial = nullptr;
   VK_UNSUPPORTED_IF(plan.tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", plan.tiles);
@@ -509,25 +529,25 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   if (g.q_out) {
     VK_REQUIRE(epi == kLinStore, "linear: the Q|K|V split takes the store epilogue");
     switch (g.qkn_mode) {
-      case 0: launch_pair<kLinStore, kQkvHnd>(rt, g, tm, grid); break;
-      case 1: launch_pair<kLinStore, kQkvHnd, 1>(rt, g, tm, grid); break;
-      case 2: launch_pair<kLinStore, kQkvHnd, 2>(rt, g, tm, grid); break;
-      case 3: launch_pair<kLinStore, kQkvHnd, 3>(rt, g, tm, grid); break;
+      case 0: launch_pair<kLinStore, kQkvHnd>(rt, g, plan, grid); break;
+      case 1: launch_pair<kLinStore, kQkvHnd, 1>(rt, g, plan, grid); break;
+      case 2: launch_pair<kLinStore, kQkvHnd, 2>(rt, g, plan, grid); break;
+      case 3: launch_pair<kLinStore, kQkvHnd, 3>(rt, g, plan, grid); break;
       default: return set_error(VK_ERR_INVALID, "linear: unknown Q/K epilogue %d", g.qkn_mode);
     }
   } else if (g.a_hnd) {
     if (epi == kLinResidual)
-      launch_pair<kLinResidual, kAHnd>(rt, g, tm, grid);
+      launch_pair<kLinResidual, kAHnd>(rt, g, plan, grid);
     else if (epi == kLinStore)
-      launch_pair<kLinStore, kAHnd>(rt, g, tm, grid);
+      launch_pair<kLinStore, kAHnd>(rt, g, plan, grid);
     else
       return set_error(VK_ERR_INVALID, "linear: head-major input takes store or residual");
   } else {
     switch (epi) {
-      case kLinStore: launch_pair<kLinStore, kPlain>(rt, g, tm, grid); break;
-      case kLinGelu: launch_pair<kLinGelu, kPlain>(rt, g, tm, grid); break;
-      case kLinGeluErf: launch_pair<kLinGeluErf, kPlain>(rt, g, tm, grid); break;
-      default: launch_pair<kLinResidual, kPlain>(rt, g, tm, grid); break;
+      case kLinStore: launch_pair<kLinStore, kPlain>(rt, g, plan, grid); break;
+      case kLinGelu: launch_pair<kLinGelu, kPlain>(rt, g, plan, grid); break;
+      case kLinGeluErf: launch_pair<kLinGeluErf, kPlain>(rt, g, plan, grid); break;
+      default: launch_pair<kLinResidual, kPlain>(rt, g, plan, grid); break;
     }
   }
   return check_launch("linear_wide_kernel");
