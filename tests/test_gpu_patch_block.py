@@ -111,8 +111,14 @@ def test_linear_patch_kats(rt):
 
 
 @pytest.mark.parametrize("m,k,n,with_ls", [(864, 588, 768, False), (865, 768, 768, True),
-                                           (5, 13, 8, False), (3456, 588, 1024, False)])
+                                           (5, 13, 8, False), (3456, 588, 1024, False),
+                                           (865, 3072, 768, True), (2000, 768, 700, False)])
 def test_linear_matches_oracle(rt, rng, m, k, n, with_ls):
+    """The plan model picks tile shape and split count by shape: 64 x 64
+    unsplit with a K tail (864 x 588 x 768), 64 x 64 split 3 (865 x 768 x
+    768), 128 x 128 unsplit with a K tail (3456 x 588 x 1024), 128 x 128
+    split 6 (865 x 3072 x 768), 64 x 64 split 2 with partial row and column
+    tiles (2000 x 768 x 700); K = 13 takes the narrow kernel."""
     x = normals(rng, m, k)
     w = normals(rng, k, n, scale=0.02)
     b = normals(rng, n, scale=0.02)
