@@ -2,15 +2,20 @@
 // FC1, FC2) with their per-token epilogues (bias, LayerScale, GELU,
 // residual add) fused into the store.
 //
-// A workgroup of 512 threads (8 waves) owns a 128 x 128 output tile; wave w
-// computes rows 32 (w/2) .. +32 and columns 64 (w%2) .. +64 as 2 x 4 tiles of
-// v_mfma_f32_16x16x4_f32 (F32 in, F32 accumulate): 32 MFMAs per 16-wide
-// k-block from six 128-bit LDS reads.  K is staged through LDS in chunks of
-// 64, A as [m][k] and B as [n][k] rows with a pitch of 68 floats (4 x odd:
-// the 16 rows of a fragment read start on 16 distinct 4-bank groups, and the
-// staging stores of 16 lanes fill one row without conflicts).  The 70 KB of
-// LDS leaves room for a second workgroup on the CU, which computes while the
-// first stages a chunk or runs its epilogue.
+// A workgroup owns a TM x TN output tile (128 x 128 with 512 threads, or
+// 64 x 128 / 64 x 64 with 256 for grids of few rows); wave w computes rows
+// 32 (w/2) .. +32 and columns TN/2 (w%2) .. +TN/2 as 2 x TN/32 tiles of
+// v_mfma_f32_16x16x4_f32 (F32 in, F32 accumulate): for 128-wide tiles 32
+// MFMAs per 16-wide k-block from six 128-bit LDS reads.  K is staged through
+// LDS in chunks of 64 by raw buffer loads (a lane's fixed offset plus the
+// chunk's uniform offset), A as [m][k] and B as [n][k] rows with a pitch of
+// 68 floats (4 x odd: the 16 rows of a fragment read start on 16 distinct
+// 4-bank groups, and the staging stores of 16 lanes fill one row without
+// conflicts).  The 70 KB of LDS of a 128 x 128 tile leaves room for a
+// second workgroup on the CU, which computes while the first stages a chunk
+// or runs its epilogue.  Grids of few tiles split K over several workgroups
+// per tile (split-K: partial sums in the runtime's work buffer, added in
+// split order by splitk_reduce_kernel).
 //
 // Fragment order as in the patch embedding: in block b, lane group g holds
 // k = 16b + 4g + j in component j of a 128-bit read and MFMA step j uses
