@@ -230,12 +230,12 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
   VK_TRY(vk_attention_into_f32(rt, ws->q, ws->k, ws->v, global ? H : H * view_count,
                                global ? rows : tpv, hd, ws->attn));
 
-  // tokens += (attn @ Wproj + b) * ls1
-  VK_TRY(vk_linear_run_hnd_residual_f32(rt, w->proj, ws->attn, rows, H, hd, tokens));
+  // tokens += (attn @ Wproj + b) * ls1, then LN2 (in the projection's
+  // split-K sum pass when it has one)
+  VK_TRY(vk::linear_hnd_residual_layernorm(rt, w->proj, ws->attn, rows, H, hd, tokens,
+                                           w->norm2_gamma, w->norm2_beta, cfg->ln_eps, ws->ln));
 
-  // LN2 -> FC1 + GELU -> tokens += (hidden @ Wfc2 + b) * ls2
-  VK_TRY(vk_layernorm_into_f32(rt, tokens, w->norm2_gamma, w->norm2_beta, rows, D, cfg->ln_eps,
-                               ws->ln));
+  // FC1 + GELU -> tokens += (hidden @ Wfc2 + b) * ls2
   VK_TRY(vk_linear_run_gelu_f32(rt, w->fc1, ws->ln, rows, ws->hidden));
   VK_TRY(vk_linear_run_residual_f32(rt, w->fc2, ws->hidden, rows, tokens));
   return VK_OK;

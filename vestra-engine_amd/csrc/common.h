@@ -179,6 +179,15 @@ struct LinearArgs {
   // 1 LayerNorm with f32 parameters, 2 with f16 parameters, 3 RoPE only.
   int qkn_mode;
   QkEpilogue qkn;
+  // LayerNorm of the finished rows after the residual epilogue (ln_out set):
+  // ln_out = LN(out) with ln_gamma/ln_beta (f32, or f16 when ln_f16), the
+  // bits of the separate LayerNorm.  With split-K and N of 768 or 1024 the
+  // sum pass does it row by row; otherwise the LayerNorm kernel runs after.
+  const void* ln_gamma;
+  const void* ln_beta;
+  int ln_f16;
+  float ln_eps;
+  float* ln_out;
 };
 
 // Epilogues of the linear: v = acc + b (then * ls when the linear has one),
@@ -196,6 +205,20 @@ enum LinearEpilogue {
 // The 128x128-tile linear for K % 4 == 0 and a 16-byte aligned x (linear.hip);
 // the head-major layouts of LinearArgs need it.
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi);
+
+// LayerNorm of `rows` x `cols` f32 rows (the layernorm_rows kernel) on raw
+// pointers; gamma/beta f16 when `f16`.
+int layernorm_raw(vk_runtime* rt, const float* x, float* y, const void* gamma, const void* beta,
+                  bool f16, int rows, int cols, float eps);
+
+// Output projection of the head-major attention output with LayerScale +
+// residual into `residual`, then ln_out = LayerNorm(residual): the calls
+// vk_linear_run_hnd_residual_f32 + vk_layernorm_into_f32 with the same
+// bits, one launch fewer when the projection runs split-K.
+int linear_hnd_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
+                                  size_t rows, size_t heads, size_t head_dim,
+                                  vk_tensor* residual, const vk_tensor* gamma,
+                                  const vk_tensor* beta, float eps, vk_tensor* ln_out);
 
 }  // namespace vk
 

@@ -417,6 +417,52 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
                         old[j]);
 }
 
+// Sum pass of a split-K linear with the residual epilogue, followed by the
+// LayerNorm of the finished rows: one wave per row, NV float4 per lane
+// (column float4 lane + 64 i).  The partial sums are added in split order
+// and the epilogue applied as in splitk_reduce_kernel, the row statistics
+// and the normalisation are vkd::row_mean_inv / vkd::ln_apply4 over the same
+// lane layout as layernorm_rows: the bits of the two separate passes.
+template <int NV, typename PT>
+__global__ __launch_bounds__(64) void splitk_residual_ln_kernel(LinearArgs g) {
+  const int lane = threadIdx.x;
+  const size_t row = blockIdx.x;
+  const size_t mn = static_cast<size_t>(g.M) * g.N;
+  const size_t rb = row * g.N;
+  float4 vv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c4 = lane + 64 * i;
+    const size_t e = rb + 4 * static_cast<size_t>(c4);
+    f32x4 acc = *reinterpret_cast<const f32x4*>(g.partial + e);
+    for (int sp = 1; sp < g.splits; ++sp)
+      acc = acc + *reinterpret_cast<const f32x4*>(g.partial + sp * mn + e);
+    const f32x4 old = *reinterpret_cast<const f32x4*>(g.out + e);
+    const int col = 4 * c4;
+    float4 v;
+    v.x = epi_value<kLinResidual>(g, acc[0], g.bias[col], g.ls ? g.ls[col] : 1.0f, old[0]);
+    v.y = epi_value<kLinResidual>(g, acc[1], g.bias[col + 1], g.ls ? g.ls[col + 1] : 1.0f,
+                                  old[1]);
+    v.z = epi_value<kLinResidual>(g, acc[2], g.bias[col + 2], g.ls ? g.ls[col + 2] : 1.0f,
+                                  old[2]);
+    v.w = epi_value<kLinResidual>(g, acc[3], g.bias[col + 3], g.ls ? g.ls[col + 3] : 1.0f,
+                                  old[3]);
+    *reinterpret_cast<float4*>(g.out + e) = v;
+    vv[i] = v;
+  }
+  float mean, inv;
+  vkd::row_mean_inv<NV, true>(vv, lane, g.N, g.ln_eps, &mean, &inv);
+  const PT* gm = static_cast<const PT*>(g.ln_gamma);
+  const PT* bt = static_cast<const PT*>(g.ln_beta);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c4 = lane + 64 * i;
+    *reinterpret_cast<float4*>(g.ln_out + rb + 4 * static_cast<size_t>(c4)) =
+        vkd::ln_apply4(vv[i], mean, inv, vkd::Param<PT>::load4(gm, c4),
+                       vkd::Param<PT>::load4(bt, c4));
+  }
+}
+
 }  // namespace
 
 namespace vk {
@@ -490,7 +536,8 @@ Plan choose_plan(const vk_runtime* rt, int M, int N, int K) {
 }
 
 template <int EPI, int LAY, int QKN = 0>
-void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 grid) {
+void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 grid,
+                 bool sum_pass = true) {
   if (plan.tm == 128)
     hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 128, 128>), grid,
                        dim3(threads_for(128)), 0, rt->stream, g);
@@ -500,7 +547,7 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 gri
   else if constexpr (QKN == 0)
     hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 64>), grid, dim3(threads_for(64)),
                        0, rt->stream, g);
-  if (g.splits > 1) {
+  if (g.splits > 1 && sum_pass) {
     const long long n4 = static_cast<long long>(g.M) * g.N / 4;
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN>),
                        dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, rt->stream,
@@ -531,6 +578,12 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
     g.partial = rt->work;
   }
   const dim3 grid(static_cast<unsigned>(plan.tiles * g.splits));
+  // LayerNorm after the residual epilogue: in the sum pass when there is
+  // one and a row is 768 or 1024 floats, else as a separate pass
+  const bool post_ln = g.ln_out != nullptr;
+  VK_REQUIRE(!post_ln || (epi == kLinResidual && !g.q_out),
+             "linear: the LayerNorm follows the residual epilogue only");
+  const bool fused_ln = post_ln && g.splits > 1 && (g.N == 768 || g.N == 1024);
   if (g.q_out) {
     VK_REQUIRE(epi == kLinStore, "linear: the Q|K|V split takes the store epilogue");
     switch (g.qkn_mode) {
@@ -542,7 +595,7 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
     }
   } else if (g.a_hnd) {
     if (epi == kLinResidual)
-      launch_pair<kLinResidual, kAHnd>(rt, g, plan, grid);
+      launch_pair<kLinResidual, kAHnd>(rt, g, plan, grid, !fused_ln);
     else if (epi == kLinStore)
       launch_pair<kLinStore, kAHnd>(rt, g, plan, grid);
     else
@@ -552,10 +605,29 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
       case kLinStore: launch_pair<kLinStore, kPlain>(rt, g, plan, grid); break;
       case kLinGelu: launch_pair<kLinGelu, kPlain>(rt, g, plan, grid); break;
       case kLinGeluErf: launch_pair<kLinGeluErf, kPlain>(rt, g, plan, grid); break;
-      default: launch_pair<kLinResidual, kPlain>(rt, g, plan, grid); break;
+      default: launch_pair<kLinResidual, kPlain>(rt, g, plan, grid, !fused_ln); break;
     }
   }
-  return check_launch("linear_wide_kernel");
+  VK_TRY(check_launch("linear_wide_kernel"));
+  if (fused_ln) {
+    const dim3 rows(static_cast<unsigned>(g.M));
+    const bool f16 = g.ln_f16 != 0;
+    if (g.N == 768 && !f16)
+      hipLaunchKernelGGL((splitk_residual_ln_kernel<3, float>), rows, dim3(64), 0, rt->stream, g);
+    else if (g.N == 768)
+      hipLaunchKernelGGL((splitk_residual_ln_kernel<3, uint16_t>), rows, dim3(64), 0, rt->stream,
+                         g);
+    else if (!f16)
+      hipLaunchKernelGGL((splitk_residual_ln_kernel<4, float>), rows, dim3(64), 0, rt->stream, g);
+    else
+      hipLaunchKernelGGL((splitk_residual_ln_kernel<4, uint16_t>), rows, dim3(64), 0, rt->stream,
+                         g);
+    return check_launch("splitk_residual_ln_kernel");
+  }
+  if (post_ln)
+    return layernorm_raw(rt, g.out, g.ln_out, g.ln_gamma, g.ln_beta, g.ln_f16 != 0, g.M, g.N,
+                         g.ln_eps);
+  return VK_OK;
 }
 
 }  // namespace vk

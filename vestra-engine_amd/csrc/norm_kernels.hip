@@ -295,6 +295,17 @@ int check_qk_params(const vk_tensor* qg, const vk_tensor* qb, const vk_tensor* k
 
 }  // namespace
 
+namespace vk {
+
+int layernorm_raw(vk_runtime* rt, const float* x, float* y, const void* gamma, const void* beta,
+                  bool f16, int rows, int cols, float eps) {
+  if (rows == 0) return VK_OK;
+  return f16 ? launch_layernorm<uint16_t>(rt, x, y, gamma, beta, rows, cols, eps)
+             : launch_layernorm<float>(rt, x, y, gamma, beta, rows, cols, eps);
+}
+
+}  // namespace vk
+
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
