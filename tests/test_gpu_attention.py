@@ -141,3 +141,50 @@ def test_attention_edges_and_errors(rt):
         rt.attention_online_f32(y, y, y, 2, 6, 64)            # size mismatch
     with pytest.raises(vh.VestraError):
         rt.attention_into_f32(y, y, y, 2, 5, 64, y)           # out overlaps q
+
+
+def test_attention_key_split_capture_rules(rng):
+    """One image's attention (12 x 866: three key splits per query tile)
+    keeps its partial results in the runtime's work buffer: the first call
+    inside a stream capture is refused, a graph captured after an eager call
+    replays the eager result bit for bit."""
+    import gc
+    rt = vh.Runtime(0)  # fresh runtime: no work buffer yet
+    _key_split_case(rt, rng)
+    gc.collect()
+    rt.close()
+
+
+def _key_split_case(rt, rng):
+    import gc
+    seqs, n = 12, 866
+    q, k, v = (rt.upload_f32(normals(rng, seqs, n, 64)) for _ in range(3))
+    out = rt.alloc_f32(seqs * n * 64)
+
+    def step():
+        rt.attention_into_f32(q, k, v, seqs, n, 64, out)
+
+    rt.synchronize()
+    gc.disable()
+    try:
+        rt.begin_capture()
+        with pytest.raises(vh.VestraError, match="before stream capture"):
+            step()
+        rt.end_capture()
+    finally:
+        gc.enable()
+    step()
+    want = out.numpy()
+    rt.synchronize()
+    gc.disable()
+    try:
+        rt.begin_capture()
+        step()
+        graph = rt.end_capture()
+    finally:
+        gc.enable()
+    for _ in range(3):
+        out.write(np.zeros(seqs * n * 64, np.float32))
+        graph.launch()
+        rt.synchronize()
+        assert np.array_equal(out.numpy(), want)
