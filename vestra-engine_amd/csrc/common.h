@@ -202,7 +202,8 @@ enum LinearEpilogue {
 };
 }  // namespace linear_epilogue
 
-// The 128x128-tile linear for K % 4 == 0 and a 16-byte aligned x (linear.hip);
+// The wide-tile linear (128 x 128, 64 x 128 or 64 x 64 tiles, split-K for
+// few rows) for K % 4 == 0 and a 16-byte aligned x (linear.hip);
 // the head-major layouts of LinearArgs need it.
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi);
 
