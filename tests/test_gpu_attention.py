@@ -61,8 +61,13 @@ def _run(rt, q, k, v, seqs, n):
                                    n, 64).numpy().reshape(seqs, n, 64)
 
 
-@pytest.mark.parametrize("seqs,n", [(1, 1), (3, 37), (2, 64), (2, 65), (1, 129), (12, 866)])
+@pytest.mark.parametrize("seqs,n", [(1, 1), (3, 37), (2, 64), (2, 65), (1, 129), (12, 866),
+                                    (2, 1000), (1, 3000)])
 def test_attention_matches_oracle(rt, rng, seqs, n):
+    """Grids of fewer than two 64-query workgroups per CU split each tile's
+    key blocks over workgroups: 12 x 866 in 3 splits, 2 x 1000 in 8 splits
+    of 2 blocks, 1 x 3000 in 8 splits of 5-6 blocks (ending in the partial
+    block); the others run one workgroup per tile."""
     q, k, v = (normals(rng, seqs, n, 64) for _ in range(3))
     got = _run(rt, q, k, v, seqs, n)
     want = oracle.attention(q, k, v, seqs, n, 64)
