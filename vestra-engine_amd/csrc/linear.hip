@@ -24,16 +24,16 @@
 // Head-major layouts (head_dim 64): the QKV projection can store Q | K | V
 // straight into three [heads, rows, 64] tensors (the split the attention
 // kernels need), and the output projection can read its input from the
-// head-major attention output; a 64-column strip of a wave is one head, and
-// a float4 of A never crosses a head.  Both are pure address changes: the
-// results are the bits of the linear plus the separate permutation.
+// head-major attention output; tiles start on 64-column head boundaries,
+// and a float4 of A never crosses a head.  Both are pure address changes:
+// the results are the bits of the linear plus the separate permutation.
 //
-// Q/K-norm + RoPE in the QKV epilogue (QKN != 0): after the last chunk each
-// wave that holds a Q or K head strip writes its 32 x 64 values (acc + b)
-// to LDS and reads them back as the Q/K kernel holds a row -- 16 lanes per
-// 64-wide row, one float4 each -- and applies the same row transform
-// (vkq::qk_row_transform) before storing the row head-major.  The values
-// and the code path are those of the separate pass, so the bits are too.
+// Q/K-norm + RoPE in the QKV epilogue (QKN != 0): after the last chunk the
+// waves holding Q or K heads write their values (acc + b) to LDS and read
+// them back as the Q/K kernel holds a row -- 16 lanes per 64-wide row, one
+// float4 each -- and apply the same row transform (vkq::qk_row_transform)
+// before storing the row head-major.  The values and the code path are
+// those of the separate pass, so the bits are too.
 //
 // Traffic: a 128 x 128 tile moves (128 + 128) x 4 bytes of operands per k for
 // 2 x 128 x 128 FLOP, 0.031 byte per FLOP from L2 (the 48 x 64 tiles of the
@@ -135,7 +135,6 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
   constexpr int WN = TN / 2;  // columns of a wave's strip
   constexpr int NU = WN / 16; // 16-column MFMA tiles per strip
   static_assert(TN == 128 || TN == 64, "tile widths 128 and 64");
-  static_assert(QKN == 0 || TN == 128, "the Q/K epilogue takes 64-column head strips");
   constexpr int kThreads = threads_for(TM);
   constexpr int kVA = TM * KC / 4 / kThreads;  // float4 of A per thread a chunk: 4
   constexpr int kVB = TN * KC / 4 / kThreads;  // float4 of B: TN / TM x 4
@@ -301,23 +300,32 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
   float bias[NU], ls[NU];
   if constexpr (QKN != 0) {
     static_assert(LAY == kQkvHnd && EPI == kLinStore, "Q/K epilogue of the QKV projection");
-    const int col0 = n0 + wn * 64;  // the wave's strip: one head of Q, K or V
+    // One head of Q, K or V: a 128-wide tile gives each wave a head of its
+    // own (its 32 x 64 strip); a 64-wide tile is one head, whose 32-row
+    // halves waves wn 0 and 1 hold 32 columns each of and then transform 16
+    // rows each.
+    const int col0 = TN == 128 ? n0 + wn * 64 : n0;
+    const int cw0 = TN == 128 ? 0 : wn * 32;  // the wave's first column in the head
+    constexpr int kRowsPerGroup = TN == 128 ? 8 : 4;
+    const int rr0 = TN == 128 ? 0 : wn * 16;
     const int embed = g.N / 3;
     const int which = col0 < g.N ? col0 / embed : 2;
     const int g4 = lane >> 4, c16 = lane & 15;
-    // a 32-row staging region per wave: the A tile holds TM / 32 of them,
-    // the B tile the rest
-    float* xs = wave < TM / 32 ? As + wave * 32 * PITCH : Bs + (wave - TM / 32) * 32 * PITCH;
+    // 32-row staging regions: TN 128, one per wave (the A tile holds TM / 32
+    // of them, the B tile the rest); TN 64, one per row half wm, in the A tile
+    float* xs = TN == 64 ? As + wm * 32 * PITCH
+                         : (wave < TM / 32 ? As + wave * 32 * PITCH
+                                           : Bs + (wave - TM / 32) * 32 * PITCH);
     __syncthreads();  // every wave is done with the last chunk's operands
     if (which < 2) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float b = g.bias[col0 + u * 16 + c16];
+      for (int u = 0; u < NU; ++u) {
+        const float b = g.bias[col0 + cw0 + u * 16 + c16];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            xs[(t * 16 + 4 * g4 + r) * PITCH + u * 16 + c16] = acc[t][u][r] + b;
+            xs[(t * 16 + 4 * g4 + r) * PITCH + cw0 + u * 16 + c16] = acc[t][u][r] + b;
       }
     }
     __syncthreads();
@@ -325,8 +333,8 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
       float* dst = (which == 0 ? g.q_out : g.k_out) +
                    static_cast<size_t>((col0 - which * embed) >> 6) * g.M * 64;
 #pragma unroll 2
-      for (int i = 0; i < 8; ++i) {
-        const int rr = g4 * 8 + i;
+      for (int i = 0; i < kRowsPerGroup; ++i) {
+        const int rr = rr0 + g4 * kRowsPerGroup + i;
         const int row = m0 + wm * 32 + rr;
         const float4 v = *reinterpret_cast<const float4*>(xs + rr * PITCH + 4 * c16);
         const float4 o = qk_head_row<QKN>(g, v, c16, which == 1, row);
@@ -544,7 +552,7 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 gri
   else if (plan.tn == 128)
     hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 128>), grid, dim3(threads_for(64)),
                        0, rt->stream, g);
-  else if constexpr (QKN == 0)
+  else
     hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 64>), grid, dim3(threads_for(64)),
                        0, rt->stream, g);
   if (g.splits > 1 && sum_pass) {
@@ -561,11 +569,8 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   LinearArgs g = g0;
   // An output element's bits depend on the split count only, so the plan
   // depends on (M, N, K) alone and every layout and epilogue of one shape
-  // gives the same bits.  The Q/K epilogue works on whole 64-column head
-  // strips: a 64-wide tile becomes 64 x 128 with the same split count.
-  Plan plan = choose_plan(rt, g.M, g.N, g.K);
-  if (g.q_out != nullptr && g.qkn_mode != 0 && plan.tn != 128)
-    plan = Plan{64, 128, plan.splits, tile_count(64, 128, g.M, g.N)};
+  // gives the same bits.
+  const Plan plan = choose_plan(rt, g.M, g.N, g.K);
   g.splits = plan.splits;
   g.partial = nullptr;
   VK_UNSUPPORTED_IF(plan.tiles * g.splits > 0x7fffffffLL, "linear: %lld tiles", plan.tiles);
