@@ -125,7 +125,9 @@ def test_head_major_linears_reject_unqualified_shapes(rt, rng):
 
 
 @pytest.mark.parametrize("embed,heads,gh,gw,views,glob,f16,norm", [
-    (768, 12, 24, 36, 1, False, False, True),     # one 504x336 image: split-K path
+    (768, 12, 24, 36, 1, False, False, True),     # one 504x336 image: 64 x 64 tiles
+    (768, 12, 24, 36, 1, False, True, True),      # the same, f16 parameters
+    (768, 12, 24, 36, 1, True, False, False),     # the same, RoPE only, global layer
     (768, 12, 24, 36, 12, True, False, True),     # 12-view global layer
     (768, 12, 24, 36, 12, False, False, True),    # 12-view local layer
     (1024, 16, 4, 8, 2, False, True, True),       # ViT-L, f16 parameters
