@@ -28,6 +28,10 @@ import statistics
 import sys
 import time
 
+# the CPU baseline's OpenMP threads stay on neighbouring cores (read when the
+# OpenMP runtime starts, so it is set before anything loads one)
+os.environ.setdefault("OMP_PROC_BIND", "close")
+
 import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -169,6 +173,7 @@ def capture(rt, fn, count=1):
 ROTATE_SETS = 8  # 8 x 288 MB at the 12-view shape: every operation's working set
                  # (>= 512 MB) exceeds the 256 MB Infinity Cache
 OP_TRIALS = 5
+SINGLE_COLD_SETS = 64  # 866-row buffer sets cycled for the cold single-image table
 
 
 def per_op_table(rt, rng, rows, rotate, iters, only=None):
@@ -236,6 +241,33 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
 
 
 MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def dispatch_overhead(rt, launches=200):
+    """Empty-kernel dispatch overhead: the per-launch time of a minimal kernel
+    (one workgroup adding 64 floats) replayed back to back in a HIP graph,
+    median of several replays -- the floor under every launch of the path."""
+    a = rt.upload_f32(np.zeros(64, np.float32))
+    b = rt.upload_f32(np.ones(64, np.float32))
+    fn = lambda: rt.add_f32_in_place(a, b)  # noqa: E731
+    fn()
+    graph = capture(rt, fn, launches)
+    graph.launch()
+    us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / launches
+                           for _ in range(OP_TRIALS))
+    return {"us_per_launch": round(us, 3), "launches_per_graph": launches,
+            "kernel": "add_kernel, 1 workgroup, 64 floats"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def linear_epilogue_timing(rt, rng, rows, iters):
@@ -654,20 +686,31 @@ def cpu_baseline(model, seconds, threads):
         lib.ora_gelu_f32(p(a["hidden"]), a["hidden"].size)
         lib.ora_layerscale_residual_f32(p(a["tokens"]), p(a["mlp_out"]), p(lay["ls2"]), r, D)
 
-    one_block()  # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 1000):
-        t0 = time.perf_counter()
-        one_block()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    def timed(budget):
+        one_block()  # warm-up
+        times = []
+        t_end = time.perf_counter() + budget
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 1000):
+            t0 = time.perf_counter()
+            one_block()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
     nbytes = ln_bytes(r) * 2 + qk_bytes(r) + lsres_bytes(r) * 2 + gelu_bytes(r)
+    med, runs = timed(seconds)
+    # the same oracle on one thread (the scalar restatement as written)
+    oracle.set_threads(1)
+    med1, runs1 = timed(seconds / 2)
+    oracle.set_threads(threads)
     return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
             "kind": "port", "us_per_block": round(med * 1e6, 1),
+            "cpu_model": cpu_model(), "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+            "single_thread": {"value": round(nbytes / med1 / 1e9, 2), "unit": "GB/s",
+                              "cores": 1, "us_per_block": round(med1 * 1e6, 1),
+                              "runs": runs1},
             "sample": (f"oracle (scalar C, OpenMP over rows) on one ViT-B block's fused ops "
                        f"(LN1, Q/K-norm+RoPE, LS+res, LN2, GELU, LS+res) over {r} rows "
-                       f"(12 views x {TPV}); median of {len(times)} runs after 1 warm-up")}
+                       f"(12 views x {TPV}); median of {runs} runs after 1 warm-up")}
 
 
 def measured_traffic(op, algorithmic_bytes):
@@ -800,6 +843,11 @@ def main():
     log("per-operation table")
     ops12 = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters)
     ops1 = per_op_table(rt, rng, TPV, rotate=1, iters=args.op_iters)
+    # the single-image shape again with its inputs in HBM: 64 rotating sets
+    # (>= 340 MB per operation) cycle past the 256 MB Infinity Cache
+    ops1_cold = per_op_table(rt, rng, TPV, rotate=SINGLE_COLD_SETS,
+                             iters=max(args.op_iters, 2 * SINGLE_COLD_SETS))
+    tau0 = dispatch_overhead(rt)
     log("patch embedding")
     patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
              patch_embed_timing(rt, rng, 672, 1008, 1024, args.op_iters)]
@@ -842,7 +890,14 @@ def main():
         "us_per_block_single_image": round(ms_single * 1e3 / DEPTH, 2),
         "single_image_GB_s": round(single_bytes / (ms_single * 1e-3) / 1e9, 1),
         "ops_12view": ops12,
+        "ops_12view_mode": (f"cold HBM: {ROTATE_SETS} rotating buffer sets, every operation's "
+                            f"working set >= 512 MB, beyond the 256 MB Infinity Cache"),
         "ops_single_image": ops1,
+        "ops_single_image_mode": ("warm (effective GB/s): one buffer set of 5-21 MB, "
+                                  "cache-resident between launches"),
+        "ops_single_image_cold": ops1_cold,
+        "ops_single_image_cold_mode": (f"cold HBM: {SINGLE_COLD_SETS} rotating buffer sets"),
+        "dispatch_overhead": tau0,
         "patch_embed": patch,
         "linear_epilogues": linear,
         "attention": attention,
