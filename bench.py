@@ -243,7 +243,7 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
-def dispatch_overhead(rt, launches=200):
+def dispatch_overhead(rt, launches=100):
     """Empty-kernel dispatch overhead: the per-launch time of a minimal kernel
     (one workgroup adding 64 floats) replayed back to back in a HIP graph,
     median of several replays -- the floor under every launch of the path."""
@@ -846,7 +846,7 @@ def main():
     # the single-image shape again with its inputs in HBM: 64 rotating sets
     # (>= 340 MB per operation) cycle past the 256 MB Infinity Cache
     ops1_cold = per_op_table(rt, rng, TPV, rotate=SINGLE_COLD_SETS,
-                             iters=max(args.op_iters, 2 * SINGLE_COLD_SETS))
+                             iters=max(args.op_iters, SINGLE_COLD_SETS))
     tau0 = dispatch_overhead(rt)
     log("patch embedding")
     patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
