@@ -271,23 +271,35 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
 
 // Combines the key splits of the PART form: 16 threads per query row, one
 // float4 of O each; the splits' weights 2^(m_s - m) and sums are taken in
-// split order.
+// split order.  SP (the split count) is a template parameter so that every
+// load of a row is issued before the first is used: with a run-time count
+// each loop iteration waited for its own loads.
+template <int SP>
 __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __restrict__ part,
                                                               float* __restrict__ out,
-                                                              long long rows, int splits) {
+                                                              long long rows) {
   const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
   const long long row = idx >> 4;
   const int c4 = static_cast<int>(idx & 15);
   if (row >= rows) return;
-  const float* ml = part + static_cast<size_t>(splits) * rows * HD;
+  const float* ml = part + static_cast<size_t>(SP) * rows * HD;
+  float2 st[SP];
+  f32x4 po[SP];
+#pragma unroll
+  for (int sp = 0; sp < SP; ++sp) {
+    st[sp] = *reinterpret_cast<const float2*>(ml + 2 * (sp * rows + row));
+    po[sp] = *reinterpret_cast<const f32x4*>(part + (sp * rows + row) * HD + 4 * c4);
+  }
   float m = -INFINITY;
-  for (int sp = 0; sp < splits; ++sp) m = fmaxf(m, ml[2 * (sp * rows + row)]);
+#pragma unroll
+  for (int sp = 0; sp < SP; ++sp) m = fmaxf(m, st[sp].x);
   float l = 0.0f;
   f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int sp = 0; sp < splits; ++sp) {
-    const float w = __builtin_amdgcn_exp2f(ml[2 * (sp * rows + row)] - m);
-    l = l + ml[2 * (sp * rows + row) + 1] * w;
-    o = o + *reinterpret_cast<const f32x4*>(part + (sp * rows + row) * HD + 4 * c4) * w;
+#pragma unroll
+  for (int sp = 0; sp < SP; ++sp) {
+    const float w = __builtin_amdgcn_exp2f(st[sp].x - m);
+    l = l + st[sp].y * w;
+    o = o + po[sp] * w;
   }
   *reinterpret_cast<f32x4*>(out + row * HD + 4 * c4) =
       f32x4{o[0] / l, o[1] / l, o[2] / l, o[3] / l};
@@ -353,8 +365,19 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
                        dim3(256), 0, rt->stream, Q, K, V, O, S, N, splits, part);
     VK_TRY(vk::check_launch("attention_kernel"));
     const long long threads = static_cast<long long>(rows) * 16;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
-                       dim3(256), 0, rt->stream, part, O, static_cast<long long>(rows), splits);
+    const dim3 mgrid(static_cast<unsigned>((threads + 255) / 256));
+    const long long R = static_cast<long long>(rows);
+    switch (splits) {
+#define VK_MERGE_CASE(SPN)                                                                     \
+  case SPN:                                                                                    \
+    hipLaunchKernelGGL(attention_merge_kernel<SPN>, mgrid, dim3(256), 0, rt->stream, part, O, R); \
+    break;
+      VK_MERGE_CASE(2) VK_MERGE_CASE(3) VK_MERGE_CASE(4) VK_MERGE_CASE(5)
+      VK_MERGE_CASE(6) VK_MERGE_CASE(7) VK_MERGE_CASE(8)
+#undef VK_MERGE_CASE
+      default:
+        return vk::set_error(VK_ERR_INVALID, "attention: %d key splits", splits);
+    }
     return vk::check_launch("attention_merge_kernel");
   }
   hipLaunchKernelGGL((attention_kernel<false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
