@@ -386,19 +386,49 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
     }
 }
 
+// Most split-K slices a sum pass reads (the plan's limit, checked where it
+// is defined).  The sum passes are instantiated for split-count buckets SPB
+// of 2, 4 and 8 (split_bucket).
+constexpr int kMaxSplits = 8;
+constexpr int split_bucket(int splits) { return splits <= 2 ? 2 : (splits <= 4 ? 4 : 8); }
+
+// The NV float4 at offsets e[i] of every split's slice (splits <= SPB),
+// summed in split order.  All SPB x NV loads are issued before the first
+// addition (a run-time loop over the splits waited for each iteration's
+// load); slots past `splits` re-read the last slice and are not added.
+template <int NV, int SPB>
+__device__ __forceinline__ void split_sums(const float* __restrict__ partial, size_t mn,
+                                           const size_t (&e)[NV], int splits, f32x4 (&acc)[NV]) {
+  f32x4 p[NV][SPB];
+#pragma unroll
+  for (int sp = 0; sp < SPB; ++sp) {
+    const size_t slice = static_cast<size_t>(sp < splits ? sp : splits - 1) * mn;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) p[i][sp] = *reinterpret_cast<const f32x4*>(partial + slice + e[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    acc[i] = p[i][0];
+#pragma unroll
+    for (int sp = 1; sp < SPB; ++sp)
+      if (sp < splits) acc[i] = acc[i] + p[i][sp];
+  }
+}
+
 // Second pass of a split-K linear: one thread per 4 consecutive outputs of a
 // row; the splits' partial sums are added in split order, then the epilogue
 // of the single-pass kernel is applied.
-template <int EPI, int LAY, int QKN = 0>
+template <int EPI, int LAY, int QKN, int SPB>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
   const long long i4 = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
   const long long mn = static_cast<long long>(g.M) * g.N;
   if (i4 * 4 >= mn) return;  // whole 16-lane groups (M*N/4 is a multiple of 16 here)
   const size_t e = static_cast<size_t>(i4) * 4;
   const int row = static_cast<int>(e / g.N), col = static_cast<int>(e % g.N);
-  f32x4 acc = *reinterpret_cast<const f32x4*>(g.partial + e);
-  for (int sp = 1; sp < g.splits; ++sp)
-    acc = acc + *reinterpret_cast<const f32x4*>(g.partial + static_cast<size_t>(sp) * mn + e);
+  const size_t es[1] = {e};
+  f32x4 accs[1];
+  split_sums<1, SPB>(g.partial, static_cast<size_t>(mn), es, g.splits, accs);
+  const f32x4 acc = accs[0];
   if constexpr (QKN != 0) {
     // 16 consecutive threads hold one 64-wide head row of one token
     const int embed = g.N / 3;
@@ -431,20 +461,23 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
 // and the epilogue applied as in splitk_reduce_kernel, the row statistics
 // and the normalisation are vkd::row_mean_inv / vkd::ln_apply4 over the same
 // lane layout as layernorm_rows: the bits of the two separate passes.
-template <int NV, typename PT>
+template <int NV, typename PT, int SPB>
 __global__ __launch_bounds__(64) void splitk_residual_ln_kernel(LinearArgs g) {
   const int lane = threadIdx.x;
   const size_t row = blockIdx.x;
   const size_t mn = static_cast<size_t>(g.M) * g.N;
   const size_t rb = row * g.N;
   float4 vv[NV];
+  size_t es[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) es[i] = rb + 4 * static_cast<size_t>(lane + 64 * i);
+  f32x4 accs[NV];
+  split_sums<NV, SPB>(g.partial, mn, es, g.splits, accs);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c4 = lane + 64 * i;
-    const size_t e = rb + 4 * static_cast<size_t>(c4);
-    f32x4 acc = *reinterpret_cast<const f32x4*>(g.partial + e);
-    for (int sp = 1; sp < g.splits; ++sp)
-      acc = acc + *reinterpret_cast<const f32x4*>(g.partial + sp * mn + e);
+    const size_t e = es[i];
+    const f32x4 acc = accs[i];
     const f32x4 old = *reinterpret_cast<const f32x4*>(g.out + e);
     const int col = 4 * c4;
     float4 v;
@@ -495,6 +528,8 @@ namespace {
 #ifndef VK_SPLITK_MAX
 #define VK_SPLITK_MAX 8  // most partial slices
 #endif
+static_assert(VK_SPLITK_MAX >= 1 && VK_SPLITK_MAX <= kMaxSplits,
+              "the sum passes read at most kMaxSplits slices");
 #ifndef VK_SPLITK_MAX_FLOATS
 #define VK_SPLITK_MAX_FLOATS (1LL << 26)  // 256 MB of partial sums
 #endif
@@ -557,9 +592,21 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 gri
                        0, rt->stream, g);
   if (g.splits > 1 && sum_pass) {
     const long long n4 = static_cast<long long>(g.M) * g.N / 4;
-    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN>),
-                       dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, rt->stream,
-                       g);
+    const dim3 sgrid(static_cast<unsigned>((n4 + 255) / 256));
+    switch (split_bucket(g.splits)) {
+      case 2:
+        hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN, 2>), sgrid, dim3(256), 0,
+                           rt->stream, g);
+        break;
+      case 4:
+        hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN, 4>), sgrid, dim3(256), 0,
+                           rt->stream, g);
+        break;
+      default:
+        hipLaunchKernelGGL((splitk_reduce_kernel<EPI, LAY, QKN, 8>), sgrid, dim3(256), 0,
+                           rt->stream, g);
+        break;
+    }
   }
 }
 
@@ -617,16 +664,17 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
   if (fused_ln) {
     const dim3 rows(static_cast<unsigned>(g.M));
     const bool f16 = g.ln_f16 != 0;
-    if (g.N == 768 && !f16)
-      hipLaunchKernelGGL((splitk_residual_ln_kernel<3, float>), rows, dim3(64), 0, rt->stream, g);
-    else if (g.N == 768)
-      hipLaunchKernelGGL((splitk_residual_ln_kernel<3, uint16_t>), rows, dim3(64), 0, rt->stream,
-                         g);
-    else if (!f16)
-      hipLaunchKernelGGL((splitk_residual_ln_kernel<4, float>), rows, dim3(64), 0, rt->stream, g);
-    else
-      hipLaunchKernelGGL((splitk_residual_ln_kernel<4, uint16_t>), rows, dim3(64), 0, rt->stream,
-                         g);
+    const int nv = g.N == 768 ? 3 : 4;
+    const int spb = split_bucket(g.splits);
+#define VK_SKLN(NVV, PTT, SPBB)                                                                \
+  if (nv == NVV && f16 == (sizeof(PTT) == 2) && spb == SPBB)                                    \
+    hipLaunchKernelGGL((splitk_residual_ln_kernel<NVV, PTT, SPBB>), rows, dim3(64), 0,          \
+                       rt->stream, g);
+    VK_SKLN(3, float, 2) VK_SKLN(3, float, 4) VK_SKLN(3, float, 8)
+    VK_SKLN(3, uint16_t, 2) VK_SKLN(3, uint16_t, 4) VK_SKLN(3, uint16_t, 8)
+    VK_SKLN(4, float, 2) VK_SKLN(4, float, 4) VK_SKLN(4, float, 8)
+    VK_SKLN(4, uint16_t, 2) VK_SKLN(4, uint16_t, 4) VK_SKLN(4, uint16_t, 8)
+#undef VK_SKLN
     return check_launch("splitk_residual_ln_kernel");
   }
   if (post_ln)
