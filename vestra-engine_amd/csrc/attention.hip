@@ -92,6 +92,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   const int split = PART ? tile_all % splits : 0;
   const int tile = PART ? tile_all / splits : tile_all;
   const int seq = tile / nqb, q0 = (tile % nqb) * QB + wq * 16;
+  const bool live = q0 < n;  // uniform over the wave
   const size_t base = static_cast<size_t>(seq) * n * HD;
 
   // Q^T fragments (B operand): query q0 + c16, d = 16 bd + 4 g + j
@@ -174,6 +175,9 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
       for (int c = 0; c < 4; ++c) Vt[(d + c) * PITCH + key] = vr[i][c];
     }
     __syncthreads();
+    // a wave whose 16 queries all lie past n only stages (the last query tile
+    // of a sequence whose length is not a multiple of 64)
+    if (!live) continue;
 
     // S^T tiles: s[t][r] = score of query q0 + c16 with key k0 + 16t + 4g + r
     f32x4 s[4];
