@@ -125,15 +125,16 @@ using namespace vkq;
 // [Q rows | K rows] index space; both rows' loads are issued before either
 // row's reductions, doubling the bytes in flight per wave.
 constexpr int kQkRowsPerGroup = 2;
+constexpr int kQkThreads = 256;  // threads per workgroup: kQkThreads / 16 row groups
 
 template <typename PT, bool HAS_NORM, int POS>
-__global__ __launch_bounds__(256) void qk_norm_rope_rows(
+__global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
     const PT* __restrict__ qb, const PT* __restrict__ kg, const PT* __restrict__ kb,
     const float* __restrict__ pos_yx, const float* __restrict__ table, QkShape sh,
     float eps) {
   const int l = threadIdx.x & 15;
-  const uint32_t grp = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const uint32_t grp = blockIdx.x * (kQkThreads / 16u) + (threadIdx.x >> 4);
   const uint32_t total = 2u * sh.rows_per_tensor;
   float4 v[kQkRowsPerGroup];
   int py[kQkRowsPerGroup], px[kQkRowsPerGroup];
@@ -258,9 +259,9 @@ int launch_qk(vk_runtime* rt, float* q, float* k, const void* qg, const void* qb
               const QkShape& sh, float eps) {
   const long long total = 2LL * sh.rows_per_tensor;
   const long long groups = (total + kQkRowsPerGroup - 1) / kQkRowsPerGroup;
-  const long long blocks = (groups + 15) / 16;
+  const long long blocks = (groups + kQkThreads / 16 - 1) / (kQkThreads / 16);
   hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), 0, rt->stream, q, k, static_cast<const PT*>(qg),
+                     dim3(kQkThreads), 0, rt->stream, q, k, static_cast<const PT*>(qg),
                      static_cast<const PT*>(qb), static_cast<const PT*>(kg),
                      static_cast<const PT*>(kb), pos, table, sh, eps);
   return vk::check_launch("qk_norm_rope_rows");
