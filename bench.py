@@ -50,24 +50,37 @@ def log(msg):
 
 
 # ---------------------------------------------------------------- byte model
-def ln_bytes(rows):
-    return 2 * rows * D * 4 + 2 * D * 4
+class Shape:
+    """Model shape of one fused-op sequence: embed dim, heads, MLP width,
+    patch grid, block count and the first local/global alternation layer."""
+
+    def __init__(self, D, H, M, gh, gw, depth, alt):
+        self.D, self.H, self.M, self.gh, self.gw, self.depth, self.alt = D, H, M, gh, gw, depth, alt
+        self.tpv = 1 + NREG + gh * gw
 
 
-def qk_bytes(rows):
-    return 4 * H * rows * HD * 4 + 4 * HD * 4
+VITB = Shape(D, H, M, GH, GW, DEPTH, ALT)          # 504x336: 866 tokens per view
+VITL = Shape(1024, 16, 4096, 48, 72, 24, 8)        # 1008x672: 3,458 tokens
 
 
-def lsres_ln_bytes(rows):
-    return 4 * rows * D * 4 + 3 * D * 4
+def ln_bytes(rows, shape=VITB, w=4):
+    return 2 * rows * shape.D * 4 + 2 * shape.D * w
 
 
-def lsres_bytes(rows):
-    return 3 * rows * D * 4 + D * 4
+def qk_bytes(rows, shape=VITB, w=4):
+    return 4 * shape.H * rows * HD * 4 + 4 * HD * w
 
 
-def gelu_bytes(rows):
-    return 2 * rows * M * 4
+def lsres_ln_bytes(rows, shape=VITB, w=4):
+    return 4 * rows * shape.D * 4 + 3 * shape.D * w
+
+
+def lsres_bytes(rows, shape=VITB, w=4):
+    return 3 * rows * shape.D * 4 + shape.D * w
+
+
+def gelu_bytes(rows, shape=VITB):
+    return 2 * rows * shape.M * 4
 
 
 def block_plan(depth=DEPTH, alt=ALT):
@@ -88,60 +101,79 @@ def block_plan(depth=DEPTH, alt=ALT):
     return plan
 
 
-def step_bytes(rows, views, plan):
+def step_bytes(rows, views, plan, shape=VITB, w=4):
+    """Algorithmic bytes of one pass of the fused-op sequence (parameter
+    vectors of w bytes per element)."""
     import vestra_hip as vh
     total = 0
     for i, flags in enumerate(plan):
-        if i == ALT:
-            total += 2 * views * D * 4  # camera slot copies
-        if not (flags & vh.VK_BLOCK_SKIP_LN1) or i == ALT:
-            total += ln_bytes(rows)
-        total += qk_bytes(rows) + lsres_ln_bytes(rows) + gelu_bytes(rows)
-        total += lsres_ln_bytes(rows) if flags & vh.VK_BLOCK_FUSE_NEXT_LN1 else lsres_bytes(rows)
+        if i == shape.alt:
+            total += 2 * views * shape.D * 4  # camera slot copies
+        if not (flags & vh.VK_BLOCK_SKIP_LN1) or i == shape.alt:
+            total += ln_bytes(rows, shape, w)
+        total += qk_bytes(rows, shape, w) + lsres_ln_bytes(rows, shape, w) + gelu_bytes(rows, shape)
+        total += (lsres_ln_bytes(rows, shape, w) if flags & vh.VK_BLOCK_FUSE_NEXT_LN1
+                  else lsres_bytes(rows, shape, w))
     return total
 
 
 # ---------------------------------------------------------------- GPU setup
 class Model:
-    def __init__(self, rt, rng, views):
+    """The fused-op sequence of every block of `shape` over `views` views
+    (rows = views * tokens per view, view-major), with seeded parameters
+    (f32, or f16 storage with f16=True) and seeded activations resident in
+    HBM.  enqueue_block(i) issues block i exactly as the timed step does."""
+
+    def __init__(self, rt, rng, views, shape=VITB, f16=False):
         import vestra_hip as vh
-        self.rt, self.views = rt, views
-        self.rows = TPV * views
-        r = self.rows
+        self.rt, self.views, self.shape, self.f16 = rt, views, shape, f16
+        self.rows = shape.tpv * views
+        r, Dm, Mm = self.rows, shape.D, shape.M
 
         def n(*s, scale=1.0, shift=0.0):
             return (shift + scale * rng.standard_normal(s)).astype(np.float32)
 
+        pdt = np.float16 if f16 else np.float32
+        up = rt.upload_f16 if f16 else rt.upload_f32
         self.host_layers = []
         self.dev_layers = []
-        for _ in range(DEPTH):
-            h = {"norm1_gamma": n(D, scale=0.02, shift=1), "norm1_beta": n(D, scale=0.02),
+        for _ in range(shape.depth):
+            h = {"norm1_gamma": n(Dm, scale=0.02, shift=1), "norm1_beta": n(Dm, scale=0.02),
                  "qnorm_gamma": n(HD, scale=0.02, shift=1), "qnorm_beta": n(HD, scale=0.02),
                  "knorm_gamma": n(HD, scale=0.02, shift=1), "knorm_beta": n(HD, scale=0.02),
-                 "ls1": rng.uniform(0, 0.1, D).astype(np.float32),
-                 "norm2_gamma": n(D, scale=0.02, shift=1), "norm2_beta": n(D, scale=0.02),
-                 "ls2": rng.uniform(0, 0.1, D).astype(np.float32)}
+                 "ls1": rng.uniform(0, 0.1, Dm).astype(np.float32),
+                 "norm2_gamma": n(Dm, scale=0.02, shift=1), "norm2_beta": n(Dm, scale=0.02),
+                 "ls2": rng.uniform(0, 0.1, Dm).astype(np.float32)}
+            h = {k: v.astype(pdt) for k, v in h.items()}
             self.host_layers.append(h)
-            self.dev_layers.append({k: rt.upload_f32(v) for k, v in h.items()})
+            self.dev_layers.append({k: up(v) for k, v in h.items()})
         self.structs = [vh.layer_struct(**d) for d in self.dev_layers]
-        self.host_act = {"tokens": n(r, D), "q": n(r * D), "k": n(r * D), "attn_proj": n(r, D),
-                         "hidden": n(r, M), "mlp_out": n(r, D)}
-        self.camera_host = n(2 * D, scale=0.02)
+        self.host_act = {"tokens": n(r, Dm), "q": n(r * Dm), "k": n(r * Dm),
+                         "attn_proj": n(r, Dm), "hidden": n(r, Mm), "mlp_out": n(r, Dm)}
+        self.camera_host = n(2 * Dm, scale=0.02)
         self.act = {k: rt.upload_f32(v) for k, v in self.host_act.items()}
-        self.act["ln1"] = rt.alloc_f32(r * D)
-        self.act["ln2"] = rt.alloc_f32(r * D)
+        self.act["ln1"] = rt.alloc_f32(r * Dm)
+        self.act["ln2"] = rt.alloc_f32(r * Dm)
         self.act_struct = vh.activations_struct(**self.act)
         self.camera = rt.upload_f32(self.camera_host)
-        self.cfg = vh.VitConfig(embed_dim=D, num_heads=H, head_dim=HD, mlp_hidden=M,
-                                num_register=NREG, ln_eps=1e-6, qk_norm_eps=1e-5,
-                                rope_freq=100.0, rope_start=0, qknorm_start=0, alt_start=ALT)
-        self.plan = block_plan()
+        self.cfg_dict = dict(embed_dim=Dm, num_heads=shape.H, head_dim=HD, mlp_hidden=Mm,
+                             num_register=NREG, ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0,
+                             rope_start=0, qknorm_start=0, alt_start=shape.alt)
+        self.cfg = vh.VitConfig(**self.cfg_dict)
+        self.plan = block_plan(shape.depth, shape.alt)
+
+    def step_bytes(self):
+        return step_bytes(self.rows, self.views, self.plan, self.shape, 2 if self.f16 else 4)
+
+    def enqueue_block(self, i):
+        nxt = self.structs[i + 1] if i + 1 < self.shape.depth else None
+        self.rt.vit_block_fused_ops(self.cfg, i, self.structs[i], nxt, self.act_struct,
+                                    self.shape.gh, self.shape.gw, self.views, self.camera,
+                                    self.plan[i])
 
     def enqueue_step(self):
-        for i, flags in enumerate(self.plan):
-            nxt = self.structs[i + 1] if i + 1 < DEPTH else None
-            self.rt.vit_block_fused_ops(self.cfg, i, self.structs[i], nxt, self.act_struct, GH, GW,
-                                        self.views, self.camera, flags)
+        for i in range(self.shape.depth):
+            self.enqueue_block(i)
 
 
 def time_loop(rt, fn, iters):
@@ -480,25 +512,6 @@ L_D, L_H, L_M, L_GH, L_GW, L_DEPTH, L_ALT = 1024, 16, 4096, 48, 72, 24, 8
 L_TPV = 1 + NREG + L_GH * L_GW  # 3458
 
 
-def vitl_fused_bytes(rows, plan):
-    """Algorithmic bytes of the ViT-L fused-op sequence, f16 parameter vectors."""
-    import vestra_hip as vh
-    w = 2
-    ln = 2 * rows * L_D * 4 + 2 * L_D * w
-    qk = 4 * L_H * rows * HD * 4 + 4 * HD * w
-    lsln = 4 * rows * L_D * 4 + 3 * L_D * w
-    ls = 3 * rows * L_D * 4 + L_D * w
-    gelu = 2 * rows * L_M * 4
-    total = 0
-    for i, flags in enumerate(plan):
-        if i == L_ALT:
-            total += 2 * L_D * 4
-        if not (flags & vh.VK_BLOCK_SKIP_LN1) or i == L_ALT:
-            total += ln
-        total += qk + lsln + gelu + (lsln if flags & vh.VK_BLOCK_FUSE_NEXT_LN1 else ls)
-    return total
-
-
 def vitl_timing(rt, rng, reps=3):
     """The ViT-L 1008x672 configuration with F16-stored weights: the 24-block
     fused-op sequence (parameter vectors in f16, widened in registers) and the
@@ -531,32 +544,17 @@ def vitl_timing(rt, rng, reps=3):
            "alt_start": L_ALT}
 
     # fused-op sequence (projections / attention outputs are seeded tensors)
-    lsv = [{"ls1": h16(rng.uniform(0, 0.1, L_D).astype(np.float32)),
-            "ls2": h16(rng.uniform(0, 0.1, L_D).astype(np.float32))} for _ in range(L_DEPTH)]
-    structs = [vh.layer_struct(**v, **l) for v, l in zip(vecs, lsv)]
-    act = {"tokens": rt.upload_f32(n(rows, L_D)), "q": rt.upload_f32(n(rows * L_D)),
-           "k": rt.upload_f32(n(rows * L_D)), "attn_proj": rt.upload_f32(n(rows, L_D)),
-           "hidden": rt.upload_f32(n(rows, L_M)), "mlp_out": rt.upload_f32(n(rows, L_D)),
-           "ln1": rt.alloc_f32(rows * L_D), "ln2": rt.alloc_f32(rows * L_D)}
-    act_struct = vh.activations_struct(**act)
-    plan = block_plan(L_DEPTH, L_ALT)
-
-    def fused_step():
-        for i, flags in enumerate(plan):
-            nxt = structs[i + 1] if i + 1 < L_DEPTH else None
-            rt.vit_block_fused_ops(cfg, i, structs[i], nxt, act_struct, L_GH, L_GW, 1, camera,
-                                   flags)
-
-    fused_step()
-    graph = capture(rt, fused_step)
+    model = Model(rt, rng, views=1, shape=VITL, f16=True)
+    model.enqueue_step()
+    graph = capture(rt, model.enqueue_step)
     graph.launch()
     ms = statistics.median(time_loop(rt, graph.launch, 1) for _ in range(reps * 3))
-    nbytes = vitl_fused_bytes(rows, plan)
+    nbytes = model.step_bytes()
     out["fused_ops"] = {"us_per_block": round(ms * 1e3 / L_DEPTH, 2),
                         "bytes_per_pass": int(nbytes),
                         "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                         "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    del graph, act, act_struct
+    del graph, model
 
     # whole blocks, weights uploaded as F16
     keep, blocks = [], []
@@ -815,7 +813,7 @@ def main():
         return
     log(f"device has {rt.cu_count()} CUs; building 12-view workload ({TPV * 12} rows)")
     model = Model(rt, rng, views=12)
-    nbytes = step_bytes(model.rows, 12, model.plan)
+    nbytes = model.step_bytes()
 
     model.enqueue_step()  # builds the RoPE table before capture
     step_graph = capture(rt, model.enqueue_step)
@@ -836,7 +834,7 @@ def main():
     rt.synchronize()
     reps = max(20, args.steps * 5)
     ms_single = time_loop(rt, graph.launch, reps)
-    single_bytes = step_bytes(single.rows, 1, single.plan)
+    single_bytes = single.step_bytes()
     log(f"single image: {ms_single * 1e3 / DEPTH:.2f} us per block")
     del single, graph
 

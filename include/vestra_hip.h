@@ -22,7 +22,8 @@
  *    vk_event_elapsed_ms block.  A runtime must not be used from two host
  *    threads at once without external locking; separate runtimes are
  *    independent.
- *  - Tensors are flat, contiguous, typed device buffers (f32, f16 or u8).
+ *  - Tensors are flat, contiguous, typed device buffers (f32, f16, u8, or
+ *    i32 / i64 for RoPE positions).
  *    Creators allocate; every creator has a matching destroy.  In-place
  *    operations take the tensor handle they modify; the reference's
  *    "consume and return the token tensor" (vit_block.rs:489-499,563) is
@@ -42,7 +43,7 @@
 extern "C" {
 #endif
 
-#define VK_ABI_VERSION 1
+#define VK_ABI_VERSION 2
 
 typedef enum vk_status {
   VK_OK = 0,
@@ -52,7 +53,15 @@ typedef enum vk_status {
   VK_ERR_OOM = -4          /* device allocation failed                      */
 } vk_status;
 
-typedef enum vk_dtype { VK_F32 = 0, VK_F16 = 1, VK_U8 = 2 } vk_dtype;
+/* VK_I32 / VK_I64: integer RoPE positions (the reference's CPU kernels take
+ * `&[i64]` positions, vit_block.rs:911-924, 944-948). */
+typedef enum vk_dtype {
+  VK_F32 = 0,
+  VK_F16 = 1,
+  VK_U8 = 2,
+  VK_I32 = 3,
+  VK_I64 = 4
+} vk_dtype;
 
 typedef struct vk_runtime vk_runtime;
 typedef struct vk_tensor vk_tensor;
@@ -79,8 +88,8 @@ int vk_runtime_create(int device, vk_runtime** out);
 /* Waits for the runtime's queued work and retires the handle: it takes no
  * new work (calls on it fail).  Tensors, linears and events created on it
  * may still be destroyed afterwards; the stream and the runtime's own
- * buffers are released with the last of them.  Graphs captured on it must
- * not be launched afterwards. */
+ * buffers are released with the last of them.  Launching a graph captured
+ * on it fails afterwards (VK_ERR_INVALID). */
 int vk_runtime_destroy(vk_runtime* rt);
 /* Blocks until all work queued on the runtime's stream has finished. */
 int vk_runtime_synchronize(vk_runtime* rt);
@@ -108,6 +117,10 @@ void* vk_tensor_device_ptr(const vk_tensor* t);
 int vk_upload_f32(vk_runtime* rt, const float* host, size_t len, vk_tensor** out);
 int vk_upload_f16(vk_runtime* rt, const uint16_t* host, size_t len, vk_tensor** out);
 int vk_upload_u8(vk_runtime* rt, const uint8_t* host, size_t len, vk_tensor** out);
+/* Integer RoPE positions [rows*2] (y, x) for vk_qk_norm_rope_mode_f32 and
+ * vk_rope2d_f32.  Synchronous. */
+int vk_upload_i32(vk_runtime* rt, const int32_t* host, size_t len, vk_tensor** out);
+int vk_upload_i64(vk_runtime* rt, const int64_t* host, size_t len, vk_tensor** out);
 /* Host -> existing tensor (len must equal the tensor length). Synchronous. */
 int vk_write_f32(vk_runtime* rt, vk_tensor* t, const float* host, size_t len);
 int vk_write_u8(vk_runtime* rt, vk_tensor* t, const uint8_t* host, size_t len);
@@ -177,6 +190,21 @@ int vk_layerscale_residual_layernorm_f32(vk_runtime* rt, vk_tensor* x,
                                          size_t cols, float eps,
                                          vk_tensor* ln_out);
 
+/* 2D RoPE convention, `rope_mode` = one pairing | one exponent flag.
+ * Every row of head_dim 64 splits into a y half (elements 0..31, rotated by
+ * the row's y coordinate) and an x half (32..63, rotated by x), with the
+ * frequency base `freq` (100 for DA3, config.rs:375).  The pairing inside a
+ * half and the frequency exponent are fixed only inside the reference's
+ * kernel crate (vestra-kernels, absent from its tree; its value test needs
+ * absent dumps, crates/da-engine/tests/kernel_rope_parity.rs:4-19), so both
+ * are selectable.  The default (0) is the rotation of Depth-Anything-3's
+ * RotaryPositionEmbedding2D. */
+#define VK_ROPE_ROTATE_HALF 0u /* pairs (j, j+16) of each half, j < 16        */
+#define VK_ROPE_INTERLEAVED 1u /* pairs (2i, 2i+1) of each half, i < 16        */
+#define VK_ROPE_EXP_HALF 0u    /* pair j turns by p * freq^(-2j/32)            */
+#define VK_ROPE_EXP_HEAD 2u    /* pair j turns by p * freq^(-2j/64)            */
+#define VK_ROPE_DEFAULT 0u
+
 /* CudaRuntime::qk_norm_rope_f32_da3_base(q, k, q_gamma, q_beta, k_gamma,
  * k_beta, positions, heads, rows, freq, eps) (vit_block.rs:343-357, 543-557):
  * in place on head-major q and k [heads, rows, 64]: LayerNorm over each
@@ -188,6 +216,26 @@ int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
                         const vk_tensor* k_gamma, const vk_tensor* k_beta,
                         const vk_tensor* positions, size_t heads, size_t rows,
                         float freq, float eps);
+/* The same with an explicit RoPE convention (VK_ROPE_* flags; 0 gives
+ * vk_qk_norm_rope_f32) and positions of dtype f32 (the CUDA runtime's
+ * device encoding, truncated toward zero), i32 or i64 (the CPU kernel's
+ * `&[i64]`, qk_norm_rope_f32_da3_base at vit_block.rs:911-924; values must
+ * fit in 32 bits).  Positions outside the runtime's cos/sin table (negative
+ * or above 1023 and every grid coordinate seen so far) take the same
+ * f32 angle and double-precision trig on the device. */
+int vk_qk_norm_rope_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                             const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                             const vk_tensor* k_gamma, const vk_tensor* k_beta,
+                             const vk_tensor* positions, size_t heads,
+                             size_t rows, float freq, float eps,
+                             unsigned rope_mode);
+/* vestra_kernels::rope2d(x, heads, n, head_dim, pos_yx, freq)
+ * (vit_block.rs:944-948; cpu_backend.rs:286-295): the 2D rotation alone, in
+ * place on one head-major tensor x [heads, rows, 64], positions [rows*2]
+ * (y, x) of dtype f32, i32 or i64, convention `rope_mode`. */
+int vk_rope2d_f32(vk_runtime* rt, vk_tensor* x, const vk_tensor* positions,
+                  size_t heads, size_t rows, size_t head_dim, float freq,
+                  unsigned rope_mode);
 
 /* Layouts of q/k for the grid form below. */
 typedef enum vk_qk_layout {
@@ -213,6 +261,16 @@ int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
                              size_t gh, size_t gw, size_t view_count,
                              int global, vk_qk_layout layout, float freq,
                              float eps);
+/* The grid form with an explicit RoPE convention (0 gives the call above). */
+int vk_qk_norm_rope_grid_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                                  const vk_tensor* q_gamma,
+                                  const vk_tensor* q_beta,
+                                  const vk_tensor* k_gamma,
+                                  const vk_tensor* k_beta, size_t heads,
+                                  size_t head_dim, size_t n_special,
+                                  size_t gh, size_t gw, size_t view_count,
+                                  int global, vk_qk_layout layout,
+                                  float freq, float eps, unsigned rope_mode);
 
 /* Device positions tensor [rows*2] f32, as built on the host at
  * vit_block.rs:512-526 (for callers of vk_qk_norm_rope_f32). */
@@ -345,6 +403,13 @@ int vk_linear_run_qkv_hnd_norm_rope_f32(
     const vk_tensor* q_gamma, const vk_tensor* q_beta, const vk_tensor* k_gamma,
     const vk_tensor* k_beta, size_t n_special, size_t gh, size_t gw,
     size_t view_count, int global, float freq, float eps);
+/* The same with an explicit RoPE convention (0 gives the call above). */
+int vk_linear_run_qkv_hnd_norm_rope_mode_f32(
+    vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
+    size_t heads, size_t head_dim, vk_tensor* q, vk_tensor* k, vk_tensor* v,
+    const vk_tensor* q_gamma, const vk_tensor* q_beta, const vk_tensor* k_gamma,
+    const vk_tensor* k_beta, size_t n_special, size_t gh, size_t gw,
+    size_t view_count, int global, float freq, float eps, unsigned rope_mode);
 /* The output projection reading the head-major attention output
  * [heads, rows, 64] directly (in_features = heads*64): bit-identical to
  * vk_hnd_to_token_into_f32 followed by vk_linear_run_into_f32 /
@@ -496,6 +561,7 @@ typedef struct vk_vit_config {
   int rope_start;       /* first layer with RoPE, -1 never          */
   int qknorm_start;     /* first layer with Q/K-norm, -1 never      */
   int alt_start;        /* first local/global alternation layer     */
+  unsigned rope_mode;   /* VK_ROPE_* convention, 0 = default        */
 } vk_vit_config;
 
 /* Per-layer parameters (the vit.blk.{i}.* tensors of vit_block.rs:30-50).
@@ -643,7 +709,14 @@ int vk_event_elapsed_ms(vk_event* start, vk_event* stop, float* ms);
  * tables grow only outside capture, so a sequence is run once eagerly
  * before it is captured; a call that would grow them during capture fails
  * with an error and enqueues nothing.  Buffers they replace stay valid for
- * graphs captured earlier until the runtime is released. */
+ * graphs captured earlier until the runtime is released.  Device copies
+ * (segment copies, the camera-slot write) are kernels, so a captured
+ * sequence holds kernel nodes only.
+ * Lifetime: a graph keeps its runtime alive and launches only on the
+ * runtime it was captured on (another runtime, or one already passed to
+ * vk_runtime_destroy, gives VK_ERR_INVALID).  vk_graph_destroy waits for
+ * the runtime's stream before releasing the graph.  The tensors and linears
+ * that the captured calls named must outlive every launch of the graph. */
 int vk_graph_begin_capture(vk_runtime* rt);
 int vk_graph_end_capture(vk_runtime* rt, vk_graph** out);
 int vk_graph_launch(vk_runtime* rt, vk_graph* g);

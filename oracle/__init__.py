@@ -49,9 +49,12 @@ _SIGS = {
     "ora_layerscale_residual_w16": ([_vp, _vp, _vp, _sz, _sz], None),
     "ora_rope_positions": ([_vp, _sz, _sz, _sz, _sz, _i], None),
     "ora_rope_inv_freq": ([_vp, _sz, _f], None),
+    "ora_rope_inv_freq_mode": ([_vp, _sz, _f, C.c_uint], None),
     "ora_rope2d_f32": ([_vp, _sz, _sz, _sz, _vp, _f], None),
+    "ora_rope2d_mode_f32": ([_vp, _sz, _sz, _sz, _vp, _f, C.c_uint], None),
     "ora_qk_norm_rope_f32": ([_vp] * 7 + [_sz, _sz, _sz, _f, _f], None),
-    "ora_qk_norm_rope_w16": ([_vp] * 7 + [_sz, _sz, _sz, _f, _f], None),
+    "ora_qk_norm_rope_mode_f32": ([_vp] * 7 + [_sz, _sz, _sz, _f, _f, C.c_uint], None),
+    "ora_qk_norm_rope_w16": ([_vp] * 7 + [_sz, _sz, _sz, _f, _f, C.c_uint], None),
     "ora_normalize_u8_hwc": ([_vp, _vp, _sz, _sz, _vp, _vp], None),
     "ora_patchify_nchw": ([_vp, _vp, _sz, _sz, _sz, _sz], None),
     "ora_linear_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _sz], None),
@@ -168,33 +171,41 @@ def rope_positions(n_special: int, gh: int, gw: int, view_count: int, global_lay
     return out
 
 
-def rope_inv_freq(head_dim: int, base: float = 100.0) -> np.ndarray:
+# RoPE convention flags (the device ABI's VK_ROPE_* bits); 0 is the default:
+# rotate-half pairing (i, i+16) and exponent 2j/32 for head_dim 64
+ROPE_INTERLEAVED = 1
+ROPE_EXP_HEAD = 2
+ROPE_MODES = (0, ROPE_INTERLEAVED, ROPE_EXP_HEAD, ROPE_INTERLEAVED | ROPE_EXP_HEAD)
+
+
+def rope_inv_freq(head_dim: int, base: float = 100.0, mode: int = 0) -> np.ndarray:
     out = np.empty(head_dim // 4, np.float32)
-    lib.ora_rope_inv_freq(_p(out), head_dim, base)
+    lib.ora_rope_inv_freq_mode(_p(out), head_dim, base, mode)
     return out
 
 
-def rope2d(x, heads: int, n: int, head_dim: int, pos_yx, base: float = 100.0) -> np.ndarray:
+def rope2d(x, heads: int, n: int, head_dim: int, pos_yx, base: float = 100.0,
+           mode: int = 0) -> np.ndarray:
     """vestra_kernels::rope2d on [heads, n, head_dim] (returns a copy)."""
     y = _f32(x).copy()
     pos = np.ascontiguousarray(pos_yx, dtype=np.int64)
-    lib.ora_rope2d_f32(_p(y), heads, n, head_dim, _p(pos), base)
+    lib.ora_rope2d_mode_f32(_p(y), heads, n, head_dim, _p(pos), base, mode)
     return y
 
 
 def qk_norm_rope(q, k, qg, qb, kg, kb, pos_yx, heads: int, n: int, head_dim: int = 64,
-                 base: float = 100.0, eps: float = 1e-5):
+                 base: float = 100.0, eps: float = 1e-5, mode: int = 0):
     """qk_norm_rope_f32_da3_base (vit_block.rs:911-924), returns (q, k) copies."""
     qo, ko = _f32(q).copy(), _f32(k).copy()
     pos = _f32(pos_yx)
     if np.asarray(qg).dtype == np.float16:
         args = [f16_bits(a) for a in (qg, qb, kg, kb)]
         lib.ora_qk_norm_rope_w16(_p(qo), _p(ko), *[_p(a) for a in args], _p(pos), heads, n,
-                                 head_dim, base, eps)
+                                 head_dim, base, eps, mode)
     else:
         args = [_f32(a) for a in (qg, qb, kg, kb)]
-        lib.ora_qk_norm_rope_f32(_p(qo), _p(ko), *[_p(a) for a in args], _p(pos), heads, n,
-                                 head_dim, base, eps)
+        lib.ora_qk_norm_rope_mode_f32(_p(qo), _p(ko), *[_p(a) for a in args], _p(pos), heads,
+                                      n, head_dim, base, eps, mode)
     return qo, ko
 
 
@@ -336,8 +347,9 @@ def block_fused_ops(tokens, q, k, attn_proj, hidden, mlp_out, layer: dict, cfg: 
                 kb_[...] = layernorm(kb_, layer["knorm_gamma"], layer["knorm_beta"], cfg["qk_norm_eps"])
             if use_rope:
                 pi = p.astype(np.int64)
-                qb_[...] = rope2d(qb_, H, n, hd, pi, cfg["rope_freq"]).reshape(qb_.shape)
-                kb_[...] = rope2d(kb_, H, n, hd, pi, cfg["rope_freq"]).reshape(kb_.shape)
+                mode = cfg.get("rope_mode", 0)
+                qb_[...] = rope2d(qb_, H, n, hd, pi, cfg["rope_freq"], mode).reshape(qb_.shape)
+                kb_[...] = rope2d(kb_, H, n, hd, pi, cfg["rope_freq"], mode).reshape(kb_.shape)
     x = layerscale_residual(x, _f32(attn_proj).reshape(rows, D), layer.get("ls1"))
     ln2 = layernorm(x, layer["norm2_gamma"], layer["norm2_beta"], cfg["ln_eps"])
     hid = gelu(hidden)
@@ -382,8 +394,9 @@ def block_forward(tokens, params: dict, cfg: dict, layer_idx: int, gh: int, gw: 
         k = layernorm(k, params["knorm_gamma"], params["knorm_beta"], cfg["qk_norm_eps"])
     if use_rope:
         pos = rope_positions(n_special, gh, gw, view_count, glob).astype(np.int64)
-        q = rope2d(q, H, rows, hd, pos, cfg["rope_freq"]).reshape(H, rows, hd)
-        k = rope2d(k, H, rows, hd, pos, cfg["rope_freq"]).reshape(H, rows, hd)
+        mode = cfg.get("rope_mode", 0)
+        q = rope2d(q, H, rows, hd, pos, cfg["rope_freq"], mode).reshape(H, rows, hd)
+        k = rope2d(k, H, rows, hd, pos, cfg["rope_freq"], mode).reshape(H, rows, hd)
     if glob:
         attn = attention(q, k, v, H, rows, hd)
     else:

@@ -25,12 +25,16 @@
  *                    the reference's per-view special-token layout.
  *   rope2d rotation  PARITY UNPINNED against the reference: the pairing and
  *                    frequency exponent live only in the absent
- *                    vestra-kernels crate and absent dumps.  The convention of
- *                    the upstream DA3 RotaryPositionEmbedding2D is restated
- *                    (rotate-half pairs (i, i+d/4) inside each half,
- *                    inv_freq_j = base^(-2j/(d/2))); tests pin it by
- *                    invariants (norm preservation, identity at (0,0),
- *                    relative-position property, recovered angles).
+ *                    vestra-kernels crate and absent dumps.  Both are
+ *                    selectable (mode flags as the device ABI's VK_ROPE_*):
+ *                    pairing rotate-half (i, i+d/4) inside each half (the
+ *                    upstream DA3 RotaryPositionEmbedding2D, the default) or
+ *                    interleaved (2i, 2i+1); exponent inv_freq_j =
+ *                    base^(-2j/(d/2)) (default) or base^(-2j/d).  Tests pin
+ *                    each form to the mathematics: complex-multiplication
+ *                    twins, closed-form angles (j = 0 turns by p radians,
+ *                    base 100 at j = 8 by p/10 or p/sqrt(10)), norm
+ *                    preservation, identity at (0,0), relative positions.
  *   patch embed      pinned: patch_embed.rs:280-339 known answers (10, 18,
  *                    42, 50; bias broadcast), preprocess.rs:549-583
  *                    normalisation, float64 GEMM brute force.
@@ -244,16 +248,23 @@ void ora_rope_positions(float* pos_yx, size_t n_special, size_t gh, size_t gw,
 }
 
 /* Inverse frequencies of one rotary half of width half = head_dim/2:
- * inv_freq_j = 1 / base^((2j)/half) for j < half/2, each step in f32
- * (RotaryPositionEmbedding2D of upstream Depth-Anything-3, referenced by the
- * reference's plan docs/plans/2026-07-18-rust-engine-v1.md:1290: "head_dim in
- * two halves y/x, each rotary over its coordinate", frequency 100). */
-void ora_rope_inv_freq(float* inv_freq, size_t head_dim, float base) {
+ * inv_freq_j = 1 / base^((2j)/denom) for j < half/2, each step in f32, with
+ * denom = half (mode without ORA_ROPE_EXP_HEAD: RotaryPositionEmbedding2D
+ * of upstream Depth-Anything-3, referenced by the reference's plan
+ * docs/plans/2026-07-18-rust-engine-v1.md:1290: "head_dim in two halves y/x,
+ * each rotary over its coordinate", frequency 100) or denom = head_dim
+ * (ORA_ROPE_EXP_HEAD). */
+void ora_rope_inv_freq_mode(float* inv_freq, size_t head_dim, float base, unsigned mode) {
   const size_t half = head_dim / 2;
+  const float denom = (float)((mode & ORA_ROPE_EXP_HEAD) ? head_dim : half);
   for (size_t j = 0; j < half / 2; ++j) {
-    const float e = (float)(2 * j) / (float)half;
+    const float e = (float)(2 * j) / denom;
     inv_freq[j] = 1.0f / powf(base, e);
   }
+}
+
+void ora_rope_inv_freq(float* inv_freq, size_t head_dim, float base) {
+  ora_rope_inv_freq_mode(inv_freq, head_dim, base, 0);
 }
 
 /* cos/sin of angle = (float)pos * inv_freq (f32 product), evaluated in
@@ -264,22 +275,26 @@ static void rope_cs(float pos, float inv_freq, float* c, float* s) {
   *s = (float)sin((double)angle);
 }
 
-/* Rotate one half (width hd2) by coordinate p: rotate-half pairing
- * out[i] = x[i]*cos_i - x[i+q]*sin_i, out[i+q] = x[i+q]*cos_i + x[i]*sin_i,
- * q = hd2/2, each product rounded then added (no FMA). */
-static void rope_half(float* x, size_t hd2, float p, const float* inv_freq) {
+/* Rotate one half (width hd2) by coordinate p.  Pair i (i < hd2/2) is
+ * (x[i], x[i+hd2/2]) with rotate-half pairing, (x[2i], x[2i+1]) with
+ * ORA_ROPE_INTERLEAVED; a pair (a, b) becomes (a*cos_i - b*sin_i,
+ * b*cos_i + a*sin_i), each product rounded then added (no FMA). */
+static void rope_half(float* x, size_t hd2, float p, const float* inv_freq, unsigned mode) {
   const size_t q = hd2 / 2;
+  const int inter = (mode & ORA_ROPE_INTERLEAVED) != 0;
   for (size_t i = 0; i < q; ++i) {
     float c, s;
     rope_cs(p, inv_freq[i], &c, &s);
-    const float a = x[i];
-    const float b = x[i + q];
+    const size_t ia = inter ? 2 * i : i;
+    const size_t ib = inter ? 2 * i + 1 : i + q;
+    const float a = x[ia];
+    const float b = x[ib];
     const float ac = a * c;
     const float nbs = (-b) * s;
     const float bc = b * c;
     const float as = a * s;
-    x[i] = ac + nbs;
-    x[i + q] = bc + as;
+    x[ia] = ac + nbs;
+    x[ib] = bc + as;
   }
 }
 
@@ -287,19 +302,24 @@ static void rope_half(float* x, size_t hd2, float p, const float* inv_freq) {
  * (interface docs/plans/2026-07-18-rust-engine-v1.md:1259; call site
  * crates/da-engine/src/vit_block.rs:944-948).  First half rotated by y,
  * second half by x. */
-void ora_rope2d_f32(float* x, size_t heads, size_t n, size_t head_dim,
-                    const int64_t* pos_yx, float base) {
+void ora_rope2d_mode_f32(float* x, size_t heads, size_t n, size_t head_dim,
+                         const int64_t* pos_yx, float base, unsigned mode) {
   float inv_freq[512];
-  ora_rope_inv_freq(inv_freq, head_dim, base);
+  ora_rope_inv_freq_mode(inv_freq, head_dim, base, mode);
   const size_t half = head_dim / 2;
   long hr;
 #pragma omp parallel for schedule(static)
   for (hr = 0; hr < (long)(heads * n); ++hr) {
     const size_t t = (size_t)hr % n;
     float* row = x + (size_t)hr * head_dim;
-    rope_half(row, half, (float)pos_yx[2 * t], inv_freq);
-    rope_half(row + half, half, (float)pos_yx[2 * t + 1], inv_freq);
+    rope_half(row, half, (float)pos_yx[2 * t], inv_freq, mode);
+    rope_half(row + half, half, (float)pos_yx[2 * t + 1], inv_freq, mode);
   }
+}
+
+void ora_rope2d_f32(float* x, size_t heads, size_t n, size_t head_dim,
+                    const int64_t* pos_yx, float base) {
+  ora_rope2d_mode_f32(x, heads, n, head_dim, pos_yx, base, 0);
 }
 
 /* qk_norm_rope_f32_da3_base: per (head, token) row LayerNorm over head_dim
@@ -308,13 +328,13 @@ void ora_rope2d_f32(float* x, size_t heads, size_t n, size_t head_dim,
  * fused call vit_block.rs:911-924; CUDA vit_block.rs:543-557).  Positions are
  * the reference's f32 device encoding, truncated to integers like the CPU
  * caller's `value as i64` (vit_block.rs:912). */
-void ora_qk_norm_rope_f32(float* q, float* k, const float* q_gamma,
-                          const float* q_beta, const float* k_gamma,
-                          const float* k_beta, const float* pos_yx,
-                          size_t heads, size_t n, size_t head_dim, float base,
-                          float eps) {
+void ora_qk_norm_rope_mode_f32(float* q, float* k, const float* q_gamma,
+                               const float* q_beta, const float* k_gamma,
+                               const float* k_beta, const float* pos_yx,
+                               size_t heads, size_t n, size_t head_dim,
+                               float base, float eps, unsigned mode) {
   float inv_freq[512];
-  ora_rope_inv_freq(inv_freq, head_dim, base);
+  ora_rope_inv_freq_mode(inv_freq, head_dim, base, mode);
   const size_t half = head_dim / 2;
   long hr;
 #pragma omp parallel for schedule(static)
@@ -326,23 +346,33 @@ void ora_qk_norm_rope_f32(float* q, float* k, const float* q_gamma,
     float* kr = k + (size_t)hr * head_dim;
     ln_row(qr, qr, head_dim, q_gamma, q_beta, eps);
     ln_row(kr, kr, head_dim, k_gamma, k_beta, eps);
-    rope_half(qr, half, py, inv_freq);
-    rope_half(qr + half, half, px, inv_freq);
-    rope_half(kr, half, py, inv_freq);
-    rope_half(kr + half, half, px, inv_freq);
+    rope_half(qr, half, py, inv_freq, mode);
+    rope_half(qr + half, half, px, inv_freq, mode);
+    rope_half(kr, half, py, inv_freq, mode);
+    rope_half(kr + half, half, px, inv_freq, mode);
   }
+}
+
+void ora_qk_norm_rope_f32(float* q, float* k, const float* q_gamma,
+                          const float* q_beta, const float* k_gamma,
+                          const float* k_beta, const float* pos_yx,
+                          size_t heads, size_t n, size_t head_dim, float base,
+                          float eps) {
+  ora_qk_norm_rope_mode_f32(q, k, q_gamma, q_beta, k_gamma, k_beta, pos_yx, heads,
+                            n, head_dim, base, eps, 0);
 }
 
 void ora_qk_norm_rope_w16(float* q, float* k, const uint16_t* q_gamma,
                           const uint16_t* q_beta, const uint16_t* k_gamma,
                           const uint16_t* k_beta, const float* pos_yx,
                           size_t heads, size_t n, size_t head_dim, float base,
-                          float eps) {
+                          float eps, unsigned mode) {
   float* qg = widen(q_gamma, head_dim);
   float* qb = widen(q_beta, head_dim);
   float* kg = widen(k_gamma, head_dim);
   float* kb = widen(k_beta, head_dim);
-  ora_qk_norm_rope_f32(q, k, qg, qb, kg, kb, pos_yx, heads, n, head_dim, base, eps);
+  ora_qk_norm_rope_mode_f32(q, k, qg, qb, kg, kb, pos_yx, heads, n, head_dim, base,
+                            eps, mode);
   free(qg);
   free(qb);
   free(kg);

@@ -59,20 +59,33 @@ void ora_layerscale_residual_w16(float* x, const float* y, const uint16_t* gamma
 /* positions [rows*2] (y, x) as f32, special tokens (0,0) per view */
 void ora_rope_positions(float* pos_yx, size_t n_special, size_t gh, size_t gw,
                         size_t view_count, int global);
+/* RoPE convention flags (the same bits as the device ABI's VK_ROPE_*):
+ * pairing (i, i+d/4) inside each half unless ORA_ROPE_INTERLEAVED (2i, 2i+1);
+ * exponent 2j/(d/2) unless ORA_ROPE_EXP_HEAD (2j/d).  0 is the default. */
+#define ORA_ROPE_INTERLEAVED 1u
+#define ORA_ROPE_EXP_HEAD 2u
 /* inverse frequency and angle tables of the 2D rotary embedding */
 void ora_rope_inv_freq(float* inv_freq, size_t head_dim, float base);
+void ora_rope_inv_freq_mode(float* inv_freq, size_t head_dim, float base, unsigned mode);
 void ora_rope2d_f32(float* x, size_t heads, size_t n, size_t head_dim,
                     const int64_t* pos_yx, float base);
+void ora_rope2d_mode_f32(float* x, size_t heads, size_t n, size_t head_dim,
+                         const int64_t* pos_yx, float base, unsigned mode);
 void ora_qk_norm_rope_f32(float* q, float* k, const float* q_gamma,
                           const float* q_beta, const float* k_gamma,
                           const float* k_beta, const float* pos_yx,
                           size_t heads, size_t n, size_t head_dim, float base,
                           float eps);
+void ora_qk_norm_rope_mode_f32(float* q, float* k, const float* q_gamma,
+                               const float* q_beta, const float* k_gamma,
+                               const float* k_beta, const float* pos_yx,
+                               size_t heads, size_t n, size_t head_dim,
+                               float base, float eps, unsigned mode);
 void ora_qk_norm_rope_w16(float* q, float* k, const uint16_t* q_gamma,
                           const uint16_t* q_beta, const uint16_t* k_gamma,
                           const uint16_t* k_beta, const float* pos_yx,
                           size_t heads, size_t n, size_t head_dim, float base,
-                          float eps);
+                          float eps, unsigned mode);
 
 /* ---- patch embedding ---- */
 void ora_normalize_u8_hwc(const uint8_t* img, float* chw, size_t h, size_t w,

@@ -37,10 +37,10 @@ def make_params(rng, D, M, with_qkn=True, with_ls=True):
     return p
 
 
-def config(D, H, M, nreg=1, alt=4, rope_start=0, qknorm_start=0):
+def config(D, H, M, nreg=1, alt=4, rope_start=0, qknorm_start=0, rope_mode=0):
     return dict(embed_dim=D, num_heads=H, head_dim=64, mlp_hidden=M, num_register=nreg,
                 ln_eps=1e-6, qk_norm_eps=1e-5, rope_freq=100.0, rope_start=rope_start,
-                qknorm_start=qknorm_start, alt_start=alt)
+                qknorm_start=qknorm_start, alt_start=alt, rope_mode=rope_mode)
 
 
 def is_global(cfg, layer):
@@ -63,17 +63,18 @@ def _gelu64(x):
     return 0.5 * x * (1.0 + erf)
 
 
-def _rope64(x, pos, inv_freq):
+def _rope64(x, pos, inv_freq, mode=0):
+    # pairs (j, j+16) of each half, or (2j, 2j+1) with the interleaved flag
+    first = np.arange(16) * 2 if mode & oracle.ROPE_INTERLEAVED else np.arange(16)
+    second = first + 1 if mode & oracle.ROPE_INTERLEAVED else first + 16
     out = x.copy()
-    for half, coord in ((slice(0, 32), 0), (slice(32, 64), 1)):
+    for base, coord in ((0, 0), (32, 1)):
         p = pos[:, coord].astype(np.float32)
         ang = (p[:, None] * inv_freq[None, :]).astype(np.float32).astype(np.float64)
         c, s = np.cos(ang), np.sin(ang)
-        a, b = x[..., half][..., :16], x[..., half][..., 16:]
-        o = out[..., half]
-        o[..., :16] = a * c - b * s
-        o[..., 16:] = b * c + a * s
-        out[..., half] = o
+        a, b = x[..., base + first], x[..., base + second]
+        out[..., base + first] = a * c - b * s
+        out[..., base + second] = b * c + a * s
     return out
 
 
@@ -103,8 +104,9 @@ def block_f64(tokens, p, cfg, layer, gh, gw, views, camera=None):
         k = _ln64(k, f["knorm_gamma"], f["knorm_beta"], cfg["qk_norm_eps"])
     if cfg["rope_start"] >= 0 and layer >= cfg["rope_start"]:
         pos = oracle.rope_positions(ns, gh, gw, views, glob)
-        inv = oracle.rope_inv_freq(64, cfg["rope_freq"])
-        q, k = _rope64(q, pos, inv), _rope64(k, pos, inv)
+        mode = cfg.get("rope_mode", 0)
+        inv = oracle.rope_inv_freq(64, cfg["rope_freq"], mode)
+        q, k = _rope64(q, pos, inv, mode), _rope64(k, pos, inv, mode)
     if glob:
         attn = _attn64(q, k, v)
     else:

@@ -28,7 +28,8 @@ def test_header_declares_the_runtime_surface():
                      "vk_qk_norm_rope_f32", "vk_patchify_nchw_f32", "vk_linear_prepare_f32",
                      "vk_linear_run_f32", "vk_prepend_cls_add_pos_f32",
                      "vk_pos_embed_bicubic_f32", "vk_patch_embed_u8",
-                     "vk_vit_block_fused_ops"):
+                     "vk_vit_block_fused_ops", "vk_qk_norm_rope_mode_f32", "vk_rope2d_f32",
+                     "vk_upload_i32", "vk_upload_i64"):
         assert required in names, required
 
 
@@ -44,7 +45,7 @@ def test_python_mirror_binds_every_declared_symbol():
     import vestra_hip
     missing = [n for n in declared_functions() if n not in vestra_hip._SIGS]
     assert not missing, missing
-    assert vestra_hip.lib.vk_abi_version() == 1
+    assert vestra_hip.lib.vk_abi_version() == 2
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="libvestra_hip.so not built")

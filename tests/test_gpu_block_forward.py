@@ -73,7 +73,8 @@ def unfused_block(rt, dev, cfg, layer, tokens, gh, gw, views, camera):
         g = [dev.vec[n] if use_qkn else None
              for n in ("qnorm_gamma", "qnorm_beta", "knorm_gamma", "knorm_beta")]
         rt.qk_norm_rope_grid_f32(q, k, *g, H, 64, ns, gh, gw, views, glob,
-                                 vh.VK_QK_HEADS_OUTER, cfg["rope_freq"], cfg["qk_norm_eps"])
+                                 vh.VK_QK_HEADS_OUTER, cfg["rope_freq"], cfg["qk_norm_eps"],
+                                 rope_mode=cfg.get("rope_mode", 0))
     elif use_qkn:
         rt.layernorm_into_f32(q, dev.vec["qnorm_gamma"], dev.vec["qnorm_beta"], rows * H, 64,
                               cfg["qk_norm_eps"], q)
@@ -100,6 +101,10 @@ CASES = [
     pytest.param(768, 12, 3072, 3, 5, 2, 3, dict(qknorm_start=-1, alt=-1), id="vitb-rope-no-qknorm"),
     pytest.param(1024, 16, 4096, 3, 4, 2, 7, {}, id="vitl-2views-global"),
     pytest.param(768, 12, 3072, 24, 36, 1, 0, {}, id="vitb-504x336-local"),
+    pytest.param(768, 12, 3072, 4, 6, 3, 2, dict(rope_mode=1), id="vitb-3views-local-interleaved"),
+    pytest.param(768, 12, 3072, 4, 6, 3, 5, dict(rope_mode=3),
+                 id="vitb-3views-global-interleaved-exphead"),
+    pytest.param(768, 12, 3072, 24, 36, 1, 0, dict(rope_mode=2), id="vitb-504x336-exphead"),
 ]
 
 

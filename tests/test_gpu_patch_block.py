@@ -85,6 +85,65 @@ def test_events_and_graph_replays(rt, rng):
     assert e0.elapsed_ms(e1) >= 0.0
 
 
+def test_graph_of_copies_replays(rt, rng):
+    """Segment copies and the prefix (camera-slot) write are kernels: a
+    captured sequence of them replays with the eager bits, replay after
+    replay, with eager work in between."""
+    D, rows = 768, 30
+    x = normals(rng, rows, D)
+    cam = normals(rng, 2 * D)
+    tokens, camera, snap = rt.upload_f32(x), rt.upload_f32(cam), rt.alloc_f32(rows * D)
+    ones_h = np.ones((rows, D), np.float32)
+    ones = rt.upload_f32(ones_h)
+    odd = rt.alloc_f32(5)
+
+    def step():
+        rt.copy_segment_into_f32(snap, 0, tokens, 0, rows * D)
+        rt.copy_segment_into_f32(odd, 0, tokens, 3, 5)  # 4-byte aligned only
+        rt.overwrite_prefix_f32(tokens, camera, D)      # the camera-slot write
+
+    expect = x.copy()
+    rt.synchronize()
+    rt.begin_capture()
+    step()
+    graph = rt.end_capture()
+    for r in range(3):
+        graph.launch()
+        rt.synchronize()
+        snap_want = expect.copy()
+        expect[0] = cam[:D]
+        assert np.array_equal(snap.numpy().reshape(rows, D), snap_want), f"replay {r}"
+        assert np.array_equal(odd.numpy(), snap_want.reshape(-1)[3:8]), f"replay {r}"
+        assert np.array_equal(tokens.numpy().reshape(rows, D), expect), f"replay {r}"
+        rt.add_f32_in_place(tokens, ones)
+        expect = oracle.add(expect, ones_h)
+
+
+def test_graph_lifetime_rules(rng):
+    """A graph launches only on the runtime it was captured on, not after
+    that runtime was destroyed, and its destroy is clean afterwards."""
+    a, b = vh.Runtime(0), vh.Runtime(0)
+    x, y = normals(rng, 4096), normals(rng, 4096)
+    t, u = a.upload_f32(x), a.upload_f32(y)
+    a.synchronize()
+    a.begin_capture()
+    try:
+        a.add_f32_in_place(t, u)
+    finally:
+        graph = a.end_capture()
+    graph.launch()
+    a.synchronize()
+    assert np.array_equal(t.numpy(), x + y)
+    with pytest.raises(vh.VestraError, match="another runtime"):
+        vh._check(vh.lib.vk_graph_launch(b.handle, graph.handle))
+    handle = a.handle
+    a.close()
+    with pytest.raises(vh.VestraError, match="destroyed"):
+        vh._check(vh.lib.vk_graph_launch(handle, graph.handle))
+    del graph, t, u  # the graph and the tensors release the runtime
+    b.close()
+
+
 # ---------------------------------------------------------------- patch embedding pieces
 def test_patchify_bit_exact(rt, rng):
     img = normals(rng, 3, 336, 504)
@@ -251,6 +310,32 @@ def test_patch_embed_u8_matches_oracle(rt, rng, h, w, embed, n_register):
     scale = a @ np.abs(wt.reshape(embed, -1)).astype(np.float64).T
     assert_dot_parity(got[1 + n_register:], ref[1 + n_register:], scale, 588,
                       f"patch_embed {h}x{w}")
+
+
+def test_patch_embed_f16_filter_vitl_matches_oracle(rt, rng):
+    """ViT-L at 1008x672 with the patch filter stored as F16 (GGUF F16
+    element layout) and widened on the device: the oracle runs on the same
+    filter widened on the host, which is exact (reader.rs:303-318)."""
+    h, w, embed, n_register = 672, 1008, 1024, 1
+    gh, gw = h // 14, w // 14
+    img = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    wt16 = normals(rng, embed, 3, 14, 14, scale=0.02).astype(np.float16)
+    wt = wt16.astype(np.float32)
+    b = normals(rng, embed, scale=0.02)
+    cls = normals(rng, embed, scale=0.02)
+    regs = normals(rng, n_register, embed, scale=0.02)
+    pos = normals(rng, 1 + gh * gw, embed, scale=0.02)
+    proj = rt.prepare_linear_oihw_w16(588, embed, wt16, b)
+    out = rt.alloc_f32((1 + n_register + gh * gw) * embed)
+    rt.patch_embed_u8(rt.upload_u8(img), h, w, 14, MEAN, STD, proj, rt.upload_f32(cls),
+                      rt.upload_f32(regs), n_register, rt.upload_f32(pos), out)
+    ref = oracle.patch_embed_u8(img, 14, MEAN, STD, wt, b, cls, regs, pos)
+    got = out.numpy().reshape(ref.shape)
+    assert np.array_equal(got[:1 + n_register], ref[:1 + n_register])
+    a = np.abs(oracle.patchify_nchw(oracle.normalize_u8_hwc(img, MEAN, STD), 14)).astype(np.float64)
+    scale = a @ np.abs(wt.reshape(embed, -1)).astype(np.float64).T
+    assert_dot_parity(got[1 + n_register:], ref[1 + n_register:], scale, 588,
+                      "patch_embed 672x1008 f16 filter")
 
 
 def test_patch_embed_rejects_unqualified_patch(rt, rng):

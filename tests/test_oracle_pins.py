@@ -204,15 +204,72 @@ def test_rope_identity_at_origin(rng):
     assert np.array_equal(oracle.rope2d(x, 2, 3, 64, pos), x)
 
 
-def test_rope_preserves_pair_norms(rng):
+def _pairs(mode):
+    """Element pairs (a, b) of one 32-wide half under a RoPE convention:
+    rotate-half (j, j+16) or interleaved (2j, 2j+1), in frequency order j."""
+    if mode & oracle.ROPE_INTERLEAVED:
+        return [(2 * j, 2 * j + 1) for j in range(16)]
+    return [(j, j + 16) for j in range(16)]
+
+
+@pytest.mark.parametrize("mode", oracle.ROPE_MODES)
+def test_rope_preserves_pair_norms(rng, mode):
     x = rng.standard_normal((3, 5, 64)).astype(np.float32)
     pos = rng.integers(0, 80, (5, 2))
-    y = oracle.rope2d(x, 3, 5, 64, pos).astype(np.float64)
+    y = oracle.rope2d(x, 3, 5, 64, pos, 100.0, mode).astype(np.float64)
     xd = x.astype(np.float64)
     for half in (0, 32):
-        a, b = xd[..., half:half + 16], xd[..., half + 16:half + 32]
-        a2, b2 = y[..., half:half + 16], y[..., half + 16:half + 32]
-        assert np.allclose(a * a + b * b, a2 * a2 + b2 * b2, rtol=1e-5, atol=1e-6)
+        for a, b in _pairs(mode):
+            n0 = xd[..., half + a] ** 2 + xd[..., half + b] ** 2
+            n1 = y[..., half + a] ** 2 + y[..., half + b] ** 2
+            assert np.allclose(n0, n1, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("mode", oracle.ROPE_MODES)
+def test_rope_complex_twin(rng, mode):
+    # float64 twin written as complex multiplication: pair (a, b) of half h
+    # is z = x_a + i x_b, rotated to z * exp(i p_h w_j) with
+    # w_j = base^(-2j / denom), denom = 32 (exponent over the half) or 64
+    # (over the head); the y half takes the row coordinate, the x half the
+    # column.  The oracle rounds the angle once in f32, so the bound grows
+    # with the angle.
+    heads, n, base = 2, 9, 100.0
+    x = rng.standard_normal((heads, n, 64)).astype(np.float32)
+    pos = rng.integers(0, 60, (n, 2))
+    pos[0] = (0, 0)
+    got = oracle.rope2d(x, heads, n, 64, pos, base, mode).astype(np.float64)
+    denom = 64.0 if mode & oracle.ROPE_EXP_HEAD else 32.0
+    w = base ** (-2.0 * np.arange(16) / denom)
+    expect = np.empty_like(got)
+    for half, coord in ((0, 0), (32, 1)):
+        for j, (a, b) in enumerate(_pairs(mode)):
+            z = x[..., half + a].astype(np.float64) + 1j * x[..., half + b]
+            z = z * np.exp(1j * pos[:, coord] * w[j])
+            expect[..., half + a] = z.real
+            expect[..., half + b] = z.imag
+    mag = np.abs(x).astype(np.float64).max()
+    bound = 4e-7 * mag * (1.0 + pos.max())
+    assert np.max(np.abs(got - expect)) < bound
+
+
+@pytest.mark.parametrize("mode", oracle.ROPE_MODES)
+def test_rope_closed_form_angles(mode):
+    # Textbook values: frequency 0 turns by exactly p radians; with base 100,
+    # frequency 8 turns by p * 100^(-16/32) = p/10 (exponent over the half)
+    # or p * 100^(-16/64) = p/sqrt(10) (over the head).  A unit vector at the
+    # pair's first element lands on (cos t, sin t) in (first, second).
+    pairs = _pairs(mode)
+    slow = 1.0 / math.sqrt(10.0) if mode & oracle.ROPE_EXP_HEAD else 0.1
+    for j, p, theta in ((0, 1, 1.0), (0, 3, 3.0), (8, 10, 10 * slow), (8, 7, 7 * slow)):
+        for half, pos in ((0, [p, 0]), (32, [0, p])):
+            a, b = pairs[j]
+            x = np.zeros((1, 1, 64), np.float32)
+            x[0, 0, half + a] = 1.0
+            y = oracle.rope2d(x, 1, 1, 64, np.array([pos], np.int64), 100.0, mode)[0, 0]
+            assert abs(float(y[half + a]) - math.cos(theta)) < 2e-6
+            assert abs(float(y[half + b]) - math.sin(theta)) < 2e-6
+            others = np.delete(y, [half + a, half + b])
+            assert not others.any()
 
 
 def test_rope_relative_position_property(rng):
@@ -232,21 +289,35 @@ def test_rope_relative_position_property(rng):
     assert abs(dot((4, 5), (1, 2)) - base) > 1e-3
 
 
-def test_rope_recovered_angles_and_pairing():
-    # a unit vector at element j of a half rotates inside the (j, j+16) pair by
-    # pos * base^(-2j/32): y half by the row coordinate, x half by the column.
+@pytest.mark.parametrize("mode", oracle.ROPE_MODES)
+def test_rope_recovered_angles_and_pairing(mode):
+    # a unit vector at the first element of pair j of a half rotates inside
+    # that pair only, by pos * base^(-2j/denom): y half by the row
+    # coordinate, x half by the column.
     py, px = 7, 3
+    denom = 64.0 if mode & oracle.ROPE_EXP_HEAD else 32.0
     for half, p in ((0, py), (32, px)):
-        for j in range(16):
+        for j, (a, b) in enumerate(_pairs(mode)):
             x = np.zeros((1, 1, 64), np.float32)
-            x[0, 0, half + j] = 1.0
-            y = oracle.rope2d(x, 1, 1, 64, np.array([[py, px]], np.int64))[0, 0]
+            x[0, 0, half + a] = 1.0
+            y = oracle.rope2d(x, 1, 1, 64, np.array([[py, px]], np.int64), 100.0, mode)[0, 0]
             nz = np.flatnonzero(np.abs(y) > 1e-7)
-            assert set(nz.tolist()) <= {half + j, half + j + 16}
-            theta = math.atan2(float(y[half + j + 16]), float(y[half + j]))
-            expect = p * 100.0 ** (-2.0 * j / 32.0)
+            assert set(nz.tolist()) <= {half + a, half + b}
+            theta = math.atan2(float(y[half + b]), float(y[half + a]))
+            expect = p * 100.0 ** (-2.0 * j / denom)
             d = (theta - expect + math.pi) % (2 * math.pi) - math.pi
             assert abs(d) < 2e-5 * max(1.0, expect)
+
+
+def test_rope_conventions_differ(rng):
+    # the four conventions are four different functions of the same input
+    x = rng.standard_normal((1, 4, 64)).astype(np.float32)
+    pos = np.array([[0, 0], [3, 5], [2, 7], [11, 4]], np.int64)
+    outs = [oracle.rope2d(x, 1, 4, 64, pos, 100.0, m) for m in oracle.ROPE_MODES]
+    for i in range(len(outs)):
+        assert np.array_equal(outs[i][:, 0], x[:, 0])
+        for j in range(i):
+            assert np.max(np.abs(outs[i][:, 1:] - outs[j][:, 1:])) > 1e-3
 
 
 def test_rope_changes_output(kats):
@@ -259,16 +330,20 @@ def test_rope_changes_output(kats):
     assert np.max(np.abs(y[:, 1] - x[:, 1])) > 1e-4
 
 
-def test_qk_norm_rope_is_norm_then_rope(rng):
+@pytest.mark.parametrize("mode", oracle.ROPE_MODES)
+def test_qk_norm_rope_is_norm_then_rope(rng, mode):
     heads, n = 3, 7
     q = rng.standard_normal((heads, n, 64)).astype(np.float32)
     k = rng.standard_normal((heads, n, 64)).astype(np.float32)
     qg, qb, kg, kb = [(1 + 0.02 * rng.standard_normal(64)).astype(np.float32) for _ in range(4)]
     pos = oracle.rope_positions(1, 2, 3, 1, False)
-    qo, ko = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n)
-    q_ref = oracle.rope2d(oracle.layernorm(q, qg, qb, 1e-5), heads, n, 64, pos.astype(np.int64))
-    k_ref = oracle.rope2d(oracle.layernorm(k, kg, kb, 1e-5), heads, n, 64, pos.astype(np.int64))
+    qo, ko = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n, mode=mode)
+    pi = pos.astype(np.int64)
+    q_ref = oracle.rope2d(oracle.layernorm(q, qg, qb, 1e-5), heads, n, 64, pi, 100.0, mode)
+    k_ref = oracle.rope2d(oracle.layernorm(k, kg, kb, 1e-5), heads, n, 64, pi, 100.0, mode)
     assert np.array_equal(qo, q_ref) and np.array_equal(ko, k_ref)
+    if mode:
+        return
     # rope-then-norm is a different function
     wrong = oracle.layernorm(oracle.rope2d(q, heads, n, 64, pos.astype(np.int64)), qg, qb, 1e-5)
     assert not np.allclose(qo, wrong, atol=1e-4)

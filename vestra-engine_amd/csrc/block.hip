@@ -69,10 +69,8 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
     VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D, "camera token must hold >= %zu f32", D);
     VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
                "multi-view camera token must hold reference and source slots (2*%zu)", D);
-    for (size_t v = 0; v < view_count; ++v) {
-      const size_t slot = v > 0 ? 1 : 0;
-      VK_TRY(vk_copy_segment_into_f32(rt, act->tokens, v * tpv * D, camera, slot * D, D));
-    }
+    VK_TRY(vk::write_camera_rows(rt, static_cast<float*>(act->tokens->ptr),
+                                 static_cast<const float*>(camera->ptr), view_count, tpv, D));
     camera_written = true;
   }
 
@@ -91,11 +89,11 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
       cfg->rope_start >= 0 && static_cast<long long>(layer_idx) >= cfg->rope_start;
   const vk_qk_layout layout = global ? VK_QK_HEADS_OUTER : VK_QK_VIEWS_OUTER;
   if (use_rope) {
-    VK_TRY(vk_qk_norm_rope_grid_f32(
+    VK_TRY(vk_qk_norm_rope_grid_mode_f32(
         rt, act->q, act->k, use_qknorm ? layer->qnorm_gamma : nullptr,
         use_qknorm ? layer->qnorm_beta : nullptr, use_qknorm ? layer->knorm_gamma : nullptr,
         use_qknorm ? layer->knorm_beta : nullptr, H, hd, n_special, gh, gw, view_count,
-        global ? 1 : 0, layout, cfg->rope_freq, cfg->qk_norm_eps));
+        global ? 1 : 0, layout, cfg->rope_freq, cfg->qk_norm_eps, cfg->rope_mode));
   } else if (use_qknorm) {
     // Q/K-norm without RoPE: LayerNorm over every (head, token) row
     VK_TRY(vk_layernorm_into_f32(rt, act->q, layer->qnorm_gamma, layer->qnorm_beta, rows * H, hd,
@@ -193,10 +191,8 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
     VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D, "camera token must hold >= %zu f32", D);
     VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
                "multi-view camera token must hold reference and source slots (2*%zu)", D);
-    for (size_t v = 0; v < view_count; ++v) {
-      const size_t slot = v > 0 ? 1 : 0;
-      VK_TRY(vk_copy_segment_into_f32(rt, tokens, v * tpv * D, camera, slot * D, D));
-    }
+    VK_TRY(vk::write_camera_rows(rt, static_cast<float*>(tokens->ptr),
+                                 static_cast<const float*>(camera->ptr), view_count, tpv, D));
   }
 
   // LN1 -> QKV (head-major Q, K, V) with Q/K-norm + RoPE, gated as in
@@ -210,11 +206,11 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
   const bool use_rope =
       cfg->rope_start >= 0 && static_cast<long long>(layer_idx) >= cfg->rope_start;
   if (use_rope) {
-    VK_TRY(vk_linear_run_qkv_hnd_norm_rope_f32(
+    VK_TRY(vk_linear_run_qkv_hnd_norm_rope_mode_f32(
         rt, w->qkv, ws->ln, rows, H, hd, ws->q, ws->k, ws->v,
         use_qknorm ? w->qnorm_gamma : nullptr, use_qknorm ? w->qnorm_beta : nullptr,
         use_qknorm ? w->knorm_gamma : nullptr, use_qknorm ? w->knorm_beta : nullptr, n_special,
-        gh, gw, view_count, global ? 1 : 0, cfg->rope_freq, cfg->qk_norm_eps));
+        gh, gw, view_count, global ? 1 : 0, cfg->rope_freq, cfg->qk_norm_eps, cfg->rope_mode));
   } else {
     VK_TRY(vk_linear_run_qkv_hnd_f32(rt, w->qkv, ws->ln, rows, H, hd, ws->q, ws->k, ws->v));
   }

@@ -10,6 +10,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "vestra_hip.h"
@@ -31,9 +32,9 @@ struct vk_runtime {
   hipStream_t stream = nullptr;
   int cu_count = 0;
   // cos/sin tables of the 2D rotary embedding, keyed by (frequency bits,
-  // head_dim): device pointer (owned by the runtime) and the largest
-  // position the table covers.
-  std::map<std::pair<uint32_t, int>, std::pair<float*, int>> rope_tables;
+  // head_dim, exponent over the whole head): device pointer (owned by the
+  // runtime) and the largest position the table covers.
+  std::map<std::tuple<uint32_t, int, int>, std::pair<float*, int>> rope_tables;
   // Work buffer (f32) of launches that hand intermediate values from one
   // kernel to the next on the runtime's stream: split-K partial sums, the
   // row statistics of the token -> CHW hand-off.  Every user is ordered on
@@ -75,6 +76,10 @@ struct vk_event {
 };
 
 struct vk_graph {
+  // The runtime whose stream was captured: the graph keeps it alive (its
+  // nodes name the runtime's work buffer and RoPE tables) and launches only
+  // on its stream.
+  vk_runtime* rt = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 };
@@ -132,13 +137,23 @@ int check_launch(const char* what);
 // positions 0..max(min_max_pos, kRopeTableMax); *table_max receives the
 // largest covered position.  Grows (re-allocates) when a larger grid needs
 // it, so call it before any stream capture that uses the table.
-int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
-               int* table_max);
+int rope_table(vk_runtime* rt, float freq, int head_dim, unsigned rope_mode, int min_max_pos,
+               const float** out, int* table_max);
+// VK_ERR_INVALID for RoPE convention flags other than VK_ROPE_*.
+int check_rope_mode(unsigned rope_mode);
 // Makes rt->work hold at least `floats` floats (at least 8 Mi once
 // allocated, doubling on growth).  Growth is refused during stream capture:
 // run the sequence once eagerly first.  The buffer it replaces is retired,
 // not freed.
 int ensure_work(vk_runtime* rt, size_t floats, const char* who);
+// Stream-ordered device-to-device copy of `bytes` bytes as a kernel (a
+// captured sequence then holds kernel nodes only).
+int device_copy(vk_runtime* rt, void* dst, const void* src, size_t bytes);
+// Camera-token slot write (backbone.rs:446-457, 746-768) as one launch:
+// row v * tokens_per_view of the view-major `tokens` [views * tpv, D] takes
+// camera slot 0 (v == 0, the reference view) or slot 1 (source views).
+int write_camera_rows(vk_runtime* rt, float* tokens, const float* camera, size_t view_count,
+                      size_t tokens_per_view, size_t D);
 
 // Q/K-norm + RoPE parameters of the QKV projection's fused epilogue: the
 // row's token index m gives its position (rows are view-major tokens).
@@ -154,6 +169,7 @@ struct QkEpilogue {
   vkd::FastDivU32 tpv;  // tokens per view
   vkd::FastDivU32 gw;   // patch grid width
   float eps;
+  uint32_t interleaved;  // RoPE pairing: 0 (j, j+16), 1 (2i, 2i+1)
 };
 
 // F32 linear out[m, n] = epilogue(sum_k x[m, k] W[n, k] + b[n]).

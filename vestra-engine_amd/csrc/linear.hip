@@ -125,7 +125,11 @@ __device__ __forceinline__ float4 qk_head_row(const LinearArgs& g, float4 v, int
                      g.qkn.global, g.qkn.gw, &py, &px);
   const PT* gm = static_cast<const PT*>(is_k ? g.qkn.kg : g.qkn.qg);
   const PT* bt = static_cast<const PT*>(is_k ? g.qkn.kb : g.qkn.qb);
-  return vkq::qk_row_transform<PT, QknTraits<QKN>::kNorm, vkq::kPosGrid>(
+  // the pairing is uniform over the launch: a scalar branch
+  if (g.qkn.interleaved)
+    return vkq::qk_row_transform<PT, QknTraits<QKN>::kNorm, vkq::kPosGrid, vkq::kInterleaved>(
+        v, l, gm, bt, py, px, g.qkn.table, g.qkn.table_max, g.qkn.eps);
+  return vkq::qk_row_transform<PT, QknTraits<QKN>::kNorm, vkq::kPosGrid, vkq::kRotateHalf>(
       v, l, gm, bt, py, px, g.qkn.table, g.qkn.table_max, g.qkn.eps);
 }
 

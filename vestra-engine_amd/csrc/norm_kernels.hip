@@ -127,15 +127,15 @@ using namespace vkq;
 constexpr int kQkRowsPerGroup = 2;
 constexpr int kQkThreads = 256;  // threads per workgroup: kQkThreads / 16 row groups
 
-template <typename PT, bool HAS_NORM, int POS>
+template <typename PT, bool HAS_NORM, int POS, int PAIR>
 __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
     const PT* __restrict__ qb, const PT* __restrict__ kg, const PT* __restrict__ kb,
-    const float* __restrict__ pos_yx, const float* __restrict__ table, QkShape sh,
+    const void* __restrict__ pos_yx, const float* __restrict__ table, QkShape sh,
     float eps) {
   const int l = threadIdx.x & 15;
   const uint32_t grp = blockIdx.x * (kQkThreads / 16u) + (threadIdx.x >> 4);
-  const uint32_t total = 2u * sh.rows_per_tensor;
+  const uint32_t total = sh.tensors * sh.rows_per_tensor;
   float4 v[kQkRowsPerGroup];
   int py[kQkRowsPerGroup], px[kQkRowsPerGroup];
 #pragma unroll
@@ -152,9 +152,9 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
   for (int j = 0; j < kQkRowsPerGroup; ++j) {
     const uint32_t gr = grp * kQkRowsPerGroup + j;
     const bool is_k = gr >= sh.rows_per_tensor;
-    const float4 o = qk_row_transform<PT, HAS_NORM, POS>(v[j], l, is_k ? kg : qg,
-                                                         is_k ? kb : qb, py[j], px[j], table,
-                                                         sh.table_max, eps);
+    const float4 o = qk_row_transform<PT, HAS_NORM, POS, PAIR>(v[j], l, is_k ? kg : qg,
+                                                               is_k ? kb : qb, py[j], px[j],
+                                                               table, sh.table_max, eps);
     if (gr < total) {
       const uint32_t r = is_k ? gr - sh.rows_per_tensor : gr;
       vkd::st_stream(reinterpret_cast<float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l, o);
@@ -253,30 +253,81 @@ int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
   return vk::check_launch("ls_residual_layernorm_rows");
 }
 
-template <typename PT, bool HAS_NORM, int POS>
+template <typename PT, bool HAS_NORM, int POS, int PAIR>
 int launch_qk(vk_runtime* rt, float* q, float* k, const void* qg, const void* qb,
-              const void* kg, const void* kb, const float* pos, const float* table,
+              const void* kg, const void* kb, const void* pos, const float* table,
               const QkShape& sh, float eps) {
-  const long long total = 2LL * sh.rows_per_tensor;
+  const long long total = static_cast<long long>(sh.tensors) * sh.rows_per_tensor;
   const long long groups = (total + kQkRowsPerGroup - 1) / kQkRowsPerGroup;
   const long long blocks = (groups + kQkThreads / 16 - 1) / (kQkThreads / 16);
-  hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kQkThreads), 0, rt->stream, q, k, static_cast<const PT*>(qg),
-                     static_cast<const PT*>(qb), static_cast<const PT*>(kg),
-                     static_cast<const PT*>(kb), pos, table, sh, eps);
+  hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q, k,
+                     static_cast<const PT*>(qg), static_cast<const PT*>(qb),
+                     static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh, eps);
   return vk::check_launch("qk_norm_rope_rows");
 }
 
-template <int POS>
-int dispatch_qk(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_tensor* qg,
-                const vk_tensor* qb, const vk_tensor* kg, const vk_tensor* kb,
-                const float* pos, const float* table, const QkShape& sh, float eps) {
-  float* Q = static_cast<float*>(q->ptr);
-  float* K = static_cast<float*>(k->ptr);
-  if (!qg) return launch_qk<float, false, POS>(rt, Q, K, nullptr, nullptr, nullptr, nullptr, pos, table, sh, eps);
+template <int POS, int PAIR>
+int dispatch_qk_pair(vk_runtime* rt, float* Q, float* K, const vk_tensor* qg,
+                     const vk_tensor* qb, const vk_tensor* kg, const vk_tensor* kb,
+                     const void* pos, const float* table, const QkShape& sh, float eps) {
+  if (!qg)
+    return launch_qk<float, false, POS, PAIR>(rt, Q, K, nullptr, nullptr, nullptr, nullptr, pos,
+                                              table, sh, eps);
   if (qg->dtype == VK_F16)
-    return launch_qk<uint16_t, true, POS>(rt, Q, K, qg->ptr, qb->ptr, kg->ptr, kb->ptr, pos, table, sh, eps);
-  return launch_qk<float, true, POS>(rt, Q, K, qg->ptr, qb->ptr, kg->ptr, kb->ptr, pos, table, sh, eps);
+    return launch_qk<uint16_t, true, POS, PAIR>(rt, Q, K, qg->ptr, qb->ptr, kg->ptr, kb->ptr,
+                                                pos, table, sh, eps);
+  return launch_qk<float, true, POS, PAIR>(rt, Q, K, qg->ptr, qb->ptr, kg->ptr, kb->ptr, pos,
+                                           table, sh, eps);
+}
+
+// q, k: the tensors (k == q with sh.tensors == 1); qg..kb null: RoPE only.
+template <int POS>
+int dispatch_qk(vk_runtime* rt, float* Q, float* K, const vk_tensor* qg, const vk_tensor* qb,
+                const vk_tensor* kg, const vk_tensor* kb, const void* pos, const float* table,
+                const QkShape& sh, float eps, unsigned rope_mode) {
+  if (rope_mode & VK_ROPE_INTERLEAVED)
+    return dispatch_qk_pair<POS, kInterleaved>(rt, Q, K, qg, qb, kg, kb, pos, table, sh, eps);
+  return dispatch_qk_pair<POS, kRotateHalf>(rt, Q, K, qg, qb, kg, kb, pos, table, sh, eps);
+}
+
+// Explicit positions: the f32, i32 or i64 instance for the tensor's dtype.
+int dispatch_qk_explicit(vk_runtime* rt, float* Q, float* K, const vk_tensor* qg,
+                         const vk_tensor* qb, const vk_tensor* kg, const vk_tensor* kb,
+                         const vk_tensor* positions, const float* table, const QkShape& sh,
+                         float eps, unsigned rope_mode) {
+  switch (positions->dtype) {
+    case VK_I32:
+      return dispatch_qk<kPosExplicitI32>(rt, Q, K, qg, qb, kg, kb, positions->ptr, table, sh,
+                                          eps, rope_mode);
+    case VK_I64:
+      return dispatch_qk<kPosExplicitI64>(rt, Q, K, qg, qb, kg, kb, positions->ptr, table, sh,
+                                          eps, rope_mode);
+    default:
+      return dispatch_qk<kPosExplicit>(rt, Q, K, qg, qb, kg, kb, positions->ptr, table, sh, eps,
+                                       rope_mode);
+  }
+}
+
+bool positions_ok(const vk_tensor* p) {
+  return p && (p->dtype == VK_F32 || p->dtype == VK_I32 || p->dtype == VK_I64);
+}
+
+// The positions-tensor shape of the reference-signature forms: rows_per_tensor
+// = heads * rows, one sequence of `rows` tokens.
+QkShape explicit_shape(size_t heads, size_t rows, int table_max, uint32_t tensors) {
+  QkShape sh;
+  sh.rows_per_tensor = static_cast<uint32_t>(heads * rows);
+  sh.tensors = tensors;
+  sh.table_max = table_max;
+  sh.n_special = 0;
+  sh.global = 0;
+  sh.layout = VK_QK_HEADS_OUTER;
+  sh.ntok = vkd::make_fastdiv(static_cast<uint32_t>(rows));
+  sh.tpv = sh.ntok;
+  sh.per_view = vkd::make_fastdiv(static_cast<uint32_t>(heads * rows));
+  sh.gw = vkd::make_fastdiv(1);
+  return sh;
 }
 
 int check_qk_params(const vk_tensor* qg, const vk_tensor* qb, const vk_tensor* kg,
@@ -386,14 +437,15 @@ int vk_layerscale_residual_layernorm_f32(vk_runtime* rt, vk_tensor* x, const vk_
             : launch_ls_res_ln<float, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps);
 }
 
-int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_tensor* q_gamma,
-                        const vk_tensor* q_beta, const vk_tensor* k_gamma,
-                        const vk_tensor* k_beta, const vk_tensor* positions, size_t heads,
-                        size_t rows, float freq, float eps) {
+int vk_qk_norm_rope_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                             const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                             const vk_tensor* k_gamma, const vk_tensor* k_beta,
+                             const vk_tensor* positions, size_t heads, size_t rows, float freq,
+                             float eps, unsigned rope_mode) {
   VK_TRY(vk::bind(rt));
   VK_REQUIRE(q && k && positions, "null tensor");
-  VK_REQUIRE(q->dtype == VK_F32 && k->dtype == VK_F32 && positions->dtype == VK_F32,
-             "q, k and positions must be f32");
+  VK_REQUIRE(q->dtype == VK_F32 && k->dtype == VK_F32, "q and k must be f32");
+  VK_REQUIRE(positions_ok(positions), "positions must be f32, i32 or i64");
   const size_t head_dim = 64;
   VK_REQUIRE(heads > 0 && q->len == heads * rows * head_dim && k->len == q->len,
              "q/k must hold heads*rows*64 = %zu elements (q %zu, k %zu)",
@@ -403,30 +455,57 @@ int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_ten
   VK_REQUIRE(q->ptr != k->ptr, "q and k must be distinct buffers");
   VK_TRY(check_qk_params(q_gamma, q_beta, k_gamma, k_beta, head_dim));
   VK_UNSUPPORTED_IF(2 * heads * rows > 0x7fffffffULL, "heads*rows=%zu too large", heads * rows);
+  VK_TRY(vk::check_rope_mode(rope_mode));
   if (rows == 0) return VK_OK;
   const float* table = nullptr;
   int table_max = 0;
-  VK_TRY(vk::rope_table(rt, freq, 64, 0, &table, &table_max));
-  QkShape sh;
-  sh.rows_per_tensor = static_cast<uint32_t>(heads * rows);
-  sh.table_max = table_max;
-  sh.n_special = 0;
-  sh.global = 0;
-  sh.layout = VK_QK_HEADS_OUTER;
-  sh.ntok = vkd::make_fastdiv(static_cast<uint32_t>(rows));
-  sh.tpv = sh.ntok;
-  sh.per_view = vkd::make_fastdiv(static_cast<uint32_t>(heads * rows));
-  sh.gw = vkd::make_fastdiv(1);
-  return dispatch_qk<kPosExplicit>(rt, q, k, q_gamma, q_beta, k_gamma, k_beta,
-                                   static_cast<const float*>(positions->ptr), table, sh, eps);
+  VK_TRY(vk::rope_table(rt, freq, 64, rope_mode, 0, &table, &table_max));
+  const QkShape sh = explicit_shape(heads, rows, table_max, 2);
+  return dispatch_qk_explicit(rt, static_cast<float*>(q->ptr), static_cast<float*>(k->ptr),
+                              q_gamma, q_beta, k_gamma, k_beta, positions, table, sh, eps,
+                              rope_mode);
 }
 
-int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
-                             const vk_tensor* q_gamma, const vk_tensor* q_beta,
-                             const vk_tensor* k_gamma, const vk_tensor* k_beta, size_t heads,
-                             size_t head_dim, size_t n_special, size_t gh, size_t gw,
-                             size_t view_count, int global, vk_qk_layout layout, float freq,
-                             float eps) {
+int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k, const vk_tensor* q_gamma,
+                        const vk_tensor* q_beta, const vk_tensor* k_gamma,
+                        const vk_tensor* k_beta, const vk_tensor* positions, size_t heads,
+                        size_t rows, float freq, float eps) {
+  VK_REQUIRE(positions == nullptr || positions->dtype == VK_F32, "positions must be f32");
+  return vk_qk_norm_rope_mode_f32(rt, q, k, q_gamma, q_beta, k_gamma, k_beta, positions, heads,
+                                  rows, freq, eps, VK_ROPE_DEFAULT);
+}
+
+int vk_rope2d_f32(vk_runtime* rt, vk_tensor* x, const vk_tensor* positions, size_t heads,
+                  size_t rows, size_t head_dim, float freq, unsigned rope_mode) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(x && positions, "null tensor");
+  VK_REQUIRE(x->dtype == VK_F32, "x must be f32");
+  VK_REQUIRE(positions_ok(positions), "positions must be f32, i32 or i64");
+  VK_UNSUPPORTED_IF(head_dim != 64, "rope2d: head_dim=%zu (qualified: 64)", head_dim);
+  VK_REQUIRE(heads > 0 && x->len == heads * rows * head_dim,
+             "x must hold heads*rows*64 = %zu elements (got %zu)", heads * rows * head_dim,
+             x->len);
+  VK_REQUIRE(positions->len == rows * 2, "positions must hold rows*2 = %zu (got %zu)",
+             rows * 2, positions->len);
+  VK_UNSUPPORTED_IF(heads * rows > 0x7fffffffULL, "heads*rows=%zu too large", heads * rows);
+  VK_TRY(vk::check_rope_mode(rope_mode));
+  if (rows == 0) return VK_OK;
+  const float* table = nullptr;
+  int table_max = 0;
+  VK_TRY(vk::rope_table(rt, freq, 64, rope_mode, 0, &table, &table_max));
+  const QkShape sh = explicit_shape(heads, rows, table_max, 1);
+  float* X = static_cast<float*>(x->ptr);
+  return dispatch_qk_explicit(rt, X, X, nullptr, nullptr, nullptr, nullptr, positions, table, sh,
+                              0.0f, rope_mode);
+}
+
+int vk_qk_norm_rope_grid_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                                  const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                                  const vk_tensor* k_gamma, const vk_tensor* k_beta,
+                                  size_t heads, size_t head_dim, size_t n_special, size_t gh,
+                                  size_t gw, size_t view_count, int global,
+                                  vk_qk_layout layout, float freq, float eps,
+                                  unsigned rope_mode) {
   VK_TRY(vk::bind(rt));
   VK_REQUIRE(q && k, "null tensor");
   VK_REQUIRE(q->dtype == VK_F32 && k->dtype == VK_F32, "q and k must be f32");
@@ -442,15 +521,18 @@ int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
   VK_REQUIRE(q->ptr != k->ptr, "q and k must be distinct buffers");
   VK_TRY(check_qk_params(q_gamma, q_beta, k_gamma, k_beta, head_dim));
   VK_UNSUPPORTED_IF(2 * heads * rows > 0x7fffffffULL, "heads*rows=%zu too large", heads * rows);
+  VK_TRY(vk::check_rope_mode(rope_mode));
   if (rows == 0) return VK_OK;
   // the grid's largest coordinate is max(gh, gw) + 1: size the table to it
   const float* table = nullptr;
   int table_max = 0;
   const size_t max_coord = (gh > gw ? gh : gw) + 1;
   VK_UNSUPPORTED_IF(max_coord > (1u << 22), "patch grid %zux%zu too large", gh, gw);
-  VK_TRY(vk::rope_table(rt, freq, 64, static_cast<int>(max_coord), &table, &table_max));
+  VK_TRY(vk::rope_table(rt, freq, 64, rope_mode, static_cast<int>(max_coord), &table,
+                        &table_max));
   QkShape sh;
   sh.rows_per_tensor = static_cast<uint32_t>(heads * rows);
+  sh.tensors = 2;
   sh.table_max = table_max;
   sh.n_special = static_cast<uint32_t>(n_special);
   sh.global = global ? 1u : 0u;
@@ -459,8 +541,20 @@ int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
   sh.tpv = vkd::make_fastdiv(static_cast<uint32_t>(tpv));
   sh.per_view = vkd::make_fastdiv(static_cast<uint32_t>(heads * tpv));
   sh.gw = vkd::make_fastdiv(static_cast<uint32_t>(gw));
-  return dispatch_qk<kPosGrid>(rt, q, k, q_gamma, q_beta, k_gamma, k_beta, nullptr, table, sh,
-                               eps);
+  return dispatch_qk<kPosGrid>(rt, static_cast<float*>(q->ptr), static_cast<float*>(k->ptr),
+                               q_gamma, q_beta, k_gamma, k_beta, nullptr, table, sh, eps,
+                               rope_mode);
+}
+
+int vk_qk_norm_rope_grid_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
+                             const vk_tensor* q_gamma, const vk_tensor* q_beta,
+                             const vk_tensor* k_gamma, const vk_tensor* k_beta, size_t heads,
+                             size_t head_dim, size_t n_special, size_t gh, size_t gw,
+                             size_t view_count, int global, vk_qk_layout layout, float freq,
+                             float eps) {
+  return vk_qk_norm_rope_grid_mode_f32(rt, q, k, q_gamma, q_beta, k_gamma, k_beta, heads,
+                                       head_dim, n_special, gh, gw, view_count, global, layout,
+                                       freq, eps, VK_ROPE_DEFAULT);
 }
 
 int vk_rope_positions_f32(vk_runtime* rt, size_t n_special, size_t gh, size_t gw,

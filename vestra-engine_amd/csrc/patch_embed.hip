@@ -1095,7 +1095,23 @@ int vk_linear_run_qkv_hnd_norm_rope_f32(vk_runtime* rt, const vk_linear* lin,
                                         const vk_tensor* k_beta, size_t n_special, size_t gh,
                                         size_t gw, size_t view_count, int global, float freq,
                                         float eps) {
+  return vk_linear_run_qkv_hnd_norm_rope_mode_f32(rt, lin, x, rows, heads, head_dim, q, k, v,
+                                                  q_gamma, q_beta, k_gamma, k_beta, n_special,
+                                                  gh, gw, view_count, global, freq, eps,
+                                                  VK_ROPE_DEFAULT);
+}
+
+int vk_linear_run_qkv_hnd_norm_rope_mode_f32(vk_runtime* rt, const vk_linear* lin,
+                                             const vk_tensor* x, size_t rows, size_t heads,
+                                             size_t head_dim, vk_tensor* q, vk_tensor* k,
+                                             vk_tensor* v, const vk_tensor* q_gamma,
+                                             const vk_tensor* q_beta, const vk_tensor* k_gamma,
+                                             const vk_tensor* k_beta, size_t n_special,
+                                             size_t gh, size_t gw, size_t view_count,
+                                             int global, float freq, float eps,
+                                             unsigned rope_mode) {
   VK_TRY(vk::bind(rt));
+  VK_TRY(vk::check_rope_mode(rope_mode));
   VK_REQUIRE(lin && x && q && k && v, "null argument");
   VK_UNSUPPORTED_IF(head_dim != 64, "qkv norm_rope: head_dim=%zu (qualified: 64)", head_dim);
   VK_REQUIRE(view_count > 0 && gw > 0, "view_count and gw must be > 0");
@@ -1132,7 +1148,8 @@ int vk_linear_run_qkv_hnd_norm_rope_f32(vk_runtime* rt, const vk_linear* lin,
   VK_UNSUPPORTED_IF(max_coord > (1u << 22), "patch grid %zux%zu too large", gh, gw);
   const float* table = nullptr;
   int table_max = 0;
-  VK_TRY(vk::rope_table(rt, freq, 64, static_cast<int>(max_coord), &table, &table_max));
+  VK_TRY(vk::rope_table(rt, freq, 64, rope_mode, static_cast<int>(max_coord), &table,
+                        &table_max));
   LinearArgs g = linear_args(lin, x, rows, nullptr);
   g.q_out = static_cast<float*>(q->ptr);
   g.k_out = static_cast<float*>(k->ptr);
@@ -1149,6 +1166,7 @@ int vk_linear_run_qkv_hnd_norm_rope_f32(vk_runtime* rt, const vk_linear* lin,
   g.qkn.tpv = vkd::make_fastdiv(static_cast<uint32_t>(n_special + gh * gw));
   g.qkn.gw = vkd::make_fastdiv(static_cast<uint32_t>(gw));
   g.qkn.eps = eps;
+  g.qkn.interleaved = (rope_mode & VK_ROPE_INTERLEAVED) ? 1u : 0u;
   return vk::launch_linear_wide(rt, g, kLinStore);
 }
 

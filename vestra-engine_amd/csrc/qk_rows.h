@@ -8,10 +8,18 @@
 
 namespace vkq {
 
-enum PosMode { kPosExplicit = 0, kPosGrid = 1 };
+// Where a row's position comes from: a positions tensor [tokens*2] (y, x)
+// of f32 (the CUDA runtime's device encoding), i32 or i64 (the CPU kernels'
+// integer positions), or the patch grid.
+enum PosMode { kPosExplicit = 0, kPosGrid = 1, kPosExplicitI32 = 2, kPosExplicitI64 = 3 };
+
+// RoPE pairing inside each 32-wide half: element j with j + 16 (rotate-half)
+// or element 2i with 2i + 1 (interleaved).
+enum Pairing { kRotateHalf = 0, kInterleaved = 1 };
 
 struct QkShape {
   uint32_t rows_per_tensor;  // heads * total tokens; 2 * rows_per_tensor < 2^31
+  uint32_t tensors;          // 2: Q then K; 1: Q only (the rotation of one tensor)
   int table_max;             // largest position the cos/sin table covers
   uint32_t n_special;
   uint32_t global;
@@ -22,22 +30,20 @@ struct QkShape {
   vkd::FastDivU32 gw;        // patch grid width
 };
 
-// cos/sin of the four frequencies j0..j0+3 for a coordinate outside the
+// cos/sin of the frequencies j0..j0+NF-1 for a coordinate outside the
 // table: angle rounded in f32, trig in double, as the host table does.  Only
-// the explicit-position form can meet such a coordinate (grid forms size the
-// table on the host); kept out of line so its double-precision trig does not
-// inflate the register footprint of the streaming path.
-__device__ __noinline__ void rope_cs_slow4(const float* __restrict__ table, int table_max,
-                                           int p, int j0, float4* c, float4* s) {
-  float cv[4], sv[4];
-  for (int u = 0; u < 4; ++u) {
+// the explicit-position forms can meet such a coordinate (grid forms size
+// the table on the host); kept out of line so its double-precision trig does
+// not inflate the register footprint of the streaming path.
+template <int NF>
+__device__ __noinline__ void rope_cs_slow(const float* __restrict__ table, int table_max, int p,
+                                          int j0, float* cv, float* sv) {
+  for (int u = 0; u < NF; ++u) {
     const float inv_freq = table[static_cast<size_t>(table_max + 1) * 32 + j0 + u];
     const float angle = static_cast<float>(p) * inv_freq;
     cv[u] = static_cast<float>(cos(static_cast<double>(angle)));
     sv[u] = static_cast<float>(sin(static_cast<double>(angle)));
   }
-  *c = make_float4(cv[0], cv[1], cv[2], cv[3]);
-  *s = make_float4(sv[0], sv[1], sv[2], sv[3]);
 }
 
 __device__ __forceinline__ float4 swizzle_xor4(float4 v) {
@@ -74,7 +80,7 @@ __device__ __forceinline__ void grid_position(uint32_t lt, uint32_t n_special, u
 // index math is 32-bit with multiply-shift division by the shape constants.
 template <int POS>
 __device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
-                                                const float* __restrict__ pos_yx, int* py,
+                                                const void* __restrict__ pos_yx, int* py,
                                                 int* px) {
   uint32_t t;   // index in the position sequence
   uint32_t lt;  // index inside its view
@@ -90,16 +96,27 @@ __device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
   *px = 0;
   if (POS == kPosExplicit) {
     // the reference's f32 device encoding, truncated like `value as i64`
-    *py = static_cast<int>(pos_yx[2 * static_cast<size_t>(t)]);
-    *px = static_cast<int>(pos_yx[2 * static_cast<size_t>(t) + 1]);
+    const float* p = static_cast<const float*>(pos_yx);
+    *py = static_cast<int>(p[2 * static_cast<size_t>(t)]);
+    *px = static_cast<int>(p[2 * static_cast<size_t>(t) + 1]);
+  } else if (POS == kPosExplicitI32) {
+    const int2 p = static_cast<const int2*>(pos_yx)[t];
+    *py = p.x;
+    *px = p.y;
+  } else if (POS == kPosExplicitI64) {
+    const long long* p = static_cast<const long long*>(pos_yx);
+    *py = static_cast<int>(p[2 * static_cast<size_t>(t)]);
+    *px = static_cast<int>(p[2 * static_cast<size_t>(t) + 1]);
   } else {
     grid_position(lt, sh.n_special, sh.global, sh.gw, py, px);
   }
 }
 
 // LayerNorm of one 64-wide row held as one float4 per lane of a 16-lane DPP
-// row, then its 2D rotation.
-template <typename PT, bool HAS_NORM, int POS>
+// row, then its 2D rotation.  Lanes 0-7 hold the y half (elements 0..31),
+// lanes 8-15 the x half.  Every rotated pair (a, b) with angle frequency j
+// becomes (a*cos - b*sin, b*cos + a*sin), each product rounded, then the sum.
+template <typename PT, bool HAS_NORM, int POS, int PAIR>
 __device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
                                                    const PT* __restrict__ b, int py, int px,
                                                    const float* __restrict__ table,
@@ -126,33 +143,57 @@ __device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __
     v.z = (v.z - mean) * inv * gv.z + bv.z;
     v.w = (v.w - mean) * inv * gv.w + bv.w;
   }
-  // RoPE.  Lanes 0-7 hold the y half (elements 0..31), lanes 8-15 the x half.
-  // Inside a half, lanes with bit 2 clear hold elements j (j < 16) and rotate
-  // against the lane 4 above, which holds element j + 16.
   const int coord = (l < 8) ? py : px;
-  const int j0 = (l & 3) * 4;
-  float4 c, s;
-  if (POS == kPosGrid || (coord >= 0 && coord <= table_max)) {
-    const float* e = table + static_cast<size_t>(coord) * 32;
-    c = *reinterpret_cast<const float4*>(e + j0);
-    s = *reinterpret_cast<const float4*>(e + 16 + j0);
-  } else {
-    rope_cs_slow4(table, table_max, coord, j0, &c, &s);
-  }
-  const float4 p = swizzle_xor4(v);
+  const bool in_table = POS == kPosGrid || (coord >= 0 && coord <= table_max);
+  const float* e = table + static_cast<size_t>(in_table ? coord : 0) * 32;
   float4 o;
-  if ((l & 4) == 0) {
-    // out[j] = x[j]*cos - x[j+16]*sin
-    o.x = v.x * c.x + (-p.x) * s.x;
-    o.y = v.y * c.y + (-p.y) * s.y;
-    o.z = v.z * c.z + (-p.z) * s.z;
-    o.w = v.w * c.w + (-p.w) * s.w;
+  if (PAIR == kRotateHalf) {
+    // Inside a half, lanes with bit 2 clear hold elements j (j < 16) and
+    // rotate against the lane 4 above, which holds element j + 16; both use
+    // frequencies j0..j0+3.
+    const int j0 = (l & 3) * 4;
+    float4 c, s;
+    if (in_table) {
+      c = *reinterpret_cast<const float4*>(e + j0);
+      s = *reinterpret_cast<const float4*>(e + 16 + j0);
+    } else {
+      float cv[4], sv[4];
+      rope_cs_slow<4>(table, table_max, coord, j0, cv, sv);
+      c = make_float4(cv[0], cv[1], cv[2], cv[3]);
+      s = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    }
+    const float4 p = swizzle_xor4(v);
+    if ((l & 4) == 0) {
+      // out[j] = x[j]*cos - x[j+16]*sin
+      o.x = v.x * c.x + (-p.x) * s.x;
+      o.y = v.y * c.y + (-p.y) * s.y;
+      o.z = v.z * c.z + (-p.z) * s.z;
+      o.w = v.w * c.w + (-p.w) * s.w;
+    } else {
+      // out[j+16] = x[j+16]*cos + x[j]*sin
+      o.x = v.x * c.x + p.x * s.x;
+      o.y = v.y * c.y + p.y * s.y;
+      o.z = v.z * c.z + p.z * s.z;
+      o.w = v.w * c.w + p.w * s.w;
+    }
   } else {
-    // out[j+16] = x[j+16]*cos + x[j]*sin
-    o.x = v.x * c.x + p.x * s.x;
-    o.y = v.y * c.y + p.y * s.y;
-    o.z = v.z * c.z + p.z * s.z;
-    o.w = v.w * c.w + p.w * s.w;
+    // The lane's four elements 4m..4m+3 of its half (m = l & 7) are the two
+    // pairs 2m and 2m + 1: frequencies j0 = 2m and j0 + 1, no lane exchange.
+    const int j0 = (l & 7) * 2;
+    float2 c, s;
+    if (in_table) {
+      c = *reinterpret_cast<const float2*>(e + j0);
+      s = *reinterpret_cast<const float2*>(e + 16 + j0);
+    } else {
+      float cv[2], sv[2];
+      rope_cs_slow<2>(table, table_max, coord, j0, cv, sv);
+      c = make_float2(cv[0], cv[1]);
+      s = make_float2(sv[0], sv[1]);
+    }
+    o.x = v.x * c.x + (-v.y) * s.x;
+    o.y = v.y * c.x + v.x * s.x;
+    o.z = v.z * c.y + (-v.w) * s.y;
+    o.w = v.w * c.y + v.z * s.y;
   }
   return o;
 }

@@ -346,7 +346,7 @@ int vk_preprocess_resize_u8(vk_runtime* rt, const vk_tensor* src, size_t h, size
   // when no snap follows
   uint8_t* first = l.mode2 < 0 ? dst : mid;
   if (l.mode1 < 0) {
-    VK_HIP(hipMemcpyAsync(first, in, h * w * 3, hipMemcpyDeviceToDevice, rt->stream));
+    VK_TRY(vk::device_copy(rt, first, in, h * w * 3));
   } else {
     VK_TRY(enqueue_resize(rt, in, h, w, first, s.bh, s.bw, l.mode1, tmp1));
   }

@@ -6,6 +6,7 @@
 // 161-184, 335, 370, 402-478 and backbone.rs:991-1027).
 #include <cmath>
 #include <cstring>
+#include <tuple>
 #include <vector>
 
 #include "common.h"
@@ -37,6 +38,8 @@ size_t dtype_size(vk_dtype d) {
     case VK_F32: return 4;
     case VK_F16: return 2;
     case VK_U8: return 1;
+    case VK_I32: return 4;
+    case VK_I64: return 8;
   }
   return 0;
 }
@@ -61,19 +64,30 @@ int check_launch(const char* what) {
   return VK_OK;
 }
 
+int check_rope_mode(unsigned rope_mode) {
+  VK_REQUIRE((rope_mode & ~(VK_ROPE_INTERLEAVED | VK_ROPE_EXP_HEAD)) == 0,
+             "unknown RoPE convention flags 0x%x", rope_mode);
+  return VK_OK;
+}
+
 // Host build of the RoPE cos/sin table for head_dim 64 (two rotary halves of
-// 32, 16 frequency pairs each).  inv_freq_j = 1 / base^((2j)/32), each step in
-// f32; angle = (f32)p * inv_freq_j as one f32 product; cos/sin evaluated in
-// double and rounded once (the published RotaryPositionEmbedding2D of
-// Depth-Anything-3 computes the same f32 angle).
-int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const float** out,
-               int* table_max) {
+// 32, 16 frequency pairs each).  inv_freq_j = 1 / base^((2j)/32) (exponent
+// over the half, the default), or 1 / base^((2j)/64) with VK_ROPE_EXP_HEAD,
+// each step in f32; angle = (f32)p * inv_freq_j as one f32 product; cos/sin
+// evaluated in double and rounded once (the published
+// RotaryPositionEmbedding2D of Depth-Anything-3 computes the same f32
+// angle).  The pairing does not change the table: frequency j belongs to
+// pair (j, j+16) or (2j, 2j+1).
+int rope_table(vk_runtime* rt, float freq, int head_dim, unsigned rope_mode, int min_max_pos,
+               const float** out, int* table_max) {
   VK_UNSUPPORTED_IF(head_dim != 64, "RoPE table supports head_dim 64 (got %d)", head_dim);
   VK_UNSUPPORTED_IF(min_max_pos > (1 << 22), "RoPE positions up to %d exceed the table limit",
                     min_max_pos);
+  VK_TRY(check_rope_mode(rope_mode));
+  const bool exp_head = (rope_mode & VK_ROPE_EXP_HEAD) != 0;
   uint32_t fbits;
   std::memcpy(&fbits, &freq, sizeof fbits);
-  auto key = std::make_pair(fbits, head_dim);
+  auto key = std::make_tuple(fbits, head_dim, exp_head ? 1 : 0);
   auto it = rt->rope_tables.find(key);
   if (it != rt->rope_tables.end() && it->second.second >= min_max_pos) {
     *out = it->second.first;
@@ -84,8 +98,10 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, int min_max_pos, const 
   const int half = head_dim / 2;
   const int quarter = half / 2;
   std::vector<float> inv_freq(quarter);
+  // exponent denominator: the rotary half's width, or the whole head
+  const float denom = static_cast<float>(exp_head ? head_dim : half);
   for (int j = 0; j < quarter; ++j) {
-    const float e = static_cast<float>(2 * j) / static_cast<float>(half);
+    const float e = static_cast<float>(2 * j) / denom;
     inv_freq[j] = 1.0f / std::pow(freq, e);
   }
   const size_t entries = static_cast<size_t>(max_pos) + 1;
@@ -156,10 +172,58 @@ int ensure_work(vk_runtime* rt, size_t floats, const char* who) {
   return VK_OK;
 }
 
+// Device-to-device copies as kernels: 16-byte, 4-byte or 1-byte elements,
+// the widest that both ends and the length are aligned to.  Grid-stride
+// loops over at most 4096 workgroups of 256 threads.
+template <typename T>
+__global__ void copy_elems_kernel(T* __restrict__ dst, const T* __restrict__ src, size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride)
+    dst[i] = src[i];
+}
+
+// One workgroup per view: row v * tpv of tokens <- camera slot (v > 0).
+__global__ void camera_rows_kernel(float* __restrict__ tokens, const float* __restrict__ camera,
+                                   size_t tpv, size_t D) {
+  const size_t v = blockIdx.x;
+  const float* src = camera + (v > 0 ? D : 0);
+  float* dst = tokens + v * tpv * D;
+  for (size_t c = threadIdx.x; c < D; c += blockDim.x) dst[c] = src[c];
+}
+
+int device_copy(vk_runtime* rt, void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return VK_OK;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes;
+  const size_t unit = (a & 15) == 0 ? 16 : (a & 3) == 0 ? 4 : 1;
+  const size_t n = bytes / unit;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  if (unit == 16)
+    hipLaunchKernelGGL(copy_elems_kernel<uint4>, grid, block, 0, rt->stream,
+                       static_cast<uint4*>(dst), static_cast<const uint4*>(src), n);
+  else if (unit == 4)
+    hipLaunchKernelGGL(copy_elems_kernel<uint32_t>, grid, block, 0, rt->stream,
+                       static_cast<uint32_t*>(dst), static_cast<const uint32_t*>(src), n);
+  else
+    hipLaunchKernelGGL(copy_elems_kernel<uint8_t>, grid, block, 0, rt->stream,
+                       static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), n);
+  return check_launch("device copy");
+}
+
+int write_camera_rows(vk_runtime* rt, float* tokens, const float* camera, size_t view_count,
+                      size_t tokens_per_view, size_t D) {
+  if (view_count == 0 || D == 0) return VK_OK;
+  VK_UNSUPPORTED_IF(view_count > 0x7fffffffULL, "camera write: %zu views", view_count);
+  hipLaunchKernelGGL(camera_rows_kernel, dim3(static_cast<unsigned>(view_count)), dim3(256), 0,
+                     rt->stream, tokens, camera, tokens_per_view, D);
+  return check_launch("camera_rows_kernel");
+}
+
 static int new_tensor(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** out) {
   VK_REQUIRE(out != nullptr, "null output handle");
-  VK_REQUIRE(dtype == VK_F32 || dtype == VK_F16 || dtype == VK_U8,
-             "unknown dtype %d", static_cast<int>(dtype));
+  VK_REQUIRE(dtype_size(dtype) != 0, "unknown dtype %d", static_cast<int>(dtype));
   VK_TRY(bind(rt));
   void* p = nullptr;
   if (len > 0) VK_HIP(hipMalloc(&p, len * dtype_size(dtype)));
@@ -299,6 +363,14 @@ int vk_upload_u8(vk_runtime* rt, const uint8_t* host, size_t len, vk_tensor** ou
   return upload(rt, VK_U8, host, len, out);
 }
 
+int vk_upload_i32(vk_runtime* rt, const int32_t* host, size_t len, vk_tensor** out) {
+  return upload(rt, VK_I32, host, len, out);
+}
+
+int vk_upload_i64(vk_runtime* rt, const int64_t* host, size_t len, vk_tensor** out) {
+  return upload(rt, VK_I64, host, len, out);
+}
+
 static int write_host(vk_runtime* rt, vk_tensor* t, vk_dtype dtype,
                       const void* host, size_t len) {
   VK_REQUIRE(t != nullptr && (host != nullptr || len == 0), "null tensor or host pointer");
@@ -355,13 +427,10 @@ int vk_copy_segment_f32(vk_runtime* rt, const vk_tensor* src, size_t offset,
              "segment [%zu, +%zu) outside tensor of %zu", offset, len, src->len);
   vk_tensor* t = nullptr;
   VK_TRY(new_tensor(rt, VK_F32, len, &t));
-  if (len > 0) {
-    hipError_t e = hipMemcpyAsync(t->ptr, static_cast<const float*>(src->ptr) + offset,
-                                  len * 4, hipMemcpyDeviceToDevice, rt->stream);
-    if (e != hipSuccess) {
-      vk_tensor_destroy(t);
-      return hip_fail(e, "copy_segment");
-    }
+  const int s = device_copy(rt, t->ptr, static_cast<const float*>(src->ptr) + offset, len * 4);
+  if (s != VK_OK) {
+    vk_tensor_destroy(t);
+    return s;
   }
   *out = t;
   return VK_OK;
@@ -377,11 +446,8 @@ int vk_copy_segment_into_f32(vk_runtime* rt, vk_tensor* dst, size_t dst_offset,
              "destination segment [%zu, +%zu) outside tensor of %zu", dst_offset, len,
              dst->len);
   VK_TRY(bind(rt));
-  if (len == 0) return VK_OK;
-  VK_HIP(hipMemcpyAsync(static_cast<float*>(dst->ptr) + dst_offset,
-                        static_cast<const float*>(src->ptr) + src_offset, len * 4,
-                        hipMemcpyDeviceToDevice, rt->stream));
-  return VK_OK;
+  return device_copy(rt, static_cast<float*>(dst->ptr) + dst_offset,
+                     static_cast<const float*>(src->ptr) + src_offset, len * 4);
 }
 
 int vk_overwrite_prefix_f32(vk_runtime* rt, vk_tensor* tokens, const vk_tensor* prefix,
@@ -445,6 +511,8 @@ int vk_graph_end_capture(vk_runtime* rt, vk_graph** out) {
     return hip_fail(e, "hipGraphInstantiate");
   }
   auto* vg = new vk_graph;
+  vg->rt = rt;
+  retain(rt);
   vg->graph = g;
   vg->exec = exec;
   *out = vg;
@@ -452,7 +520,10 @@ int vk_graph_end_capture(vk_runtime* rt, vk_graph** out) {
 }
 
 int vk_graph_launch(vk_runtime* rt, vk_graph* g) {
-  VK_REQUIRE(g != nullptr, "null graph");
+  VK_REQUIRE(g != nullptr && g->exec != nullptr, "null graph");
+  // a graph's nodes use its runtime's work buffer and tables: it runs on
+  // that runtime's stream only, and not after the runtime was destroyed
+  VK_REQUIRE(rt == g->rt, "graph was captured on another runtime");
   VK_TRY(bind(rt));
   VK_HIP(hipGraphLaunch(g->exec, rt->stream));
   return VK_OK;
@@ -460,9 +531,15 @@ int vk_graph_launch(vk_runtime* rt, vk_graph* g) {
 
 int vk_graph_destroy(vk_graph* g) {
   if (!g) return VK_OK;
-  (void)hipGraphExecDestroy(g->exec);
-  (void)hipGraphDestroy(g->graph);
+  vk_runtime* rt = g->rt;
+  if (bind_device(rt) == VK_OK) {
+    // launches still queued on the stream finish before their exec goes
+    (void)hipStreamSynchronize(rt->stream);
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+  }
   delete g;
+  release(rt);
   return VK_OK;
 }
 

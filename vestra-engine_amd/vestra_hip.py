@@ -29,7 +29,11 @@ VK_ERR_UNSUPPORTED = -2
 VK_ERR_HIP = -3
 VK_ERR_OOM = -4
 
-VK_F32, VK_F16, VK_U8 = 0, 1, 2
+VK_F32, VK_F16, VK_U8, VK_I32, VK_I64 = 0, 1, 2, 3, 4
+# 2D RoPE convention flags (pairing | exponent); 0 is the default
+VK_ROPE_ROTATE_HALF, VK_ROPE_INTERLEAVED = 0, 1
+VK_ROPE_EXP_HALF, VK_ROPE_EXP_HEAD = 0, 2
+VK_ROPE_DEFAULT = 0
 VK_QK_HEADS_OUTER, VK_QK_VIEWS_OUTER = 0, 1
 VK_RESIZE_BILINEAR, VK_RESIZE_CUBIC, VK_RESIZE_AREA = 0, 1, 2
 
@@ -72,7 +76,7 @@ class VitConfig(C.Structure):
     _fields_ = [("embed_dim", _sz), ("num_heads", _sz), ("head_dim", _sz),
                 ("mlp_hidden", _sz), ("num_register", _sz), ("ln_eps", _f),
                 ("qk_norm_eps", _f), ("rope_freq", _f), ("rope_start", _i),
-                ("qknorm_start", _i), ("alt_start", _i)]
+                ("qknorm_start", _i), ("alt_start", _i), ("rope_mode", C.c_uint)]
 
 
 class VitLayer(C.Structure):
@@ -113,6 +117,8 @@ _SIGS = {
     "vk_upload_f32": ([_vp, _vp, _sz, _pp], _i),
     "vk_upload_f16": ([_vp, _vp, _sz, _pp], _i),
     "vk_upload_u8": ([_vp, _vp, _sz, _pp], _i),
+    "vk_upload_i32": ([_vp, _vp, _sz, _pp], _i),
+    "vk_upload_i64": ([_vp, _vp, _sz, _pp], _i),
     "vk_write_f32": ([_vp, _vp, _vp, _sz], _i),
     "vk_write_u8": ([_vp, _vp, _vp, _sz], _i),
     "vk_download_f32": ([_vp, _vp, _vp, _sz], _i),
@@ -131,8 +137,14 @@ _SIGS = {
     "vk_layerscale_residual_layernorm_f32": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _vp], _i),
     "vk_qk_norm_rope_f32": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _f], _i),
+    "vk_qk_norm_rope_mode_f32": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _f, C.c_uint], _i),
+    "vk_rope2d_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _f, C.c_uint], _i),
     "vk_qk_norm_rope_grid_f32": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i, _f, _f], _i),
+    "vk_qk_norm_rope_grid_mode_f32": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i, _f, _f,
+         C.c_uint], _i),
     "vk_rope_positions_f32": ([_vp, _sz, _sz, _sz, _sz, _i, _pp], _i),
     "vk_patchify_nchw_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _pp], _i),
     "vk_linear_prepare_f32": ([_vp, _sz, _sz, _vp, _vp, _vp, _pp], _i),
@@ -153,6 +165,9 @@ _SIGS = {
     "vk_linear_run_qkv_hnd_norm_rope_f32": (
         [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _i,
          _f, _f], _i),
+    "vk_linear_run_qkv_hnd_norm_rope_mode_f32": (
+        [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _i,
+         _f, _f, C.c_uint], _i),
     "vk_linear_run_hnd_into_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_linear_run_hnd_residual_f32": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
     "vk_split_qkv_hnd_f32": ([_vp, _vp, _sz, _sz, _sz, _pp, _pp, _pp], _i),
@@ -309,12 +324,16 @@ class Linear:
                               k_gamma: Optional[Tensor], k_beta: Optional[Tensor],
                               n_special: int, gh: int, gw: int, view_count: int,
                               global_layer: bool, freq: float = 100.0,
-                              eps: float = 1e-5) -> None:
-        """QKV projection storing head-major Q, K, V with Q/K-norm + RoPE fused."""
-        _check(lib.vk_linear_run_qkv_hnd_norm_rope_f32(
-            self.rt.handle, self.handle, x.handle, rows, heads, 64, q.handle, k.handle, v.handle,
-            _h(q_gamma), _h(q_beta), _h(k_gamma), _h(k_beta), n_special, gh, gw, view_count,
-            1 if global_layer else 0, freq, eps))
+                              eps: float = 1e-5, rope_mode: Optional[int] = None) -> None:
+        """QKV projection storing head-major Q, K, V with Q/K-norm + RoPE fused;
+        rope_mode None calls the default-convention entry point."""
+        args = (self.rt.handle, self.handle, x.handle, rows, heads, 64, q.handle, k.handle,
+                v.handle, _h(q_gamma), _h(q_beta), _h(k_gamma), _h(k_beta), n_special, gh, gw,
+                view_count, 1 if global_layer else 0, freq, eps)
+        if rope_mode is None:
+            _check(lib.vk_linear_run_qkv_hnd_norm_rope_f32(*args))
+        else:
+            _check(lib.vk_linear_run_qkv_hnd_norm_rope_mode_f32(*args, rope_mode))
 
     def run_hnd_residual(self, hnd: Tensor, rows: int, heads: int, residual: Tensor,
                          head_dim: int = 64) -> None:
@@ -409,6 +428,18 @@ class Runtime:
         h = np.ascontiguousarray(host, dtype=np.float16).reshape(-1).view(np.uint16)
         out = C.c_void_p()
         _check(lib.vk_upload_f16(self.handle, _ptr(h), h.size, C.byref(out)))
+        return Tensor(self, out)
+
+    def upload_i32(self, host: np.ndarray) -> Tensor:
+        h = np.ascontiguousarray(host, dtype=np.int32).reshape(-1)
+        out = C.c_void_p()
+        _check(lib.vk_upload_i32(self.handle, _ptr(h), h.size, C.byref(out)))
+        return Tensor(self, out)
+
+    def upload_i64(self, host: np.ndarray) -> Tensor:
+        h = np.ascontiguousarray(host, dtype=np.int64).reshape(-1)
+        out = C.c_void_p()
+        _check(lib.vk_upload_i64(self.handle, _ptr(h), h.size, C.byref(out)))
         return Tensor(self, out)
 
     def upload_u8(self, host: np.ndarray) -> Tensor:
@@ -585,16 +616,41 @@ class Runtime:
                                        _h(q_beta), _h(k_gamma), _h(k_beta), positions.handle,
                                        heads, rows, freq, eps))
 
+    def qk_norm_rope_mode_f32(self, q: Tensor, k: Tensor, q_gamma: Optional[Tensor],
+                              q_beta: Optional[Tensor], k_gamma: Optional[Tensor],
+                              k_beta: Optional[Tensor], positions: Tensor, heads: int,
+                              rows: int, freq: float = 100.0, eps: float = QK_NORM_EPS,
+                              rope_mode: int = VK_ROPE_DEFAULT) -> None:
+        """qk_norm_rope_f32_da3_base with positions of dtype f32, i32 or i64
+        and an explicit RoPE convention."""
+        _check(lib.vk_qk_norm_rope_mode_f32(self.handle, q.handle, k.handle, _h(q_gamma),
+                                            _h(q_beta), _h(k_gamma), _h(k_beta),
+                                            positions.handle, heads, rows, freq, eps,
+                                            rope_mode))
+
+    def rope2d_f32(self, x: Tensor, positions: Tensor, heads: int, rows: int,
+                   head_dim: int = 64, freq: float = 100.0,
+                   rope_mode: int = VK_ROPE_DEFAULT) -> None:
+        """vestra_kernels::rope2d in place on one head-major tensor."""
+        _check(lib.vk_rope2d_f32(self.handle, x.handle, positions.handle, heads, rows,
+                                 head_dim, freq, rope_mode))
+
     def qk_norm_rope_grid_f32(self, q: Tensor, k: Tensor, q_gamma: Optional[Tensor],
                               q_beta: Optional[Tensor], k_gamma: Optional[Tensor],
                               k_beta: Optional[Tensor], heads: int, head_dim: int,
                               n_special: int, gh: int, gw: int, view_count: int,
                               global_layer: bool, layout: int, freq: float = 100.0,
-                              eps: float = QK_NORM_EPS) -> None:
-        _check(lib.vk_qk_norm_rope_grid_f32(
-            self.handle, q.handle, k.handle, _h(q_gamma), _h(q_beta), _h(k_gamma), _h(k_beta),
-            heads, head_dim, n_special, gh, gw, view_count, 1 if global_layer else 0, layout,
-            freq, eps))
+                              eps: float = QK_NORM_EPS,
+                              rope_mode: Optional[int] = None) -> None:
+        """Grid-position Q/K-norm + RoPE; rope_mode None calls the
+        default-convention entry point."""
+        args = (self.handle, q.handle, k.handle, _h(q_gamma), _h(q_beta), _h(k_gamma),
+                _h(k_beta), heads, head_dim, n_special, gh, gw, view_count,
+                1 if global_layer else 0, layout, freq, eps)
+        if rope_mode is None:
+            _check(lib.vk_qk_norm_rope_grid_f32(*args))
+        else:
+            _check(lib.vk_qk_norm_rope_grid_mode_f32(*args, rope_mode))
 
     def rope_positions_f32(self, n_special: int, gh: int, gw: int, view_count: int,
                            global_layer: bool) -> Tensor:
