@@ -410,6 +410,20 @@ int vk_linear_run_qkv_hnd_norm_rope_mode_f32(
     const vk_tensor* q_gamma, const vk_tensor* q_beta, const vk_tensor* k_gamma,
     const vk_tensor* k_beta, size_t n_special, size_t gh, size_t gw,
     size_t view_count, int global, float freq, float eps, unsigned rope_mode);
+/* vk_linear_run_into_f32 that allocates nothing.  No counterpart in the
+ * reference: for callers that cannot call hipMalloc (a sequence captured
+ * into a HIP graph without an eager run first, serving loops, harnesses that
+ * forbid allocation).  The same plan and bits as vk_linear_run_into_f32;
+ * split-K partial sums (few rows: an 866-token image's FC2 needs 4 Mi
+ * floats) go to a static device array of 8 Mi floats (32 MiB, held by each
+ * device from the library's load until the process ends) instead of the
+ * runtime's work buffer.  A plan needing more than that fails with
+ * VK_ERR_UNSUPPORTED and enqueues nothing (e.g. 3,458 rows x 4096 -> 1024).
+ * Every call on one device shares the array: calls on one device that
+ * overlap in time (two runtimes' streams) race. */
+int vk_linear_run_into_noalloc_f32(vk_runtime* rt, const vk_linear* lin,
+                                   const vk_tensor* x, size_t rows,
+                                   vk_tensor* out);
 /* The output projection reading the head-major attention output
  * [heads, rows, 64] directly (in_features = heads*64): bit-identical to
  * vk_hnd_to_token_into_f32 followed by vk_linear_run_into_f32 /

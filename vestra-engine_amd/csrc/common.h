@@ -141,6 +141,9 @@ int rope_table(vk_runtime* rt, float freq, int head_dim, unsigned rope_mode, int
                const float** out, int* table_max);
 // VK_ERR_INVALID for RoPE convention flags other than VK_ROPE_*.
 int check_rope_mode(unsigned rope_mode);
+// Looks up, once per device and with that device current, the device
+// address of the allocation-free entry point's static scratch array.
+void noalloc_setup(int device);
 // Makes rt->work hold at least `floats` floats (at least 8 Mi once
 // allocated, doubling on growth).  Growth is refused during stream capture:
 // run the sequence once eagerly first.  The buffer it replaces is retired,
@@ -221,7 +224,11 @@ enum LinearEpilogue {
 // The wide-tile linear (128 x 128, 64 x 128 or 64 x 64 tiles, split-K for
 // few rows) for K % 4 == 0 and a 16-byte aligned x (linear.hip);
 // the head-major layouts of LinearArgs need it.
-int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi);
+// `partial` / `partial_floats`: the caller's buffer for split-K partial
+// sums (nothing is allocated; a plan that needs more is refused); null: the
+// runtime's work buffer, grown as needed.
+int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi, float* partial = nullptr,
+                       size_t partial_floats = 0);
 
 // LayerNorm of `rows` x `cols` f32 rows (the layernorm_rows kernel) on raw
 // pointers; gamma/beta f16 when `f16`.

@@ -616,7 +616,8 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 gri
 
 }  // namespace
 
-int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
+int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi, float* partial,
+                       size_t partial_floats) {
   LinearArgs g = g0;
   // An output element's bits depend on the split count only, so the plan
   // depends on (M, N, K) alone and every layout and epilogue of one shape
@@ -630,8 +631,17 @@ int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi) {
                     "linear: operands of 4 GiB or more (M=%d, N=%d, K=%d)", g.M, g.N, g.K);
   if (g.splits > 1) {
     VK_REQUIRE(g.N % 4 == 0, "linear: split-K needs out_features % 4 == 0");
-    VK_TRY(vk::ensure_work(rt, static_cast<size_t>(g.splits) * g.M * g.N, "linear (split-K)"));
-    g.partial = rt->work;
+    const size_t need = static_cast<size_t>(g.splits) * g.M * g.N;
+    if (partial) {
+      VK_UNSUPPORTED_IF(need > partial_floats,
+                        "linear (M=%d, N=%d, K=%d): %d split-K slices need %zu floats of "
+                        "scratch, more than the %zu available",
+                        g.M, g.N, g.K, g.splits, need, partial_floats);
+      g.partial = partial;
+    } else {
+      VK_TRY(vk::ensure_work(rt, need, "linear (split-K)"));
+      g.partial = rt->work;
+    }
   }
   const dim3 grid(static_cast<unsigned>(plan.tiles * g.splits));
   // LayerNorm after the residual epilogue: in the sum pass when there is

@@ -680,7 +680,8 @@ int check_head_layout(const vk_linear* lin, const vk_tensor* x, size_t heads, si
 }
 
 int launch_linear(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
-                  vk_tensor* out, int epi) {
+                  vk_tensor* out, int epi, float* partial = nullptr,
+                  size_t partial_floats = 0) {
   if (rows == 0) return VK_OK;
   LinearArgs g{};
   g.x = static_cast<const float*>(x->ptr);
@@ -695,7 +696,7 @@ int launch_linear(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size
   // 128x128 tiles wherever rows of x can be read as float4; the 48x64 kernel
   // (scalar loads of x) for the rest
   if (g.K % 4 == 0 && reinterpret_cast<uintptr_t>(g.x) % 16 == 0)
-    return vk::launch_linear_wide(rt, g, epi);
+    return vk::launch_linear_wide(rt, g, epi, partial, partial_floats);
   const unsigned tiles = static_cast<unsigned>(((g.M + BM - 1) / BM) * static_cast<long long>((g.N + BN - 1) / BN));
   const dim3 grid(tiles), block(kThreads);
   switch (epi) {
@@ -1335,6 +1336,73 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t
   hipLaunchKernelGGL(patch_embed_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kPeThreads), 0,
                      rt->stream, a);
   return vk::check_launch("patch_embed_kernel");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free linear: vk_linear_run_into_f32 with the split-K partial
+// sums in a static device array instead of the runtime's work buffer.
+//
+// `scratch` is a file-scope device array: each device holds its own copy
+// from the library's load until the process ends.  Host code never uses its
+// name as an address (on the host it is a stand-in symbol): the device
+// address is looked up once per device, with that device current, when a
+// runtime is created on it (vk_runtime_create -> vk::noalloc_setup), and
+// only that address is handed to kernels.  Every call on one device shares
+// that device's array; each split writes its whole slice before the sum
+// pass reads it, so nothing needs clearing, but calls that overlap on one
+// device (two runtimes' streams at once) race on it.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchFloats = size_t{8} << 20;  // 32 MiB per device
+
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+bool g_scratch_done[kMaxDevices] = {};
+
+}  // namespace
+
+namespace vk {
+
+void noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_done[device]) return;
+  void* p = nullptr;
+  // the caller (vk_runtime_create) made `device` current
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  g_scratch_err[device] = e;
+  g_scratch_ptr[device] = e == hipSuccess ? static_cast<float*>(p) : nullptr;
+  g_scratch_done[device] = true;
+}
+
+}  // namespace vk
+
+extern "C" {
+
+int vk_linear_run_into_noalloc_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                                   size_t rows, vk_tensor* out) {
+  VK_TRY(vk::bind(rt));
+  VK_REQUIRE(lin && x && out, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
+  float* sp = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    VK_REQUIRE(rt->device < kMaxDevices && g_scratch_done[rt->device],
+               "linear_run_into_noalloc: no scratch address for device %d", rt->device);
+    if (g_scratch_err[rt->device] != hipSuccess)
+      return vk::hip_fail(g_scratch_err[rt->device], "hipGetSymbolAddress(scratch)");
+    sp = g_scratch_ptr[rt->device];
+  }
+  return launch_linear(rt, lin, x, rows, out, kLinStore, sp, kScratchFloats);
 }
 
 }  // extern "C"

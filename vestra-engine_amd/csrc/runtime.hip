@@ -276,6 +276,8 @@ int vk_runtime_create(int device, vk_runtime** out) {
   VK_HIP(hipSetDevice(device));
   hipDeviceProp_t prop;
   VK_HIP(hipGetDeviceProperties(&prop, device));
+  // with `device` current: the allocation-free entry point's scratch address
+  vk::noalloc_setup(device);
   auto* rt = new vk_runtime;
   rt->device = device;
   rt->cu_count = prop.multiProcessorCount;

@@ -158,6 +158,7 @@ _SIGS = {
     "vk_linear_input_features": ([_vp], _sz),
     "vk_linear_run_f32": ([_vp, _vp, _vp, _sz, _pp], _i),
     "vk_linear_run_into_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
+    "vk_linear_run_into_noalloc_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_gelu_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_gelu_erf_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
     "vk_linear_run_residual_f32": ([_vp, _vp, _vp, _sz, _vp], _i),
@@ -301,6 +302,12 @@ class Linear:
 
     def run_into(self, x: Tensor, rows: int, out: Tensor) -> None:
         _check(lib.vk_linear_run_into_f32(self.rt.handle, self.handle, x.handle, rows, out.handle))
+
+    def run_into_noalloc(self, x: Tensor, rows: int, out: Tensor) -> None:
+        """run_into with split-K partial sums in the library's static device
+        scratch: allocates nothing."""
+        _check(lib.vk_linear_run_into_noalloc_f32(self.rt.handle, self.handle, x.handle, rows,
+                                                  out.handle))
 
     def run_gelu(self, x: Tensor, rows: int, out: Tensor, exact_erf: bool = False) -> None:
         """FC1 + GELU: out = GELU(x W + b); A&S erf, or the device erff."""
