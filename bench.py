@@ -292,14 +292,43 @@ def dispatch_overhead(rt, launches=100):
 
 
 def cpu_model():
+    """Host CPU identification from /proc/cpuinfo: model name, vendor,
+    family/model/stepping, logical and physical core counts, AVX-512."""
+    info = {}
+    cores = set()
+    logical = 0
     try:
         with open("/proc/cpuinfo") as f:
+            phys = core = None
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if phys is not None or core is not None:
+                        cores.add((phys, core))
+                    phys = core = None
+                    continue
+                k, v = (t.strip() for t in line.split(":", 1))
+                if k == "processor":
+                    logical += 1
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif k in ("model name", "vendor_id", "cpu family", "model", "stepping") and \
+                        k not in info:
+                    info[k] = v
+                elif k == "flags" and "avx512" not in info:
+                    info["avx512"] = sorted(x for x in v.split() if x.startswith("avx512"))
+            if phys is not None or core is not None:
+                cores.add((phys, core))
     except OSError:
-        pass
-    return None
+        return None
+    info["logical_cpus"] = logical
+    info["physical_cores"] = len(cores) or None
+    try:
+        info["granted_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["granted_cpus"] = None
+    return info
 
 
 def linear_epilogue_timing(rt, rng, rows, iters):
@@ -654,61 +683,105 @@ def patch_embed_timing(rt, rng, h, w, embed, iters):
 
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(model, seconds, threads):
-    """The oracle (scalar C restatement, OpenMP over rows) timed on the host
-    on one block's fused operations over the same 12-view rows."""
+    """One block's fused operations (LN1, Q/K-norm + RoPE per view, LS1 +
+    residual, LN2, GELU, LS2 + residual) over the same 12-view rows on the
+    host: the AVX-512 + OpenMP restatement (oracle/cpu_simd.c, the stand-in
+    for the reference's AVX-512 kernels) at `threads` threads and at every
+    CPU the box grants this process, and the scalar oracle on one thread."""
     import ctypes as C
 
     import oracle
-    oracle.set_threads(threads)
-    lib = oracle.lib
+    import oracle.simd as simd
     r = model.rows
-    a = {k: np.array(v, copy=True) for k, v in model.host_act.items()}
-    ln1, ln2 = np.empty((r, D), np.float32), np.empty((r, D), np.float32)
     lay = model.host_layers[0]
     pos = oracle.rope_positions(NREG + 1, GH, GW, model.views, False)
-    p = oracle._p
+    nbytes = ln_bytes(r) * 2 + qk_bytes(r) + lsres_bytes(r) * 2 + gelu_bytes(r)
 
-    def one_block():
-        lib.ora_layernorm_f32(p(a["tokens"]), p(ln1), r, D, p(lay["norm1_gamma"]),
-                              p(lay["norm1_beta"]), C.c_float(1e-6))
-        qv = a["q"].reshape(model.views, H * TPV * HD)
-        kv = a["k"].reshape(model.views, H * TPV * HD)
+    def fresh():
+        a = {k: np.array(v, copy=True) for k, v in model.host_act.items()}
+        a["ln1"], a["ln2"] = np.empty((r, D), np.float32), np.empty((r, D), np.float32)
+        a["qv"] = a["q"].reshape(model.views, H * TPV * HD)
+        a["kv"] = a["k"].reshape(model.views, H * TPV * HD)
+        return a
+
+    pv = [np.ascontiguousarray(pos[v * TPV:(v + 1) * TPV]) for v in range(model.views)]
+
+    def simd_block(a):
+        simd.layernorm_into(a["tokens"], a["ln1"], lay["norm1_gamma"], lay["norm1_beta"], 1e-6)
         for v in range(model.views):
-            pv = np.ascontiguousarray(pos[v * TPV:(v + 1) * TPV])
-            lib.ora_qk_norm_rope_f32(p(qv[v]), p(kv[v]), p(lay["qnorm_gamma"]), p(lay["qnorm_beta"]),
-                                     p(lay["knorm_gamma"]), p(lay["knorm_beta"]), p(pv), H, TPV, HD,
+            simd.qk_norm_rope_(a["qv"][v], a["kv"][v], lay["qnorm_gamma"], lay["qnorm_beta"],
+                               lay["knorm_gamma"], lay["knorm_beta"], pv[v], H, TPV)
+        simd.layerscale_residual_(a["tokens"], a["attn_proj"], lay["ls1"])
+        simd.layernorm_into(a["tokens"], a["ln2"], lay["norm2_gamma"], lay["norm2_beta"], 1e-6)
+        simd.gelu_(a["hidden"])
+        simd.layerscale_residual_(a["tokens"], a["mlp_out"], lay["ls2"])
+
+    lib, p = oracle.lib, oracle._p
+
+    def scalar_block(a):
+        lib.ora_layernorm_f32(p(a["tokens"]), p(a["ln1"]), r, D, p(lay["norm1_gamma"]),
+                              p(lay["norm1_beta"]), C.c_float(1e-6))
+        for v in range(model.views):
+            lib.ora_qk_norm_rope_f32(p(a["qv"][v]), p(a["kv"][v]), p(lay["qnorm_gamma"]),
+                                     p(lay["qnorm_beta"]), p(lay["knorm_gamma"]),
+                                     p(lay["knorm_beta"]), p(pv[v]), H, TPV, HD,
                                      C.c_float(100.0), C.c_float(1e-5))
         lib.ora_layerscale_residual_f32(p(a["tokens"]), p(a["attn_proj"]), p(lay["ls1"]), r, D)
-        lib.ora_layernorm_f32(p(a["tokens"]), p(ln2), r, D, p(lay["norm2_gamma"]),
+        lib.ora_layernorm_f32(p(a["tokens"]), p(a["ln2"]), r, D, p(lay["norm2_gamma"]),
                               p(lay["norm2_beta"]), C.c_float(1e-6))
         lib.ora_gelu_f32(p(a["hidden"]), a["hidden"].size)
         lib.ora_layerscale_residual_f32(p(a["tokens"]), p(a["mlp_out"]), p(lay["ls2"]), r, D)
 
-    def timed(budget):
-        one_block()  # warm-up
+    def timed(fn, budget):
+        a = fresh()
+        fn(a)  # warm-up
         times = []
         t_end = time.perf_counter() + budget
         while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 1000):
             t0 = time.perf_counter()
-            one_block()
+            fn(a)
             times.append(time.perf_counter() - t0)
         return statistics.median(times), len(times)
 
-    nbytes = ln_bytes(r) * 2 + qk_bytes(r) + lsres_bytes(r) * 2 + gelu_bytes(r)
-    med, runs = timed(seconds)
-    # the same oracle on one thread (the scalar restatement as written)
+    def line(med, runs, cores, what):
+        return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": cores,
+                "us_per_block": round(med * 1e6, 1), "runs": runs, "what": what}
+
+    host = cpu_model() or {}
+    physical = host.get("physical_cores") or threads
+    out = {}
+    if simd.available():
+        simd.set_threads(threads)
+        med, runs = timed(simd_block, seconds)
+        out = line(med, runs, threads, "AVX-512 + OpenMP restatement (oracle/cpu_simd.c, "
+                                       "x86-64-v4, -O3 -ffp-contract=off)")
+        out["kind"] = "port"
+        if physical > threads:
+            out["all_physical_cores"] = {
+                "cores": physical,
+                "not_taken": f"the host has {physical} physical cores; a one-GPU run's share "
+                             f"of them is {threads} threads"}
+        elif physical < threads:
+            simd.set_threads(physical)
+            med_all, runs_all = timed(simd_block, seconds / 2)
+            out["all_physical_cores"] = line(med_all, runs_all, physical,
+                                             "same, one thread per physical core")
+            simd.set_threads(threads)
+        else:
+            out["all_physical_cores"] = {"cores": physical, "same_as_value": True}
+    # the scalar oracle as written, on one thread
     oracle.set_threads(1)
-    med1, runs1 = timed(seconds / 2)
-    oracle.set_threads(threads)
-    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port", "us_per_block": round(med * 1e6, 1),
-            "cpu_model": cpu_model(), "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
-            "single_thread": {"value": round(nbytes / med1 / 1e9, 2), "unit": "GB/s",
-                              "cores": 1, "us_per_block": round(med1 * 1e6, 1),
-                              "runs": runs1},
-            "sample": (f"oracle (scalar C, OpenMP over rows) on one ViT-B block's fused ops "
-                       f"(LN1, Q/K-norm+RoPE, LS+res, LN2, GELU, LS+res) over {r} rows "
-                       f"(12 views x {TPV}); median of {runs} runs after 1 warm-up")}
+    med1, runs1 = timed(scalar_block, seconds / 2)
+    single = line(med1, runs1, 1, "scalar oracle (vestra_oracle.c, -O2), one thread")
+    if not out:
+        out = dict(single, kind="port", note="host lacks AVX-512: the scalar oracle on one thread")
+    out["single_thread_scalar"] = single
+    out["cpu"] = host
+    out["omp_proc_bind"] = os.environ.get("OMP_PROC_BIND")
+    out["sample"] = (f"one ViT-B block's fused ops (LN1, Q/K-norm+RoPE, LS+res, LN2, GELU, "
+                     f"LS+res) over {r} rows (12 views x {TPV}); median of repeated runs after "
+                     f"1 warm-up, about {seconds:.0f} s of CPU work per figure")
+    return out
 
 
 def measured_traffic(op, algorithmic_bytes):
@@ -741,6 +814,8 @@ def main():
                                      "patch_embed"],
                     help="profile mode: launch only this operation (12-view shape, rotating "
                          "buffers) after one calibration device copy of 256 MiB")
+    ap.add_argument("--op-views", type=int, default=12,
+                    help="profile mode: view count of the operation's shape (866 rows each)")
     ap.add_argument("--linear", action="store_true",
                     help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
                          "at the 12-view shape")
@@ -806,10 +881,13 @@ def main():
         cal_dst = rt.alloc_f32(64 << 20)
         rt.copy_segment_into_f32(cal_dst, 0, cal, 0, 64 << 20)
         rt.synchronize()
-        table = per_op_table(rt, rng, TPV * 12, rotate=ROTATE_SETS, iters=args.op_iters,
+        views = args.op_views
+        sets = ROTATE_SETS * max(1, 12 // views)  # the working set stays beyond 256 MB
+        table = per_op_table(rt, rng, TPV * views, rotate=sets, iters=args.op_iters,
                              only=args.op)
-        print(json.dumps({"op": args.op, "calibration_copy_bytes": 2 * (256 << 20),
-                          **table[args.op]}), flush=True)
+        print(json.dumps({"op": args.op, "rows": TPV * views, "rotate_sets": sets,
+                          "calibration_copy_bytes": 2 * (256 << 20), **table[args.op]}),
+              flush=True)
         return
     log(f"device has {rt.cu_count()} CUs; building 12-view workload ({TPV * 12} rows)")
     model = Model(rt, rng, views=12)

@@ -422,18 +422,23 @@ __device__ __forceinline__ int xcd_tile(int lin, int n) {
 // reference's scalar GELU (docs/plans/2026-07-18-rust-engine-v1.md:870-876),
 // with the same operation order: t = 1/(1 + p*a);
 // y = 1 - ((((a5*t + a4)*t + a3)*t + a2)*t + a1)*t * exp(-a*a); erf = sign*y.
+// t takes the hardware reciprocal (v_rcp_f32, 1 ulp) and exp(-a*a) the
+// hardware base-2 exponential of -a*a*log2(e) (v_exp_f32): a few ulp from
+// the correctly rounded quotient and expf, for 2 instructions where those
+// take about 23 -- the GELU stream is otherwise as much VALU- as HBM-bound.
 // Shared by the GELU stream and the linear's GELU epilogue, so both give the
 // same bits.
 __device__ __forceinline__ float erf_as7126(float x) {
   const float s = __builtin_signbit(x) ? -1.0f : 1.0f;
   const float a = fabsf(x);
-  const float t = 1.0f / (1.0f + 0.3275911f * a);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
   float p = 1.0614054f * t - 1.4531520f;
   p = p * t;
   p = p + 1.4214137f;
   p = p * t - 0.28449674f;
   p = p * t + 0.25482959f;
-  const float y = 1.0f - p * t * expf(-a * a);
+  const float e = __builtin_amdgcn_exp2f(-(a * a) * 1.44269504f);
+  const float y = 1.0f - p * t * e;
   return s * y;
 }
 

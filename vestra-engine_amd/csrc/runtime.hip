@@ -172,9 +172,22 @@ int ensure_work(vk_runtime* rt, size_t floats, const char* who) {
   return VK_OK;
 }
 
-// Device-to-device copies as kernels: 16-byte, 4-byte or 1-byte elements,
-// the widest that both ends and the length are aligned to.  Grid-stride
-// loops over at most 4096 workgroups of 256 threads.
+// Device-to-device copies as kernels.  16-byte aligned copies: a grid over
+// the whole tensor, two float4 per thread with both loads issued before the
+// stores, streaming (nontemporal) loads and stores -- the form of the
+// path's stream kernels.  Other alignments: 4-byte or 1-byte elements in a
+// grid-stride loop over at most 4096 workgroups of 256 threads.
+__global__ __launch_bounds__(256) void copy16_kernel(float4* __restrict__ dst,
+                                                     const float4* __restrict__ src, size_t n16) {
+  const size_t i0 = static_cast<size_t>(blockIdx.x) * 512 + threadIdx.x;
+  const size_t i1 = i0 + 256;
+  const size_t c1 = i1 < n16 ? i1 : n16 - 1;  // always a valid element
+  const float4 v0 = vkd::ld_stream(src + (i0 < n16 ? i0 : n16 - 1));
+  const float4 v1 = vkd::ld_stream(src + c1);
+  if (i0 < n16) vkd::st_stream(dst + i0, v0);
+  if (i1 < n16) vkd::st_stream(dst + i1, v1);
+}
+
 template <typename T>
 __global__ void copy_elems_kernel(T* __restrict__ dst, const T* __restrict__ src, size_t n) {
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
@@ -197,13 +210,17 @@ int device_copy(vk_runtime* rt, void* dst, const void* src, size_t bytes) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes;
   const size_t unit = (a & 15) == 0 ? 16 : (a & 3) == 0 ? 4 : 1;
   const size_t n = bytes / unit;
+  if (unit == 16) {
+    const size_t blocks = (n + 511) / 512;
+    VK_UNSUPPORTED_IF(blocks > 0x7fffffffULL, "device copy of %zu bytes", bytes);
+    hipLaunchKernelGGL(copy16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       rt->stream, static_cast<float4*>(dst), static_cast<const float4*>(src), n);
+    return check_launch("device copy");
+  }
   size_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);
-  if (unit == 16)
-    hipLaunchKernelGGL(copy_elems_kernel<uint4>, grid, block, 0, rt->stream,
-                       static_cast<uint4*>(dst), static_cast<const uint4*>(src), n);
-  else if (unit == 4)
+  if (unit == 4)
     hipLaunchKernelGGL(copy_elems_kernel<uint32_t>, grid, block, 0, rt->stream,
                        static_cast<uint32_t*>(dst), static_cast<const uint32_t*>(src), n);
   else
