@@ -124,7 +124,10 @@ using namespace vkq;
 // Each 16-lane group owns kQkRowsPerGroup consecutive rows of the flattened
 // [Q rows | K rows] index space; both rows' loads are issued before either
 // row's reductions, doubling the bytes in flight per wave.
-constexpr int kQkRowsPerGroup = 2;
+#ifndef VK_QK_ROWS_PER_GROUP
+#define VK_QK_ROWS_PER_GROUP 2
+#endif
+constexpr int kQkRowsPerGroup = VK_QK_ROWS_PER_GROUP;
 constexpr int kQkThreads = 256;  // threads per workgroup: kQkThreads / 16 row groups
 
 template <typename PT, bool HAS_NORM, int POS, int PAIR>
@@ -136,8 +139,10 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
   const int l = threadIdx.x & 15;
   const uint32_t grp = blockIdx.x * (kQkThreads / 16u) + (threadIdx.x >> 4);
   const uint32_t total = sh.tensors * sh.rows_per_tensor;
+  // every row's loads (data, parameters, cos/sin) before any row's
+  // arithmetic: one memory round trip per wave
   float4 v[kQkRowsPerGroup];
-  int py[kQkRowsPerGroup], px[kQkRowsPerGroup];
+  QkRowOperands op[kQkRowsPerGroup];
 #pragma unroll
   for (int j = 0; j < kQkRowsPerGroup; ++j) {
     const uint32_t gr = grp * kQkRowsPerGroup + j;
@@ -145,19 +150,22 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     const uint32_t gc = gr < total ? gr : total - 1;
     const bool is_k = gc >= sh.rows_per_tensor;
     const uint32_t r = is_k ? gc - sh.rows_per_tensor : gc;
-    qk_row_position<POS>(r, sh, pos_yx, &py[j], &px[j]);
+    int py, px;
+    qk_row_position<POS>(r, sh, pos_yx, &py, &px);
     v[j] = vkd::ld_stream(reinterpret_cast<const float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l);
+    op[j] = qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, is_k ? kg : qg, is_k ? kb : qb, py, px,
+                                                     table, sh.table_max);
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < kQkRowsPerGroup; ++j) v[j] = qk_row_apply<HAS_NORM, PAIR>(v[j], l, op[j], eps);
 #pragma unroll
   for (int j = 0; j < kQkRowsPerGroup; ++j) {
     const uint32_t gr = grp * kQkRowsPerGroup + j;
-    const bool is_k = gr >= sh.rows_per_tensor;
-    const float4 o = qk_row_transform<PT, HAS_NORM, POS, PAIR>(v[j], l, is_k ? kg : qg,
-                                                               is_k ? kb : qb, py[j], px[j],
-                                                               table, sh.table_max, eps);
     if (gr < total) {
+      const bool is_k = gr >= sh.rows_per_tensor;
       const uint32_t r = is_k ? gr - sh.rows_per_tensor : gr;
-      vkd::st_stream(reinterpret_cast<float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l, o);
+      vkd::st_stream(reinterpret_cast<float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l, v[j]);
     }
   }
 }

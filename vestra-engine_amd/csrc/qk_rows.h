@@ -112,15 +112,68 @@ __device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
   }
 }
 
-// LayerNorm of one 64-wide row held as one float4 per lane of a 16-lane DPP
-// row, then its 2D rotation.  Lanes 0-7 hold the y half (elements 0..31),
-// lanes 8-15 the x half.  Every rotated pair (a, b) with angle frequency j
-// becomes (a*cos - b*sin, b*cos + a*sin), each product rounded, then the sum.
+// The per-row operands of the transform below: the lane's LayerNorm gamma
+// and beta (four elements each) and the cos/sin of its rotated pairs (four
+// frequencies with rotate-half pairing, two with interleaved pairing).
+// Loading them is a stage of its own, so a caller holding several rows can
+// issue every row's loads before any row's arithmetic.
+struct QkRowOperands {
+  float4 g, b;  // LayerNorm parameters (unused without the norm)
+  float4 c, s;  // cos/sin: components 0..3 (rotate-half) or 0..1 (interleaved)
+};
+
 template <typename PT, bool HAS_NORM, int POS, int PAIR>
-__device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
-                                                   const PT* __restrict__ b, int py, int px,
-                                                   const float* __restrict__ table,
-                                                   int table_max, float eps) {
+__device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __restrict__ g,
+                                                         const PT* __restrict__ b, int py,
+                                                         int px,
+                                                         const float* __restrict__ table,
+                                                         int table_max) {
+  QkRowOperands o;
+  if (HAS_NORM) {
+    o.g = vkd::Param<PT>::load4(g, l);
+    o.b = vkd::Param<PT>::load4(b, l);
+  }
+  // lanes 0-7 rotate by the row coordinate, lanes 8-15 by the column
+  const int coord = (l < 8) ? py : px;
+  const bool in_table = POS == kPosGrid || (coord >= 0 && coord <= table_max);
+  const float* e = table + static_cast<size_t>(in_table ? coord : 0) * 32;
+  if (PAIR == kRotateHalf) {
+    const int j0 = (l & 3) * 4;  // frequencies j0..j0+3
+    if (in_table) {
+      o.c = *reinterpret_cast<const float4*>(e + j0);
+      o.s = *reinterpret_cast<const float4*>(e + 16 + j0);
+    } else {
+      float cv[4], sv[4];
+      rope_cs_slow<4>(table, table_max, coord, j0, cv, sv);
+      o.c = make_float4(cv[0], cv[1], cv[2], cv[3]);
+      o.s = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    }
+  } else {
+    const int j0 = (l & 7) * 2;  // frequencies j0, j0+1
+    float2 c, sn;
+    if (in_table) {
+      c = *reinterpret_cast<const float2*>(e + j0);
+      sn = *reinterpret_cast<const float2*>(e + 16 + j0);
+    } else {
+      float cv[2], sv[2];
+      rope_cs_slow<2>(table, table_max, coord, j0, cv, sv);
+      c = make_float2(cv[0], cv[1]);
+      sn = make_float2(sv[0], sv[1]);
+    }
+    o.c = make_float4(c.x, c.y, 0.0f, 0.0f);
+    o.s = make_float4(sn.x, sn.y, 0.0f, 0.0f);
+  }
+  return o;
+}
+
+// LayerNorm of one 64-wide row held as one float4 per lane of a 16-lane DPP
+// row, then its 2D rotation, with the operands of qk_row_operands.  Lanes 0-7
+// hold the y half (elements 0..31), lanes 8-15 the x half.  Every rotated
+// pair (a, b) with angle frequency j becomes (a*cos - b*sin, b*cos + a*sin),
+// each product rounded, then the sum.
+template <bool HAS_NORM, int PAIR>
+__device__ __forceinline__ float4 qk_row_apply(float4 v, int l, const QkRowOperands& op,
+                                               float eps) {
   if (HAS_NORM) {
     float s = v.x;
     s += v.y;
@@ -138,32 +191,16 @@ __device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __
     // hardware reciprocal square root (v_rsq_f32, 1 ulp): the correctly
     // rounded 1/sqrtf costs ~18 VALU instructions per row
     const float inv = __builtin_amdgcn_rsqf(var + eps);
-    const float4 gv = vkd::Param<PT>::load4(g, l);
-    const float4 bv = vkd::Param<PT>::load4(b, l);
-    v.x = (v.x - mean) * inv * gv.x + bv.x;
-    v.y = (v.y - mean) * inv * gv.y + bv.y;
-    v.z = (v.z - mean) * inv * gv.z + bv.z;
-    v.w = (v.w - mean) * inv * gv.w + bv.w;
+    v.x = (v.x - mean) * inv * op.g.x + op.b.x;
+    v.y = (v.y - mean) * inv * op.g.y + op.b.y;
+    v.z = (v.z - mean) * inv * op.g.z + op.b.z;
+    v.w = (v.w - mean) * inv * op.g.w + op.b.w;
   }
-  const int coord = (l < 8) ? py : px;
-  const bool in_table = POS == kPosGrid || (coord >= 0 && coord <= table_max);
-  const float* e = table + static_cast<size_t>(in_table ? coord : 0) * 32;
+  const float4 c = op.c, s = op.s;
   float4 o;
   if (PAIR == kRotateHalf) {
     // Inside a half, lanes with bit 2 clear hold elements j (j < 16) and
-    // rotate against the lane 4 above, which holds element j + 16; both use
-    // frequencies j0..j0+3.
-    const int j0 = (l & 3) * 4;
-    float4 c, s;
-    if (in_table) {
-      c = *reinterpret_cast<const float4*>(e + j0);
-      s = *reinterpret_cast<const float4*>(e + 16 + j0);
-    } else {
-      float cv[4], sv[4];
-      rope_cs_slow<4>(table, table_max, coord, j0, cv, sv);
-      c = make_float4(cv[0], cv[1], cv[2], cv[3]);
-      s = make_float4(sv[0], sv[1], sv[2], sv[3]);
-    }
+    // rotate against the lane 4 above, which holds element j + 16.
     const float4 p = swizzle_xor4(v);
     if ((l & 4) == 0) {
       // out[j] = x[j]*cos - x[j+16]*sin
@@ -179,25 +216,25 @@ __device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __
       o.w = v.w * c.w + p.w * s.w;
     }
   } else {
-    // The lane's four elements 4m..4m+3 of its half (m = l & 7) are the two
-    // pairs 2m and 2m + 1: frequencies j0 = 2m and j0 + 1, no lane exchange.
-    const int j0 = (l & 7) * 2;
-    float2 c, s;
-    if (in_table) {
-      c = *reinterpret_cast<const float2*>(e + j0);
-      s = *reinterpret_cast<const float2*>(e + 16 + j0);
-    } else {
-      float cv[2], sv[2];
-      rope_cs_slow<2>(table, table_max, coord, j0, cv, sv);
-      c = make_float2(cv[0], cv[1]);
-      s = make_float2(sv[0], sv[1]);
-    }
+    // The lane's four elements 4m..4m+3 of its half are the pairs 2m and
+    // 2m + 1: no lane exchange.
     o.x = v.x * c.x + (-v.y) * s.x;
     o.y = v.y * c.x + v.x * s.x;
     o.z = v.z * c.y + (-v.w) * s.y;
     o.w = v.w * c.y + v.z * s.y;
   }
   return o;
+}
+
+// Both stages for one row (the QKV projection's epilogue).
+template <typename PT, bool HAS_NORM, int POS, int PAIR>
+__device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
+                                                   const PT* __restrict__ b, int py, int px,
+                                                   const float* __restrict__ table,
+                                                   int table_max, float eps) {
+  const QkRowOperands op =
+      qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, g, b, py, px, table, table_max);
+  return qk_row_apply<HAS_NORM, PAIR>(v, l, op, eps);
 }
 
 }  // namespace vkq
