@@ -31,6 +31,12 @@ import time
 # the CPU baseline's OpenMP threads stay on neighbouring cores (read when the
 # OpenMP runtime starts, so it is set before anything loads one)
 os.environ.setdefault("OMP_PROC_BIND", "close")
+# the CPUs this process may run on, read before an OpenMP runtime binds the
+# main thread to the first of them
+try:
+    GRANTED_CPUS = len(os.sched_getaffinity(0))
+except (AttributeError, OSError):
+    GRANTED_CPUS = None
 
 import numpy as np
 
@@ -324,10 +330,7 @@ def cpu_model():
         return None
     info["logical_cpus"] = logical
     info["physical_cores"] = len(cores) or None
-    try:
-        info["granted_cpus"] = len(os.sched_getaffinity(0))
-    except (AttributeError, OSError):
-        info["granted_cpus"] = None
+    info["granted_cpus"] = GRANTED_CPUS
     return info
 
 
@@ -799,6 +802,16 @@ def measured_traffic(op, algorithmic_bytes):
     return entry["traffic_bytes"]
 
 
+def roofline_entry(gelu):
+    """The benchmark line's roofline object: the 12-view GELU launch, the
+    step's dominant per-token kernel, against the HBM peak."""
+    return {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
+            "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": gelu["bytes"], "avg_launch_us": gelu["us"],
+            "traffic": measured_traffic("gelu", gelu["bytes"])}
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -831,6 +844,9 @@ def main():
     ap.add_argument("--attention", action="store_true",
                     help="attention mode: the attention core at the local, global and ViT-L "
                          "shapes")
+    ap.add_argument("--headline", action="store_true",
+                    help="headline mode: only the timed 12-view step and the GELU launch "
+                         "timing behind the roofline object, without the other sections")
     ap.add_argument("--sweep", type=str, default=None, metavar="VIEWS",
                     help="size-sweep mode: the per-operation table at each comma-separated "
                          "view count (866 rows per view), one JSON line per size")
@@ -902,6 +918,16 @@ def main():
     ms_per_step = time_loop(rt, step_graph.launch, args.steps)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     log(f"{ms_per_step:.3f} ms/step, {value:.1f} GB/s")
+    if args.headline:
+        del step_graph
+        gelu = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters,
+                            only="gelu")["gelu"]
+        print(json.dumps({"headline": {"value": round(value, 1), "unit": "GB/s",
+                                       "ms_per_step": round(ms_per_step, 4),
+                                       "steps": args.steps, "warmup": args.warmup,
+                                       "bytes_per_step": int(nbytes),
+                                       "roofline": roofline_entry(gelu)}}), flush=True)
+        return
 
     # single-image block: 866 rows, 12 blocks captured in one HIP graph
     single = Model(rt, rng, views=1)
@@ -980,11 +1006,7 @@ def main():
         "full_block": full_block,
         "vitl_1008x672": vitl,
         "pipeline": pipeline,
-        "roofline": {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
-                     "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
-                     "algorithmic_bytes": gelu["bytes"], "avg_launch_us": gelu["us"],
-                     "traffic": measured_traffic("gelu", gelu["bytes"])},
+        "roofline": roofline_entry(gelu),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
