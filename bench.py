@@ -832,6 +832,9 @@ def main():
     ap.add_argument("--linear", action="store_true",
                     help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
                          "at the 12-view shape")
+    ap.add_argument("--rows", type=int, default=None,
+                    help="linear mode: token rows of the projections (default 10,392, the "
+                         "12-view shape; 866 is one image)")
     ap.add_argument("--full-block", action="store_true",
                     help="whole-block mode: 12 complete ViT-B blocks on the device "
                          "(projections and attention included), single image and 12 views")
@@ -883,7 +886,8 @@ def main():
         print(json.dumps({"attention": attention_timing(rt, rng, args.op_iters)}), flush=True)
         return
     if args.linear:
-        print(json.dumps({"linear_epilogues": linear_epilogue_timing(rt, rng, TPV * 12,
+        rows = args.rows or TPV * 12
+        print(json.dumps({"linear_epilogues": linear_epilogue_timing(rt, rng, rows,
                                                                      args.op_iters)}), flush=True)
         return
     if args.op == "patch_embed":

@@ -133,13 +133,57 @@ __device__ __forceinline__ float4 qk_head_row(const LinearArgs& g, float4 v, int
       v, l, gm, bt, py, px, g.qkn.table, g.qkn.table_max, g.qkn.eps);
 }
 
-template <int EPI, int LAY, int QKN, int TM, int TN>
-__global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4))
+// Most split-K slices a sum pass reads (the plan's limit, checked where it
+// is defined).  The sum passes are instantiated for split-count buckets SPB
+// of 2, 4 and 8 (split_bucket).
+constexpr int kMaxSplits = 8;
+constexpr int split_bucket(int splits) { return splits <= 2 ? 2 : (splits <= 4 ? 4 : 8); }
+
+// The NV float4 at offsets e[i] of every split's slice (splits <= SPB),
+// summed in split order.  All SPB x NV loads are issued before the first
+// addition (a run-time loop over the splits waited for each iteration's
+// load); slots past `splits` re-read the last slice and are not added.
+template <int NV, int SPB>
+__device__ __forceinline__ void split_sums(const float* __restrict__ partial, size_t mn,
+                                           const size_t (&e)[NV], int splits, f32x4 (&acc)[NV]) {
+  f32x4 p[NV][SPB];
+#pragma unroll
+  for (int sp = 0; sp < SPB; ++sp) {
+    const size_t slice = static_cast<size_t>(sp < splits ? sp : splits - 1) * mn;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) p[i][sp] = *reinterpret_cast<const f32x4*>(partial + slice + e[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    acc[i] = p[i][0];
+#pragma unroll
+    for (int sp = 1; sp < SPB; ++sp)
+      if (sp < splits) acc[i] = acc[i] + p[i][sp];
+  }
+}
+
+// KG: k groups.  With KG = 2 (64 x 64 tiles only) the workgroup has twice the
+// waves: group 1 runs the second half of every chunk's 16-blocks on the same
+// strips as group 0, and adds its sums to group 0's through LDS after the
+// last chunk (group 0's + group 1's, in that order).  A grid of few tiles
+// (one image: two workgroups per CU) then keeps four waves per SIMD instead
+// of two.
+//
+// PF: the next chunk's loads are issued before this chunk's MFMAs and land in
+// registers meanwhile.  It costs 2 (64 x 64) or 8 (128 x 128) more float4 per
+// thread, so the 128 x 128 tile takes it only where a launch has at most one
+// workgroup per CU (nothing else on the CU covers the load latency there,
+// and the lower occupancy costs nothing).
+template <int EPI, int LAY, int QKN, int TM, int TN, int KG = 1, bool PF = (KG == 2)>
+__global__ __launch_bounds__(threads_for(TM) * KG,
+                             TM == 128 ? (PF ? 1 : 2) : (TN == 128 ? 3 : (KG == 2 ? 3 : 4)))
     void linear_wide_kernel(LinearArgs g) {
   constexpr int WN = TN / 2;  // columns of a wave's strip
   constexpr int NU = WN / 16; // 16-column MFMA tiles per strip
   static_assert(TN == 128 || TN == 64, "tile widths 128 and 64");
-  constexpr int kThreads = threads_for(TM);
+  static_assert(KG == 1 || (KG == 2 && TM == 64 && TN == 64), "k groups: 64 x 64 tiles");
+  constexpr int kThreads = threads_for(TM) * KG;
+  constexpr int kGroupWaves = threads_for(TM) / 64;  // waves of one k group
   constexpr int kVA = TM * KC / 4 / kThreads;  // float4 of A per thread a chunk: 4
   constexpr int kVB = TN * KC / 4 / kThreads;  // float4 of B: TN / TM x 4
   static_assert(TM == 128 || TM == 64, "tile heights 128 and 64");
@@ -150,7 +194,10 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
   const int tid = threadIdx.x;
   __builtin_assume(tid < kThreads);
   const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int kh = KG == 1 ? 0 : wave / kGroupWaves;  // k group
+  const bool lead = kh == 0;                          // holds the tile's sums at the end
+  const int wl = wave % kGroupWaves;                  // wave within the k group
+  const int wm = wl >> 1, wn = wl & 1;
   const int gmt = (g.M + TM - 1) / TM;
   const int gnt = (g.N + TN - 1) / TN;
   const int tile = vkd::xcd_tile(blockIdx.x, gridDim.x);
@@ -167,7 +214,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
 #pragma unroll
     for (int u = 0; u < NU; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int kq = 4 * (lane >> 4);
+  const int kq = 4 * (lane >> 4) + kh * (KC / KG);
   const float* arow = As + (wm * 32 + (lane & 15)) * PITCH + kq;
   const float* brow = Bs + (wn * WN + (lane & 15)) * PITCH + kq;
 
@@ -194,7 +241,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
 
   auto mma_chunk = [&]() {
 #pragma unroll
-    for (int b = 0; b < KC / 16; ++b) {
+    for (int b = 0; b < KC / 16 / KG; ++b) {
       f32x4 a[2], w[NU];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -221,24 +268,42 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
       vkd::buffer_rsrc(g.x, 4u * static_cast<uint32_t>(g.M) * static_cast<uint32_t>(g.K));
   const __amdgpu_buffer_rsrc_t b_rsrc =
       vkd::buffer_rsrc(g.wnk, 4u * static_cast<uint32_t>(g.N) * static_cast<uint32_t>(g.Kp));
-  for (int ch = c_begin; ch < c_full; ++ch) {
+  auto load_chunk = [&](int ch, float4 (&ra)[kVA], float4 (&rb)[kVB]) {
     const uint32_t k0 = static_cast<uint32_t>(ch) * KC;
     const uint32_t a_chunk =
         4u * (LAY == kAHnd ? static_cast<uint32_t>(ch) * static_cast<uint32_t>(g.M) * 64u : k0);
-    float4 ra[kVA], rb[kVB];
 #pragma unroll
     for (int i = 0; i < kVA; ++i) ra[i] = vkd::buffer_load4(a_rsrc, a_off[i], a_chunk);
 #pragma unroll
     for (int i = 0; i < kVB; ++i) rb[i] = vkd::buffer_load4(b_rsrc, b_off[i], 4u * k0);
-    __syncthreads();  // every wave is done reading the previous chunk
+  };
+  auto store_chunk = [&](const float4 (&ra)[kVA], const float4 (&rb)[kVB]) {
 #pragma unroll
     for (int i = 0; i < kVA; ++i)
       *reinterpret_cast<float4*>(As + slot_row(i) * PITCH + c_ld) = ra[i];
 #pragma unroll
     for (int i = 0; i < kVB; ++i)
       *reinterpret_cast<float4*>(Bs + slot_row(i) * PITCH + c_ld) = rb[i];
-    __syncthreads();
-    mma_chunk();
+  };
+  if constexpr (PF) {
+    float4 ra[kVA], rb[kVB];
+    if (c_begin < c_full) load_chunk(c_begin, ra, rb);
+    for (int ch = c_begin; ch < c_full; ++ch) {
+      __syncthreads();  // every wave is done reading the previous chunk
+      store_chunk(ra, rb);
+      __syncthreads();
+      if (ch + 1 < c_full) load_chunk(ch + 1, ra, rb);
+      mma_chunk();
+    }
+  } else {
+    for (int ch = c_begin; ch < c_full; ++ch) {
+      float4 ra[kVA], rb[kVB];
+      load_chunk(ch, ra, rb);
+      __syncthreads();  // every wave is done reading the previous chunk
+      store_chunk(ra, rb);
+      __syncthreads();
+      mma_chunk();
+    }
   }
 
   // The last, partial chunk (K % 64 != 0): k past K reads a clamped address
@@ -282,19 +347,44 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
     mma_chunk();
   }
 
+  // k groups: group 1's sums through LDS (As, free after the last chunk) to
+  // group 0, one f32x4 per lane and MFMA tile, lane-contiguous
+  if constexpr (KG == 2) {
+    static_assert(kGroupWaves * 2 * NU * 256 <= TM * PITCH, "k-group sums fit in As");
+    float* red = As + wl * (2 * NU * 256) + 4 * lane;
+    __syncthreads();  // every wave is done reading the last chunk's operands
+    if (!lead) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          *reinterpret_cast<f32x4*>(red + (t * NU + u) * 256) = acc[t][u];
+    }
+    __syncthreads();
+    if (lead) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          acc[t][u] = acc[t][u] + *reinterpret_cast<const f32x4*>(red + (t * NU + u) * 256);
+    }
+  }
+
   // split-K: raw sums to this split's slice of the partial buffer
   if (g.splits > 1) {
-    float* part = g.partial + static_cast<size_t>(split) * g.M * g.N;
+    if (lead) {
+      float* part = g.partial + static_cast<size_t>(split) * g.M * g.N;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int u = 0; u < NU; ++u)
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
-          const int col = n0 + wn * WN + u * 16 + (lane & 15);
-          if (row < g.M && col < g.N) part[static_cast<size_t>(row) * g.N + col] = acc[t][u][r];
-        }
+          for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
+            const int col = n0 + wn * WN + u * 16 + (lane & 15);
+            if (row < g.M && col < g.N) part[static_cast<size_t>(row) * g.N + col] = acc[t][u][r];
+          }
+    }
     return;
   }
 
@@ -308,10 +398,11 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
     // own (its 32 x 64 strip); a 64-wide tile is one head, whose 32-row
     // halves waves wn 0 and 1 hold 32 columns each of and then transform 16
     // rows each.
+    // With k groups, the eight waves transform 8 rows each.
     const int col0 = TN == 128 ? n0 + wn * 64 : n0;
     const int cw0 = TN == 128 ? 0 : wn * 32;  // the wave's first column in the head
-    constexpr int kRowsPerGroup = TN == 128 ? 8 : 4;
-    const int rr0 = TN == 128 ? 0 : wn * 16;
+    constexpr int kRowsPerGroup = TN == 128 ? 8 : 4 / KG;
+    const int rr0 = TN == 128 ? 0 : (wn * KG + kh) * (16 / KG);
     const int embed = g.N / 3;
     const int which = col0 < g.N ? col0 / embed : 2;
     const int g4 = lane >> 4, c16 = lane & 15;
@@ -321,7 +412,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
                          : (wave < TM / 32 ? As + wave * 32 * PITCH
                                            : Bs + (wave - TM / 32) * 32 * PITCH);
     __syncthreads();  // every wave is done with the last chunk's operands
-    if (which < 2) {
+    if (which < 2 && lead) {
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         const float b = g.bias[col0 + cw0 + u * 16 + c16];
@@ -347,6 +438,7 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
       return;
     }
   }
+  if (!lead) return;
   // Per 16-column strip u: bias, LayerScale and the address of the column
   // at row 0 (row r adds r x the row stride), computed once; a tile inside
   // the matrix stores without bounds checks.
@@ -388,35 +480,6 @@ __global__ __launch_bounds__(threads_for(TM), TM == 128 ? 2 : (TN == 128 ? 3 : 4
         if (interior || (rok && cok[u])) cptr[u][static_cast<size_t>(row) * rs] = val;
       }
     }
-}
-
-// Most split-K slices a sum pass reads (the plan's limit, checked where it
-// is defined).  The sum passes are instantiated for split-count buckets SPB
-// of 2, 4 and 8 (split_bucket).
-constexpr int kMaxSplits = 8;
-constexpr int split_bucket(int splits) { return splits <= 2 ? 2 : (splits <= 4 ? 4 : 8); }
-
-// The NV float4 at offsets e[i] of every split's slice (splits <= SPB),
-// summed in split order.  All SPB x NV loads are issued before the first
-// addition (a run-time loop over the splits waited for each iteration's
-// load); slots past `splits` re-read the last slice and are not added.
-template <int NV, int SPB>
-__device__ __forceinline__ void split_sums(const float* __restrict__ partial, size_t mn,
-                                           const size_t (&e)[NV], int splits, f32x4 (&acc)[NV]) {
-  f32x4 p[NV][SPB];
-#pragma unroll
-  for (int sp = 0; sp < SPB; ++sp) {
-    const size_t slice = static_cast<size_t>(sp < splits ? sp : splits - 1) * mn;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) p[i][sp] = *reinterpret_cast<const f32x4*>(partial + slice + e[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    acc[i] = p[i][0];
-#pragma unroll
-    for (int sp = 1; sp < SPB; ++sp)
-      if (sp < splits) acc[i] = acc[i] + p[i][sp];
-  }
 }
 
 // Second pass of a split-K linear: one thread per 4 consecutive outputs of a
@@ -585,15 +648,19 @@ Plan choose_plan(const vk_runtime* rt, int M, int N, int K) {
 template <int EPI, int LAY, int QKN = 0>
 void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 grid,
                  bool sum_pass = true) {
-  if (plan.tm == 128)
+  const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
+  if (plan.tm == 128 && static_cast<long long>(grid.x) <= cus)
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 128, 128, 1, true>), grid,
+                       dim3(threads_for(128)), 0, rt->stream, g);
+  else if (plan.tm == 128)
     hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 128, 128>), grid,
                        dim3(threads_for(128)), 0, rt->stream, g);
   else if (plan.tn == 128)
     hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 128>), grid, dim3(threads_for(64)),
                        0, rt->stream, g);
   else
-    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 64>), grid, dim3(threads_for(64)),
-                       0, rt->stream, g);
+    hipLaunchKernelGGL((linear_wide_kernel<EPI, LAY, QKN, 64, 64, 2>), grid,
+                       dim3(2 * threads_for(64)), 0, rt->stream, g);
   if (g.splits > 1 && sum_pass) {
     const long long n4 = static_cast<long long>(g.M) * g.N / 4;
     const dim3 sgrid(static_cast<unsigned>((n4 + 255) / 256));
