@@ -32,13 +32,19 @@ using vkd::Param;
 // lane is ever out of the row and every load is issued unguarded (a guarded
 // load makes the compiler wait for each one in turn).  x and y may alias.
 // ---------------------------------------------------------------------------
+// Rows per workgroup (one wave each, no shared memory or barriers).
+#ifndef VK_LN_WAVES
+#define VK_LN_WAVES 1
+#endif
+constexpr int kLnWaves = VK_LN_WAVES;
+
 template <int NV, typename PT, bool EXACT>
-__global__ __launch_bounds__(64) void layernorm_rows(const float* x, float* y,
+__global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows(const float* x, float* y,
                                                      const PT* __restrict__ gamma,
                                                      const PT* __restrict__ beta,
                                                      int rows, int cols, float eps) {
-  const int lane = threadIdx.x;
-  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nvec = cols >> 2;
   const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
@@ -66,12 +72,12 @@ __global__ __launch_bounds__(64) void layernorm_rows(const float* x, float* y,
 // HAS_LS false: unscaled residual add.  One wave per row.
 // ---------------------------------------------------------------------------
 template <int NV, typename PT, bool HAS_LS, bool EXACT>
-__global__ __launch_bounds__(64) void ls_residual_layernorm_rows(
+__global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
     float* __restrict__ x, const float* __restrict__ yb, const PT* __restrict__ ls,
     const PT* __restrict__ gamma, const PT* __restrict__ beta,
     float* __restrict__ ln_out, int rows, int cols, float eps) {
-  const int lane = threadIdx.x;
-  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nvec = cols >> 2;
   const size_t base = static_cast<size_t>(row) * cols;
@@ -213,7 +219,7 @@ template <typename PT>
 int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
                      const void* b, int rows, int cols, float eps) {
   const int nv = ln_instance_cols(cols);
-  dim3 grid(rows), block(64);
+  dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
 #define VK_LN_CASE(N)                                                                          \
@@ -239,7 +245,7 @@ int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
                      const void* g, const void* b, float* out, int rows, int cols,
                      float eps) {
   const int nv = ln_instance_cols(cols);
-  dim3 grid(rows), block(64);
+  dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
   auto LS = static_cast<const PT*>(ls);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
