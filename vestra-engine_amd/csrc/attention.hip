@@ -341,9 +341,18 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
                "attention: out overlaps an input");
   }
   if (len == 0) return VK_OK;
-  // 64-query tiles; when they give fewer than two workgroups per CU the key
-  // blocks of each tile are split over about two workgroups per CU (at least
-  // two key blocks per split), the partial results merged by a second pass
+  // 64-query tiles.  When they give fewer than two workgroups per CU (one
+  // ViT-B image: 168 tiles), each tile's key blocks are split over about two
+  // workgroups per CU (at least two key blocks per split) and a second pass
+  // merges the partial results.  Fuller grids split only where the last
+  // round of workgroups leaves CUs unevenly loaded and a cost model puts the
+  // split at least 5% below the unsplit launch: the busiest CU runs
+  // ceil(tiles * s / CUs) workgroups of up to ceil(key blocks / s) blocks
+  // (about 2.2 us per block of one of the four workgroups a CU holds), and a
+  // split adds its partial results' traffic (s slices of rows x 66 floats
+  // written and read back) and the merge pass (about 3 us).  ViT-L at 3,458
+  // rows (880 tiles of 55 blocks, 3.4 per CU): 2 splits; the 12-view layers
+  // stay unsplit.
   const int cus = rt->cu_count > 0 ? rt->cu_count : 256;
   const long long tiles64 = static_cast<long long>(sequences) * ((n + 63) / 64);
   const int nkb = static_cast<int>((n + KB - 1) / KB);
@@ -353,6 +362,20 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
     if (splits > nkb / 2) splits = nkb / 2;
     if (splits > 8) splits = 8;
     if (splits < 1) splits = 1;
+  } else {
+    constexpr double kBlockUs = 2.2, kBytesPerUs = 5.5e6, kMergeUs = 3.0;
+    const double row_bytes = 4.0 * (HD + 2) * static_cast<double>(sequences * n);
+    const double unsplit = kBlockUs * static_cast<double>((tiles64 + cus - 1) / cus * nkb);
+    double best = unsplit;
+    for (int sp = 2; sp <= 8 && 2 * sp <= nkb; ++sp) {
+      const long long load = (tiles64 * sp + cus - 1) / cus * ((nkb + sp - 1) / sp);
+      const double us = kBlockUs * static_cast<double>(load) +
+                        2.0 * sp * row_bytes / kBytesPerUs + kMergeUs;
+      if (us < best && us < 0.95 * unsplit) {
+        best = us;
+        splits = sp;
+      }
+    }
   }
   const long long blocks = tiles64 * splits;
   VK_UNSUPPORTED_IF(blocks > 0x7fffffffLL, "attention: %lld workgroups", blocks);
