@@ -90,16 +90,19 @@ def gelu_bytes(rows, shape=VITB):
 
 
 def block_plan(depth=DEPTH, alt=ALT):
-    """Flags per layer: LS2+res is fused with the next LN1 unless the next
-    layer rewrites the camera slot first."""
+    """Flags per layer: LS1+res is fused with LN2 and LS2+res with the next
+    block's LN1; before the camera-slot layer (alt) that fused pass also
+    writes the camera slot, so the layer at alt skips both."""
     import vestra_hip as vh
     plan = []
     prev_fused = False
     for i in range(depth):
-        fuse_next = i + 1 < depth and (i + 1) != alt
+        fuse_next = i + 1 < depth
         flags = vh.VK_BLOCK_FUSE_LS_LN
-        if prev_fused and i != alt:
+        if prev_fused:
             flags |= vh.VK_BLOCK_SKIP_LN1
+            if i == alt:
+                flags |= vh.VK_BLOCK_CAMERA_WRITTEN
         if fuse_next:
             flags |= vh.VK_BLOCK_FUSE_NEXT_LN1
         plan.append(flags)
@@ -113,13 +116,18 @@ def step_bytes(rows, views, plan, shape=VITB, w=4):
     import vestra_hip as vh
     total = 0
     for i, flags in enumerate(plan):
-        if i == shape.alt:
+        camera_here = i == shape.alt and not (flags & vh.VK_BLOCK_CAMERA_WRITTEN)
+        if camera_here:
             total += 2 * views * shape.D * 4  # camera slot copies
-        if not (flags & vh.VK_BLOCK_SKIP_LN1) or i == shape.alt:
+        if not (flags & vh.VK_BLOCK_SKIP_LN1) or camera_here:
             total += ln_bytes(rows, shape, w)
         total += qk_bytes(rows, shape, w) + lsres_ln_bytes(rows, shape, w) + gelu_bytes(rows, shape)
-        total += (lsres_ln_bytes(rows, shape, w) if flags & vh.VK_BLOCK_FUSE_NEXT_LN1
-                  else lsres_bytes(rows, shape, w))
+        if flags & vh.VK_BLOCK_FUSE_NEXT_LN1:
+            total += lsres_ln_bytes(rows, shape, w)
+            if i + 1 == shape.alt:
+                total += views * shape.D * 4  # the camera token read into each view's slot
+        else:
+            total += lsres_bytes(rows, shape, w)
     return total
 
 

@@ -611,7 +611,13 @@ typedef struct vk_vit_activations {
 #define VK_BLOCK_SKIP_LN1 2u        /* LN1 already produced (by the previous
                                        block's fused LS2+res+LN1)          */
 #define VK_BLOCK_FUSE_NEXT_LN1 4u   /* finish with LS2+res fused with the next
-                                       block's LN1 (next_layer required)   */
+                                       block's LN1 (next_layer required);
+                                       when the next block is alt_start and
+                                       `camera` is given, the camera-slot
+                                       overwrite is fused too              */
+#define VK_BLOCK_CAMERA_WRITTEN 8u  /* at alt_start: the previous block's
+                                       fused LS2+res+LN1 already wrote the
+                                       camera slot (and LN1)               */
 
 /* One DA3 ViT block's fused per-token operations, in the reference order of
  * run_tail_device (vit_block.rs:489-582) and vit_block_with_views
@@ -619,12 +625,15 @@ typedef struct vk_vit_activations {
  *   [camera overwrite at alt_start] -> LN1 -> Q/K-norm + RoPE (gated by
  *   qknorm_start / rope_start; positions per view, global layers (1,1)) ->
  *   tokens += ls1 (.) attn_proj -> LN2 -> GELU(hidden) ->
- *   tokens += ls2 (.) mlp_out [-> next block's LN1].
+ *   tokens += ls2 (.) mlp_out [-> camera overwrite -> next block's LN1].
  * Every view of a multi-view batch is processed in one launch per operation
  * (rows = view_count * tokens_per_view, view-major); q/k use
  * VK_QK_HEADS_OUTER for global layers and VK_QK_VIEWS_OUTER for local ones.
  * camera: [2*D] (reference view slot 0, source views slot 1,
- * backbone.rs:746-768) or NULL when alt_start < 0. */
+ * backbone.rs:746-768) or NULL when alt_start < 0; also read by the block
+ * before alt_start when it fuses the next LN1 (VK_BLOCK_FUSE_NEXT_LN1), so
+ * that the block at alt_start can take VK_BLOCK_SKIP_LN1 |
+ * VK_BLOCK_CAMERA_WRITTEN. */
 int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
                            size_t layer_idx, const vk_vit_layer* layer,
                            const vk_vit_layer* next_layer,

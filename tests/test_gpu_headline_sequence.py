@@ -2,9 +2,9 @@
 
 bench.py times the fused-op sequence of every block as bench.Model issues it
 (block_plan: LayerScale + residual fused with LN2, the LS2 residual fused with
-the next block's LN1 except before the camera-slot layer, the camera write at
-alt_start, global layers on the flattened views and local ones in the
-views-outer Q/K layout).  These tests issue the same Model block by block and
+the next block's LN1 -- before the camera-slot layer alt_start that pass also
+writes the camera slot -- global layers on the flattened views and local ones
+in the views-outer Q/K layout).  These tests issue the same Model block by block and
 chain the oracle's block_fused_ops beside it (the reference order of
 vit_block.rs:1019-1139 over the multi-view batch of backbone.rs:688-877),
 checking every output after every block at rtol 1e-5 / atol 1e-6:
@@ -26,7 +26,8 @@ LN2 of them meet the bar.  Besides, a free-running oracle chain of q, k and
 hidden (twelve or twenty-four re-normalisations and GELUs of the same
 buffers, each adding its rounding differences) is compared at the end
 within atol 1e-5.  After a block whose LS2 residual is fused with the next
-LN1, the LN1 buffer holds the next block's LN1 of the new tokens.
+LN1, the LN1 buffer holds the next block's LN1 of the new tokens (with the
+camera slot written when the next block is alt_start).
 """
 import numpy as np
 import pytest
@@ -41,6 +42,18 @@ import bench  # noqa: E402
 
 
 CHAIN_ATOL = 1e-5  # free-running q/k/hidden chain: accumulated over every block
+
+
+def with_camera(tokens, camera, views):
+    """tokens [rows, D] with row 0 of every view replaced by the camera
+    token: slot 0 for view 0, slot 1 for the others (backbone.rs:746-768)."""
+    out = tokens.copy()
+    D = out.shape[1]
+    tpv = out.shape[0] // views
+    cam = np.asarray(camera, np.float32).reshape(-1)
+    for v in range(views):
+        out[v * tpv] = cam[D:2 * D] if v > 0 else cam[:D]
+    return out
 
 
 def run_chain(rt, rng, views, shape, f16):
@@ -62,12 +75,15 @@ def run_chain(rt, rng, views, shape, f16):
         free_ref = ora(free["q"], free["k"], free["hidden"])
         model.enqueue_block(i)
         got = {n: model.act[n].numpy() for n in ("tokens", "ln1", "ln2", "q", "k", "hidden")}
+        want_tokens = ref["tokens"]
         if flags & vh.VK_BLOCK_FUSE_NEXT_LN1:
+            if i + 1 == shape.alt:  # the camera slot, written by this block's last pass
+                want_tokens = with_camera(want_tokens, model.camera_host, views)
             nl = model.host_layers[i + 1]
-            ln1 = oracle.layernorm(ref["tokens"], nl["norm1_gamma"], nl["norm1_beta"], eps)
+            ln1 = oracle.layernorm(want_tokens, nl["norm1_gamma"], nl["norm1_beta"], eps)
         else:
             ln1 = ref["ln1"]
-        assert np.array_equal(got["tokens"].reshape(ref["tokens"].shape), ref["tokens"]), \
+        assert np.array_equal(got["tokens"].reshape(want_tokens.shape), want_tokens), \
             f"tokens after block {i} differ from the oracle's chained residual stream"
         expect = {"ln1": ln1, "ln2": ref["ln2"], "q": ref["q"], "k": ref["k"],
                   "hidden": ref["hidden"]}
@@ -85,12 +101,43 @@ def run_chain(rt, rng, views, shape, f16):
 def test_vitb_12_views_12_blocks_as_benchmarked(rt, rng):
     model = run_chain(rt, rng, 12, bench.VITB, f16=False)
     assert model.rows == 10392
-    # the camera slot was written at alt_start: row 0 of view 0 from slot 0,
-    # row 0 of the other views from slot 1, then carried by the residual adds
-    assert model.plan[bench.ALT] & vh.VK_BLOCK_SKIP_LN1 == 0
+    # the camera slot was written before alt_start by the previous block's
+    # fused pass: row 0 of view 0 from slot 0, row 0 of the other views from
+    # slot 1, then carried by the residual adds
+    assert model.plan[bench.ALT] & vh.VK_BLOCK_CAMERA_WRITTEN
+    assert model.plan[bench.ALT - 1] & vh.VK_BLOCK_FUSE_NEXT_LN1
 
 
 def test_vitl_3458_rows_24_blocks_f16_parameters(rt, rng):
     model = run_chain(rt, rng, 1, bench.VITL, f16=True)
     assert model.rows == 3458
     assert all(v.dtype == np.float16 for v in model.host_layers[0].values())
+
+
+@pytest.mark.parametrize("views", [1, 3])
+def test_camera_write_fused_into_the_previous_pass(rt, rng, views):
+    """The block before alt_start fusing its LS2 residual with the next LN1
+    also writes the camera slot (VK_BLOCK_FUSE_NEXT_LN1 with a camera token),
+    and the block at alt_start then skips the write and its LN1
+    (VK_BLOCK_SKIP_LN1 | VK_BLOCK_CAMERA_WRITTEN): every output after both
+    blocks is bit-identical to the unfused order (LS2 residual; camera write
+    and LN1 in the block at alt_start)."""
+    outs = []
+    for fused in (False, True):
+        r = np.random.default_rng(7)
+        model = bench.Model(rt, r, views=views)
+        alt = bench.ALT
+        for i in range(alt + 1):
+            flags = model.plan[i]
+            if not fused and i == alt - 1:
+                flags &= ~vh.VK_BLOCK_FUSE_NEXT_LN1
+            if not fused and i == alt:
+                flags &= ~(vh.VK_BLOCK_SKIP_LN1 | vh.VK_BLOCK_CAMERA_WRITTEN)
+            nxt = model.structs[i + 1]
+            model.rt.vit_block_fused_ops(model.cfg, i, model.structs[i], nxt, model.act_struct,
+                                         model.shape.gh, model.shape.gw, views, model.camera,
+                                         flags)
+        outs.append({n: model.act[n].numpy() for n in ("tokens", "ln1", "ln2", "q", "k",
+                                                          "hidden")})
+    for n in outs[0]:
+        assert np.array_equal(outs[0][n], outs[1][n]), n

@@ -64,7 +64,8 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
   // one view; 746-768 per view: slot 0 for the reference view, slot 1 for the
   // source views).
   bool camera_written = false;
-  if (cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start)) {
+  if (cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start) &&
+      !(flags & VK_BLOCK_CAMERA_WRITTEN)) {
     VK_REQUIRE(camera != nullptr, "camera token required at alt_start=%d", cfg->alt_start);
     VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D, "camera token must hold >= %zu f32", D);
     VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
@@ -116,11 +117,22 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
   // GELU on the FC1 output
   VK_TRY(vk_gelu_f32_inplace(rt, act->hidden));
 
-  // tokens += ls2 (.) mlp_out [, next block's LN1]
+  // tokens += ls2 (.) mlp_out [, the camera-slot overwrite when the next
+  // block is alt_start and the camera token is given, next block's LN1]
   if (flags & VK_BLOCK_FUSE_NEXT_LN1) {
-    VK_TRY(vk_layerscale_residual_layernorm_f32(rt, act->tokens, act->mlp_out, layer->ls2,
-                                                next_layer->norm1_gamma, next_layer->norm1_beta,
-                                                rows, D, cfg->ln_eps, act->ln1));
+    const bool camera_next = cfg->alt_start >= 0 &&
+                             layer_idx + 1 == static_cast<size_t>(cfg->alt_start) &&
+                             camera != nullptr;
+    if (camera_next) {
+      VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D,
+                 "camera token must hold >= %zu f32", D);
+      VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
+                 "multi-view camera token must hold reference and source slots (2*%zu)", D);
+    }
+    VK_TRY(vk::ls_residual_layernorm_camera(
+        rt, act->tokens, act->mlp_out, layer->ls2, next_layer->norm1_gamma,
+        next_layer->norm1_beta, rows, D, cfg->ln_eps, act->ln1, camera_next ? camera : nullptr,
+        tpv));
   } else {
     VK_TRY(vk_layerscale_residual_f32(rt, act->tokens, act->mlp_out, layer->ls2, rows, D));
   }

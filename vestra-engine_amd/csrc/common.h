@@ -157,6 +157,15 @@ int device_copy(vk_runtime* rt, void* dst, const void* src, size_t bytes);
 // camera slot 0 (v == 0, the reference view) or slot 1 (source views).
 int write_camera_rows(vk_runtime* rt, float* tokens, const float* camera, size_t view_count,
                       size_t tokens_per_view, size_t D);
+// tokens += ls (.) y, the camera-token slot (row 0 of each view of
+// tokens_per_view rows) overwritten by `camera` when it is non-null, then
+// ln_out = LN(tokens): the fused LayerScale+residual+LayerNorm with the
+// overwrite that comes between them before block alt_start.
+int ls_residual_layernorm_camera(vk_runtime* rt, vk_tensor* x, const vk_tensor* y,
+                                 const vk_tensor* ls_gamma, const vk_tensor* ln_gamma,
+                                 const vk_tensor* ln_beta, size_t rows, size_t cols, float eps,
+                                 vk_tensor* ln_out, const vk_tensor* camera,
+                                 size_t tokens_per_view);
 
 // Q/K-norm + RoPE parameters of the QKV projection's fused epilogue: the
 // row's token index m gives its position (rows are view-major tokens).

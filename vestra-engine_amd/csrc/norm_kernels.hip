@@ -70,12 +70,17 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows(const float* x, 
 // ---------------------------------------------------------------------------
 // x += ls (.) yb (t = yb*ls rounded, x = x + t rounded); ln_out = LN(x).
 // HAS_LS false: unscaled residual add.  One wave per row.
+// CAM: the camera-token slot, row 0 of every view of tpv rows, then takes
+// the camera token (cam[0..cols) for view 0, cam[cols..2 cols) for the
+// others) in x and in the LayerNorm, as an overwrite between the residual
+// update and the LayerNorm would.
 // ---------------------------------------------------------------------------
-template <int NV, typename PT, bool HAS_LS, bool EXACT>
+template <int NV, typename PT, bool HAS_LS, bool EXACT, bool CAM = false>
 __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
     float* __restrict__ x, const float* __restrict__ yb, const PT* __restrict__ ls,
     const PT* __restrict__ gamma, const PT* __restrict__ beta,
-    float* __restrict__ ln_out, int rows, int cols, float eps) {
+    float* __restrict__ ln_out, int rows, int cols, float eps,
+    const float* __restrict__ cam, int tpv) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -83,6 +88,10 @@ __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
   const size_t base = static_cast<size_t>(row) * cols;
   float4* xr = reinterpret_cast<float4*>(x + base);
   const float4* yr = reinterpret_cast<const float4*>(yb + base);
+  // uniform over the wave
+  const float4* camr = CAM && row % tpv == 0
+                           ? reinterpret_cast<const float4*>(cam + (row >= tpv ? cols : 0))
+                           : nullptr;
   float4 v[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -103,6 +112,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
         a.z = a.z + b.z;
         a.w = a.w + b.w;
       }
+      if (CAM && camr) a = camr[c];
       vkd::st_stream(xr + c, a);
       v[i] = a;
     } else {
@@ -243,7 +253,7 @@ int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
 template <typename PT, bool HAS_LS>
 int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
                      const void* g, const void* b, float* out, int rows, int cols,
-                     float eps) {
+                     float eps, const float* cam = nullptr, int tpv = 1) {
   const int nv = ln_instance_cols(cols);
   dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
   auto LS = static_cast<const PT*>(ls);
@@ -251,10 +261,14 @@ int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
   auto B = static_cast<const PT*>(b);
 #define VK_LSLN_CASE(N)                                                                        \
   case N:                                                                                      \
-    if (cols == N * 256)                                                                       \
-      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps); \
+    if (cam && cols == N * 256)                                                                \
+      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, true, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
+    else if (cam)                                                                              \
+      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, false, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
+    else if (cols == N * 256)                                                                  \
+      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
     else                                                                                       \
-      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, false>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps); \
+      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, false>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
     break;
   switch (nv) {
     VK_LSLN_CASE(1) VK_LSLN_CASE(2) VK_LSLN_CASE(3) VK_LSLN_CASE(4)
@@ -421,6 +435,19 @@ int vk_layerscale_residual_layernorm_f32(vk_runtime* rt, vk_tensor* x, const vk_
                                          const vk_tensor* ln_gamma,
                                          const vk_tensor* ln_beta, size_t rows,
                                          size_t cols, float eps, vk_tensor* ln_out) {
+  return vk::ls_residual_layernorm_camera(rt, x, y, ls_gamma, ln_gamma, ln_beta, rows, cols, eps,
+                                          ln_out, nullptr, 0);
+}
+
+}  // extern "C"
+
+namespace vk {
+
+int ls_residual_layernorm_camera(vk_runtime* rt, vk_tensor* x, const vk_tensor* y,
+                                 const vk_tensor* ls_gamma, const vk_tensor* ln_gamma,
+                                 const vk_tensor* ln_beta, size_t rows, size_t cols, float eps,
+                                 vk_tensor* ln_out, const vk_tensor* camera,
+                                 size_t tokens_per_view) {
   VK_TRY(vk::bind(rt));
   VK_REQUIRE(x && y && ln_out, "null tensor");
   VK_REQUIRE(x->dtype == VK_F32 && y->dtype == VK_F32 && ln_out->dtype == VK_F32,
@@ -437,19 +464,35 @@ int vk_layerscale_residual_layernorm_f32(vk_runtime* rt, vk_tensor* x, const vk_
   VK_UNSUPPORTED_IF(cols == 0 || cols % 4 != 0 || cols > 8192 || ln_instance_cols(static_cast<int>(cols)) < 0,
                     "ls_residual_layernorm: cols=%zu", cols);
   VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "rows=%zu too large", rows);
+  if (camera) {
+    VK_REQUIRE(camera->dtype == VK_F32, "camera token must be f32");
+    VK_REQUIRE(tokens_per_view > 0 && rows % tokens_per_view == 0 &&
+                   tokens_per_view <= 0x7fffffffULL,
+               "rows=%zu is not a whole number of views of %zu tokens", rows, tokens_per_view);
+    VK_REQUIRE(camera->len >= (rows > tokens_per_view ? 2 : 1) * cols,
+               "camera token must hold %s (%zu f32)",
+               rows > tokens_per_view ? "reference and source slots" : "one slot",
+               (rows > tokens_per_view ? 2 : 1) * cols);
+  }
   if (rows == 0) return VK_OK;
   float* X = static_cast<float*>(x->ptr);
   const float* Yb = static_cast<const float*>(y->ptr);
   float* O = static_cast<float*>(ln_out->ptr);
   const int r = static_cast<int>(rows), c = static_cast<int>(cols);
   const void* ls = ls_gamma ? ls_gamma->ptr : nullptr;
+  const float* cam = camera ? static_cast<const float*>(camera->ptr) : nullptr;
+  const int tpv = camera ? static_cast<int>(tokens_per_view) : 1;
   if (ln_gamma->dtype == VK_F16) {
-    return ls ? launch_ls_res_ln<uint16_t, true>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps)
-              : launch_ls_res_ln<uint16_t, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps);
+    return ls ? launch_ls_res_ln<uint16_t, true>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps, cam, tpv)
+              : launch_ls_res_ln<uint16_t, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps, cam, tpv);
   }
-  return ls ? launch_ls_res_ln<float, true>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps)
-            : launch_ls_res_ln<float, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps);
+  return ls ? launch_ls_res_ln<float, true>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps, cam, tpv)
+            : launch_ls_res_ln<float, false>(rt, X, Yb, ls, ln_gamma->ptr, ln_beta->ptr, O, r, c, eps, cam, tpv);
 }
+
+}  // namespace vk
+
+extern "C" {
 
 int vk_qk_norm_rope_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
                              const vk_tensor* q_gamma, const vk_tensor* q_beta,

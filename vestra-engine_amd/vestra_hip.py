@@ -40,6 +40,7 @@ VK_RESIZE_BILINEAR, VK_RESIZE_CUBIC, VK_RESIZE_AREA = 0, 1, 2
 VK_BLOCK_FUSE_LS_LN = 1
 VK_BLOCK_SKIP_LN1 = 2
 VK_BLOCK_FUSE_NEXT_LN1 = 4
+VK_BLOCK_CAMERA_WRITTEN = 8
 
 QK_NORM_EPS = 1e-5  # vit_block.rs:686
 
