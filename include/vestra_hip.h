@@ -728,7 +728,8 @@ int vk_event_elapsed_ms(vk_event* start, vk_event* stop, float* ms);
  * into a HIP graph, replayed with vk_graph_launch.  Nothing is allocated
  * while the stream captures: the runtime's work buffer (split-K partial sums
  * of linears over few rows, the key-split partials of attention over few
- * query tiles, the row statistics of vk_token_to_chw_f32) and its RoPE
+ * or unevenly spread query tiles, the row statistics of
+ * vk_token_to_chw_f32) and its RoPE
  * tables grow only outside capture, so a sequence is run once eagerly
  * before it is captured; a call that would grow them during capture fails
  * with an error and enqueues nothing.  Buffers they replace stay valid for
