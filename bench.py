@@ -836,7 +836,7 @@ def main():
                     help="profile mode: launch only this operation (12-view shape, rotating "
                          "buffers) after one calibration device copy of 256 MiB")
     ap.add_argument("--op-views", type=int, default=12,
-                    help="profile mode: view count of the operation's shape (866 rows each)")
+                    help="profile and headline modes: view count of the shape (866 rows each)")
     ap.add_argument("--linear", action="store_true",
                     help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
                          "at the 12-view shape")
@@ -917,8 +917,9 @@ def main():
                           "calibration_copy_bytes": 2 * (256 << 20), **table[args.op]}),
               flush=True)
         return
-    log(f"device has {rt.cu_count()} CUs; building 12-view workload ({TPV * 12} rows)")
-    model = Model(rt, rng, views=12)
+    views = args.op_views if args.headline else 12
+    log(f"device has {rt.cu_count()} CUs; building {views}-view workload ({TPV * views} rows)")
+    model = Model(rt, rng, views=views)
     nbytes = model.step_bytes()
 
     model.enqueue_step()  # builds the RoPE table before capture
