@@ -395,9 +395,11 @@ def linear_epilogue_timing(rt, rng, rows, iters):
 
 
 def full_block_timing(rt, rng, reps=3):
-    """The whole ViT block on the device (vk_vit_block_forward_f32: LN1, QKV
-    storing head-major Q/K/V, Q/K-norm + RoPE, attention, projection + LS +
-    residual, LN2, FC1 + GELU, FC2 + LS + residual), 12 ViT-B blocks with
+    """The whole ViT block on the device: 12 ViT-B blocks through the
+    backbone's block loop without captures (vk_backbone_forward_f32; per
+    block LN1, QKV storing head-major Q/K/V, Q/K-norm + RoPE, attention,
+    projection + LS + residual, LN2, FC1 + GELU, FC2 + LS + residual, the
+    next block's LN1 taken by FC2's split-K sum pass where it has one) with
     random-init weights, local/global alternation from alt_start 4, captured
     in one HIP graph: single image (866 tokens) and the 12-view sequence
     (10,392 rows).  FLOP = the four projections (2*rows*D*(3D + D + 2M)) plus
@@ -434,8 +436,8 @@ def full_block_timing(rt, rng, reps=3):
         ws = rt.block_workspace(rows, D, M)
 
         def step():
-            for i, w in enumerate(blocks):
-                rt.vit_block_forward_f32(cfg, i, w, tokens, GH, GW, views, camera, ws.struct)
+            rt.backbone_forward_f32(cfg, blocks, tokens, GH, GW, views, camera, None, None,
+                                    False, [], [], [], ws, None)
 
         step()  # builds the RoPE table before capture
         graph = capture(rt, step)
@@ -555,8 +557,9 @@ L_TPV = 1 + NREG + L_GH * L_GW  # 3458
 def vitl_timing(rt, rng, reps=3):
     """The ViT-L 1008x672 configuration with F16-stored weights: the 24-block
     fused-op sequence (parameter vectors in f16, widened in registers) and the
-    24 whole blocks on the device with the projection weights uploaded as
-    F16 and expanded on the device (vk_linear_prepare_w16)."""
+    24 whole blocks on the device (the backbone's block loop without
+    captures) with the projection weights uploaded as F16 and expanded on
+    the device (vk_linear_prepare_w16)."""
     import vestra_hip as vh
     rows = L_TPV
 
@@ -615,8 +618,8 @@ def vitl_timing(rt, rng, reps=3):
     ws = rt.block_workspace(rows, L_D, L_M)
 
     def block_step():
-        for i, w in enumerate(blocks):
-            rt.vit_block_forward_f32(cfg, i, w, tokens, L_GH, L_GW, 1, camera, ws.struct)
+        rt.backbone_forward_f32(cfg, blocks, tokens, L_GH, L_GW, 1, camera, None, None, False,
+                                [], [], [], ws, None)
 
     block_step()
     graph = capture(rt, block_step)

@@ -694,8 +694,10 @@ int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
 
 /* The backbone's block loop on the device: Backbone::forward /
  * forward_multi_view_ordered (backbone.rs:390-532, 688-877) over `depth`
- * blocks (blocks[layer], vk_vit_block_forward_f32 each) on the view-major
- * tokens [view_count * (1+num_register+gh*gw), D], in place.  At each
+ * blocks (blocks[layer], the bits of vk_vit_block_forward_f32 each; the
+ * FC2 of every block but the last and the one before alt_start also writes
+ * the next block's LN1, in its split-K sum pass when it has one) on the
+ * view-major tokens [view_count * (1+num_register+gh*gw), D], in place.  At each
  * out_layers[i] (in the caller's order) the capture of vk_capture_f32 with
  * the final vit.norm (norm_gamma/beta, cfg->ln_eps) fills feats[i]
  * [views, gh*gw, W] and cams[i] [views, W] (W = 2D with cat_token, else D);

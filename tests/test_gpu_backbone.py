@@ -73,6 +73,43 @@ def test_backbone_forward(rt, rng, D, H, M, gh, gw, views, depth, alt, outs, cat
         assert_envelope(cams[i].numpy(), caps[i][1], caps64[i][1], f"cam {outs[i]}")
 
 
+@pytest.mark.parametrize("D,H,M,gh,gw,f16", [
+    pytest.param(768, 12, 3072, 24, 36, False, id="vitb-504x336"),
+    pytest.param(1024, 16, 4096, 48, 72, True, id="vitl-1008x672-f16-params"),
+])
+def test_backbone_block_loop_full_size(rt, rng, D, H, M, gh, gw, f16):
+    """One image at full size through the block loop, where FC2 runs split-K
+    and its sum pass also writes the next block's LN1: the bits of the
+    per-block entry called block by block.  Four blocks with alt_start 2:
+    blocks 0 and 2 hand LN1 on, block 1 precedes the camera write and block
+    3 is the last."""
+    cfg = config(D, H, M, alt=2)
+    rows = 2 + gh * gw
+    devs = []
+    for _ in range(4):
+        p = make_params(rng, D, M)
+        dev = DeviceBlock(rt, p, D, M)
+        if f16:
+            dev.vec = {k: rt.upload_f16(v) for k, v in p.items()
+                       if not k.endswith(("_w", "_b"))}
+            dev.struct = vh.block_weights_struct(qkv=dev.qkv, proj=dev.proj, fc1=dev.fc1,
+                                                 fc2=dev.fc2, **dev.vec)
+        devs.append(dev)
+    x0 = normals(rng, rows, D)
+    cam = rt.upload_f32(normals(rng, 2 * D))
+    vcfg = vh.VitConfig(**cfg)
+
+    tokens, ws = rt.upload_f32(x0), rt.block_workspace(rows, D, M)
+    rt.backbone_forward_f32(vcfg, [d.struct for d in devs], tokens, gh, gw, 1, cam, None, None,
+                            False, [], [], [], ws, None)
+    t2, ws2 = rt.upload_f32(x0), rt.block_workspace(rows, D, M)
+    for layer, dev in enumerate(devs):
+        rt.vit_block_forward_f32(vcfg, layer, dev.struct, t2, gh, gw, 1, cam, ws2.struct)
+    assert np.array_equal(tokens.numpy(), t2.numpy())
+    for name in ("ln", "q", "k", "v", "attn", "hidden"):
+        assert np.array_equal(ws.tensors[name].numpy(), ws2.tensors[name].numpy()), name
+
+
 def test_backbone_forward_errors(rt, rng):
     D, H, M = 768, 12, 3072
     cfg = vh.VitConfig(**config(D, H, M))

@@ -151,7 +151,8 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
 // output projection reads the attention output head-major, so the
 // reference's split_qkv_hnd / hnd_to_token passes (vit_block.rs:539-541, 560)
 // are not separate launches, and Q/K-norm + RoPE run in the QKV epilogue.
-// 7 launches per block.
+// 7 launches per block; in the backbone's block loop FC2 also writes the
+// next block's LN1, one launch fewer wherever FC2 runs split-K.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -163,13 +164,15 @@ int check_linear(const vk_linear* l, size_t in, size_t out, const char* name) {
   return VK_OK;
 }
 
-}  // namespace
-
-extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
-                                        size_t layer_idx, const vk_vit_block_weights* w,
-                                        vk_tensor* tokens, size_t gh, size_t gw,
-                                        size_t view_count, const vk_tensor* camera,
-                                        const vk_vit_block_workspace* ws) {
+// One block.  next != NULL: FC2's residual pass also writes the next
+// block's LN1 (next->norm1) into ws->ln, in its split-K sum pass when it has
+// one (the bits of the separate LayerNorm); ln1_done: this block's LN1 is
+// already in ws->ln, written so by the previous block.  Neither is used
+// across alt_start, where the camera slot is overwritten before LN1.
+int block_forward(vk_runtime* rt, const vk_vit_config* cfg, size_t layer_idx,
+                  const vk_vit_block_weights* w, vk_tensor* tokens, size_t gh, size_t gw,
+                  size_t view_count, const vk_tensor* camera, const vk_vit_block_workspace* ws,
+                  const vk_vit_block_weights* next, bool ln1_done) {
   VK_TRY(vk::bind(rt));
   VK_REQUIRE(cfg && w && tokens && ws, "null argument");
   VK_REQUIRE(view_count > 0 && gw > 0 && gh > 0, "empty grid or view count");
@@ -198,7 +201,11 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
   const bool global = layer_uses_global(cfg, layer_idx);
 
   // camera-token slot write at alt_start (backbone.rs:446-457, 746-768)
-  if (cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start)) {
+  const bool at_alt = cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start);
+  VK_REQUIRE(!(ln1_done && at_alt), "block: LN1 cannot precede the camera write at alt_start");
+  VK_REQUIRE(!(next && cfg->alt_start >= 0 && layer_idx + 1 == static_cast<size_t>(cfg->alt_start)),
+             "block: the next block's LN1 follows its camera write at alt_start");
+  if (at_alt) {
     VK_REQUIRE(camera != nullptr, "camera token required at alt_start=%d", cfg->alt_start);
     VK_REQUIRE(camera->dtype == VK_F32 && camera->len >= D, "camera token must hold >= %zu f32", D);
     VK_REQUIRE(view_count == 1 || camera->len >= 2 * D,
@@ -210,8 +217,9 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
   // LN1 -> QKV (head-major Q, K, V) with Q/K-norm + RoPE, gated as in
   // vk_vit_block_fused_ops (vit_block.rs:835-838); with RoPE on, both run
   // in the projection's epilogue (the bits of the separate pass)
-  VK_TRY(vk_layernorm_into_f32(rt, tokens, w->norm1_gamma, w->norm1_beta, rows, D, cfg->ln_eps,
-                               ws->ln));
+  if (!ln1_done)
+    VK_TRY(vk_layernorm_into_f32(rt, tokens, w->norm1_gamma, w->norm1_beta, rows, D,
+                                 cfg->ln_eps, ws->ln));
   const bool use_qknorm = cfg->qknorm_start >= 0 &&
                           static_cast<long long>(layer_idx) >= cfg->qknorm_start &&
                           w->qnorm_gamma != nullptr;
@@ -243,10 +251,26 @@ extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg
   VK_TRY(vk::linear_hnd_residual_layernorm(rt, w->proj, ws->attn, rows, H, hd, tokens,
                                            w->norm2_gamma, w->norm2_beta, cfg->ln_eps, ws->ln));
 
-  // FC1 + GELU -> tokens += (hidden @ Wfc2 + b) * ls2
+  // FC1 + GELU -> tokens += (hidden @ Wfc2 + b) * ls2 [-> next block's LN1]
   VK_TRY(vk_linear_run_gelu_f32(rt, w->fc1, ws->ln, rows, ws->hidden));
-  VK_TRY(vk_linear_run_residual_f32(rt, w->fc2, ws->hidden, rows, tokens));
-  return VK_OK;
+  if (next) {
+    VK_REQUIRE(next->norm1_gamma && next->norm1_beta, "next block's norm1 is null");
+    return vk::linear_residual_layernorm(rt, w->fc2, ws->hidden, rows, tokens,
+                                         next->norm1_gamma, next->norm1_beta, cfg->ln_eps,
+                                         ws->ln);
+  }
+  return vk_linear_run_residual_f32(rt, w->fc2, ws->hidden, rows, tokens);
+}
+
+}  // namespace
+
+extern "C" int vk_vit_block_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
+                                        size_t layer_idx, const vk_vit_block_weights* w,
+                                        vk_tensor* tokens, size_t gh, size_t gw,
+                                        size_t view_count, const vk_tensor* camera,
+                                        const vk_vit_block_workspace* ws) {
+  return block_forward(rt, cfg, layer_idx, w, tokens, gh, gw, view_count, camera, ws, nullptr,
+                       false);
 }
 
 // ---------------------------------------------------------------------------
@@ -289,9 +313,16 @@ extern "C" int vk_backbone_forward_f32(vk_runtime* rt, const vk_vit_config* cfg,
   const bool keep_local = cat_token && any_global_capture;
   if (keep_local) VK_TRY(check_len(local_x, rows * D, "local_x"));
   if (keep_local) VK_TRY(vk_copy_segment_into_f32(rt, local_x, 0, tokens, 0, rows * D));
+  // each block but the last, and the one before alt_start, finishes with the
+  // next block's LN1 (one launch fewer where FC2 runs split-K)
+  bool ln1_done = false;
   for (size_t layer = 0; layer < depth; ++layer) {
-    VK_TRY(vk_vit_block_forward_f32(rt, cfg, layer, &blocks[layer], tokens, gh, gw, view_count,
-                                    camera, ws));
+    const bool fuse_next =
+        layer + 1 < depth &&
+        !(cfg->alt_start >= 0 && layer + 1 == static_cast<size_t>(cfg->alt_start));
+    VK_TRY(block_forward(rt, cfg, layer, &blocks[layer], tokens, gh, gw, view_count, camera, ws,
+                         fuse_next ? &blocks[layer + 1] : nullptr, ln1_done));
+    ln1_done = fuse_next;
     const bool global = layer_uses_global(cfg, layer);
     for (size_t i = 0; i < n_out; ++i) {
       if (static_cast<size_t>(out_layers[i]) != layer) continue;

@@ -253,6 +253,13 @@ int linear_hnd_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk
                                   vk_tensor* residual, const vk_tensor* gamma,
                                   const vk_tensor* beta, float eps, vk_tensor* ln_out);
 
+// The same for a token-major input: vk_linear_run_residual_f32 +
+// vk_layernorm_into_f32 with the same bits (the block loop's FC2 followed by
+// the next block's LN1).
+int linear_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                              size_t rows, vk_tensor* residual, const vk_tensor* gamma,
+                              const vk_tensor* beta, float eps, vk_tensor* ln_out);
+
 }  // namespace vk
 
 #define VK_REQUIRE(cond, ...)                              \

@@ -869,39 +869,74 @@ int expand_flat(vk_runtime* rt, int src_kind, const vk_tensor* src, size_t n, vk
 
 namespace vk {
 
-int linear_hnd_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
-                                  size_t rows, size_t heads, size_t head_dim,
-                                  vk_tensor* residual, const vk_tensor* gamma,
-                                  const vk_tensor* beta, float eps, vk_tensor* ln_out) {
+namespace {
+
+// The residual projection followed by ln_out = LayerNorm(residual), for a
+// token-major input (heads == 0) or a head-major one.  The wide kernel takes
+// the LayerNorm into its split-K sum pass; an input it cannot read (K % 4 or
+// alignment) runs the two calls.
+int residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
+                       size_t heads, size_t head_dim, vk_tensor* residual,
+                       const vk_tensor* gamma, const vk_tensor* beta, float eps,
+                       vk_tensor* ln_out) {
   VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && hnd && residual && gamma && beta && ln_out, "null argument");
-  VK_TRY(check_linear(lin, hnd, rows));
-  VK_TRY(check_head_layout(lin, hnd, heads, head_dim));
-  VK_REQUIRE(lin->in_features == heads * head_dim,
-             "linear_hnd_residual_layernorm: in_features=%zu, expected heads*64=%zu",
-             lin->in_features, heads * head_dim);
-  VK_TRY(check_linear_out(lin, hnd, residual, rows, "residual"));
+  VK_REQUIRE(lin && x && residual && gamma && beta && ln_out, "null argument");
+  VK_TRY(check_linear(lin, x, rows));
+  if (heads > 0) {
+    VK_TRY(check_head_layout(lin, x, heads, head_dim));
+    VK_REQUIRE(lin->in_features == heads * head_dim,
+               "linear_residual_layernorm: in_features=%zu, expected heads*64=%zu",
+               lin->in_features, heads * head_dim);
+  }
+  VK_TRY(check_linear_out(lin, x, residual, rows, "residual"));
   const size_t n = lin->out_features;
   VK_REQUIRE((gamma->dtype == VK_F32 || gamma->dtype == VK_F16) && gamma->dtype == beta->dtype &&
                  gamma->len == n && beta->len == n,
-             "linear_hnd_residual_layernorm: gamma/beta must be f32 or f16 [%zu]", n);
+             "linear_residual_layernorm: gamma/beta must be f32 or f16 [%zu]", n);
+  VK_UNSUPPORTED_IF(n > 8192, "linear_residual_layernorm: out_features=%zu (LayerNorm rows of "
+                    "at most 8192)", n);
   VK_REQUIRE(ln_out->dtype == VK_F32 && ln_out->len == rows * n,
-             "linear_hnd_residual_layernorm: ln_out must be f32 [%zu]", rows * n);
-  VK_REQUIRE(tensors_disjoint(ln_out, residual) && tensors_disjoint(ln_out, hnd),
-             "linear_hnd_residual_layernorm: ln_out must not overlap the other tensors");
+             "linear_residual_layernorm: ln_out must be f32 [%zu]", rows * n);
+  VK_REQUIRE(tensors_disjoint(ln_out, residual) && tensors_disjoint(ln_out, x),
+             "linear_residual_layernorm: ln_out must not overlap the other tensors");
   for (const vk_tensor* t : {static_cast<const vk_tensor*>(residual), gamma, beta,
                              static_cast<const vk_tensor*>(ln_out)})
     VK_REQUIRE(reinterpret_cast<uintptr_t>(t->ptr) % 16 == 0,
-               "linear_hnd_residual_layernorm: tensors must be 16-byte aligned");
+               "linear_residual_layernorm: tensors must be 16-byte aligned");
   if (rows == 0) return VK_OK;
-  LinearArgs g = linear_args(lin, hnd, rows, residual);
-  g.a_hnd = 1;
+  const bool wide = lin->in_features % 4 == 0 && reinterpret_cast<uintptr_t>(x->ptr) % 16 == 0;
+  if (!wide) {
+    VK_TRY(launch_linear(rt, lin, x, rows, residual, kLinResidual));
+    return vk::layernorm_raw(rt, static_cast<const float*>(residual->ptr),
+                             static_cast<float*>(ln_out->ptr), gamma->ptr, beta->ptr,
+                             gamma->dtype == VK_F16, static_cast<int>(rows),
+                             static_cast<int>(n), eps);
+  }
+  LinearArgs g = linear_args(lin, x, rows, residual);
+  g.a_hnd = heads > 0 ? 1 : 0;
   g.ln_gamma = gamma->ptr;
   g.ln_beta = beta->ptr;
   g.ln_f16 = gamma->dtype == VK_F16 ? 1 : 0;
   g.ln_eps = eps;
   g.ln_out = static_cast<float*>(ln_out->ptr);
   return vk::launch_linear_wide(rt, g, kLinResidual);
+}
+
+}  // namespace
+
+int linear_hnd_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
+                                  size_t rows, size_t heads, size_t head_dim,
+                                  vk_tensor* residual, const vk_tensor* gamma,
+                                  const vk_tensor* beta, float eps, vk_tensor* ln_out) {
+  VK_REQUIRE(heads > 0, "linear: heads must be positive");
+  return residual_layernorm(rt, lin, hnd, rows, heads, head_dim, residual, gamma, beta, eps,
+                            ln_out);
+}
+
+int linear_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
+                              size_t rows, vk_tensor* residual, const vk_tensor* gamma,
+                              const vk_tensor* beta, float eps, vk_tensor* ln_out) {
+  return residual_layernorm(rt, lin, x, rows, 0, 0, residual, gamma, beta, eps, ln_out);
 }
 
 }  // namespace vk

@@ -785,11 +785,13 @@ class Runtime:
 
     def backbone_forward_f32(self, cfg: VitConfig, blocks: Sequence[VitBlockWeights],
                              tokens: Tensor, gh: int, gw: int, view_count: int,
-                             camera: Optional[Tensor], norm_gamma: Tensor, norm_beta: Tensor,
-                             cat_token: bool, out_layers: Sequence[int],
+                             camera: Optional[Tensor], norm_gamma: Optional[Tensor],
+                             norm_beta: Optional[Tensor], cat_token: bool,
+                             out_layers: Sequence[int],
                              feats: Sequence[Tensor], cams: Sequence[Tensor],
                              ws: "BlockWorkspace", local_x: Optional[Tensor]) -> None:
-        """Backbone::forward_multi_view_ordered: all blocks + captures on the device."""
+        """Backbone::forward_multi_view_ordered: all blocks + captures on the device
+        (norm_gamma / norm_beta are read by the captures only)."""
         arr = (VitBlockWeights * len(blocks))(*blocks)
         n = len(out_layers)
         layers = (C.c_int * max(n, 1))(*out_layers)
@@ -797,7 +799,7 @@ class Runtime:
         ca = (_vp * max(n, 1))(*[c.handle.value for c in cams])
         _check(lib.vk_backbone_forward_f32(self.handle, C.byref(cfg), len(blocks), arr,
                                            tokens.handle, gh, gw, view_count, _h(camera),
-                                           norm_gamma.handle, norm_beta.handle,
+                                           _h(norm_gamma), _h(norm_beta),
                                            1 if cat_token else 0, layers, n, fa, ca,
                                            C.byref(ws.struct), _h(local_x)))
 
