@@ -686,9 +686,10 @@ void launch_pair(vk_runtime* rt, const LinearArgs& g, const Plan& plan, dim3 gri
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g0, int epi, float* partial,
                        size_t partial_floats) {
   LinearArgs g = g0;
-  // An output element's bits depend on the split count only, so the plan
-  // depends on (M, N, K) alone and every layout and epilogue of one shape
-  // gives the same bits.
+  // An output element's bits depend on the plan (its split count, and the
+  // two k groups of a 64 x 64 tile, added at the end) and the plan on
+  // (M, N, K) alone, so every layout and epilogue of one shape gives the
+  // same bits.
   const Plan plan = choose_plan(rt, g.M, g.N, g.K);
   g.splits = plan.splits;
   g.partial = nullptr;
