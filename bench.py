@@ -462,7 +462,8 @@ def pipeline_timing(rt, rng, reps=3):
     """The image-to-head-input path on the device, per frame: a 427x640 u8
     camera frame resized and patch-snapped to 336x504 (area resampling,
     vk_preprocess_resize_u8), the fused patch embedding with the bicubic
-    position table (built once and cached, as PosEmbedCache does), the 12
+    position table (built once and cached, as PosEmbedCache does; every
+    frame of a pass in one launch, vk_patch_embed_views_u8), the 12
     ViT-B blocks with captures at layers 2, 5, 8, 11 (vk_backbone_forward_f32,
     cat_token) and the head's LayerNorm + token -> CHW hand-off of each
     capture (vk_token_to_chw_f32).  One frame, and 12 frames as one
@@ -510,9 +511,9 @@ def pipeline_timing(rt, rng, reps=3):
         rows = TPV * views
         frames = [rt.upload_u8(rng.integers(0, 256, (fh, fw, 3), dtype=np.uint8))
                   for _ in range(views)]
-        resized = [rt.alloc_u8(oh * ow * 3) for _ in range(views)]
+        resized_all = rt.alloc_u8(views * oh * ow * 3)
+        resized = [resized_all.view(v * oh * ow * 3, oh * ow * 3) for v in range(views)]
         tokens = rt.alloc_f32(rows * D)
-        token_views = [tokens.view(v * TPV * D, TPV * D) for v in range(views)]
         ws = rt.block_workspace(rows, D, M)
         local = rt.alloc_f32(rows * D)
         feats = [rt.alloc_f32(views * n_patch * 2 * D) for _ in OUT_LAYERS]
@@ -528,8 +529,8 @@ def pipeline_timing(rt, rng, reps=3):
                 vh._check(vh.lib.vk_preprocess_resize_u8(rt.handle, frames[v].handle, fh, fw, 504,
                                                          14, 1, pre_ws[v].handle,
                                                          resized[v].handle))
-                rt.patch_embed_u8(resized[v], oh, ow, 14, mean, std, patch, cls, reg, NREG, pos,
-                                  token_views[v])
+            rt.patch_embed_views_u8(resized_all, views, oh, ow, 14, mean, std, patch, cls, reg,
+                                    NREG, pos, tokens)
             rt.backbone_forward_f32(cfg, blocks, tokens, gh, gw, views, camera, vit_ng, vit_nb,
                                     True, OUT_LAYERS, feats, cams, ws, local)
             for i in range(len(OUT_LAYERS)):
@@ -664,34 +665,40 @@ def attention_timing(rt, rng, iters):
     return out
 
 
-def patch_embed_timing(rt, rng, h, w, embed, iters):
-    """Fused patch embedding of one u8 image (normalise, unfold, F32-MFMA
-    projection, bias, position add, special rows): time per image and the
-    projection's FLOP rate against the F32 matrix peak."""
+def patch_embed_timing(rt, rng, h, w, embed, iters, views=1):
+    """Fused patch embedding of u8 images (normalise, unfold, F32-MFMA
+    projection, bias, position add, special rows): one image per launch, or
+    `views` images of one shape in one launch (vk_patch_embed_views_u8, the
+    multi-view preparation); time per image and the projection's FLOP rate
+    against the F32 matrix peak."""
     gh, gw = h // 14, w // 14
-    img = rt.upload_u8(rng.integers(0, 256, (h, w, 3), dtype=np.uint8))
+    img = rt.upload_u8(rng.integers(0, 256, (views, h, w, 3), dtype=np.uint8))
     wt = (0.02 * rng.standard_normal((embed, 3, 14, 14))).astype(np.float32)
     bias = (0.02 * rng.standard_normal(embed)).astype(np.float32)
     proj = rt.prepare_linear_oihw_f32(588, embed, wt, bias)
     cls = rt.upload_f32((0.02 * rng.standard_normal(embed)).astype(np.float32))
     regs = rt.upload_f32((0.02 * rng.standard_normal(embed)).astype(np.float32))
     pos = rt.upload_f32((0.02 * rng.standard_normal((1 + gh * gw) * embed)).astype(np.float32))
-    out = rt.alloc_f32((2 + gh * gw) * embed)
+    out = rt.alloc_f32(views * (2 + gh * gw) * embed)
     mean, std = [0.485, 0.456, 0.406], [0.229, 0.224, 0.225]
 
     def fn():
-        rt.patch_embed_u8(img, h, w, 14, mean, std, proj, cls, regs, 1, pos, out)
+        if views == 1:
+            rt.patch_embed_u8(img, h, w, 14, mean, std, proj, cls, regs, 1, pos, out)
+        else:
+            rt.patch_embed_views_u8(img, views, h, w, 14, mean, std, proj, cls, regs, 1, pos,
+                                    out)
 
     for _ in range(3):
         fn()
     graph = capture(rt, fn, iters)
     graph.launch()
-    us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / iters
+    us = statistics.median(time_loop(rt, graph.launch, 1) * 1e3 / (iters * views)
                            for _ in range(OP_TRIALS))
     flop = 2 * gh * gw * 588 * embed
     tflops = flop / (us * 1e-6) / 1e12
-    return {"image": f"{h}x{w}", "patches": gh * gw, "embed": embed, "us": round(us, 3),
-            "flop": flop, "TFLOP_s": round(tflops, 2),
+    return {"image": f"{h}x{w}", "views_per_launch": views, "patches": gh * gw,
+            "embed": embed, "us": round(us, 3), "flop": flop, "TFLOP_s": round(tflops, 2),
             "frac_of_f32_mfma_peak": round(tflops / MFMA_F32_PEAK_TFLOPS, 4)}
 
 
@@ -840,6 +847,8 @@ def main():
                          "buffers) after one calibration device copy of 256 MiB")
     ap.add_argument("--op-views", type=int, default=12,
                     help="profile and headline modes: view count of the shape (866 rows each)")
+    ap.add_argument("--patch-views", type=int, default=1,
+                    help="--op patch_embed: images per launch (vk_patch_embed_views_u8)")
     ap.add_argument("--linear", action="store_true",
                     help="linear mode: FC1+GELU and FC2+LayerScale+residual fused vs unfused "
                          "at the 12-view shape")
@@ -903,7 +912,8 @@ def main():
         return
     if args.op == "patch_embed":
         print(json.dumps({"op": "patch_embed",
-                          **patch_embed_timing(rt, rng, 336, 504, D, args.op_iters)}), flush=True)
+                          **patch_embed_timing(rt, rng, 336, 504, D, args.op_iters,
+                                               views=args.patch_views)}), flush=True)
         return
     if args.op:
         # calibration: a plain device copy of known size, for scaling the
@@ -968,6 +978,7 @@ def main():
     tau0 = dispatch_overhead(rt)
     log("patch embedding")
     patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
+             patch_embed_timing(rt, rng, 336, 504, D, max(1, args.op_iters // 12), views=12),
              patch_embed_timing(rt, rng, 672, 1008, 1024, args.op_iters)]
     gelu = ops12["gelu"]
     log("fused linear epilogues")

@@ -526,6 +526,20 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h,
                       size_t n_register, const vk_tensor* pos_table,
                       vk_tensor* out);
 
+/* vk_patch_embed_u8 for every view of a multi-view batch in one launch:
+ * the per-view preprocess + prepare_tokens loop of prepare_multi_view
+ * (engine.rs:573-626), whose views share one processed shape
+ * (engine.rs:594-605).  images: u8 [views, h, w, 3], every view 8-byte
+ * aligned (h*w*3 % 8 == 0 when views > 1, else VK_ERR_UNSUPPORTED); out:
+ * the view-major tokens [views * (1 + n_register + gh*gw), embed], each
+ * view's rows the bits vk_patch_embed_u8 writes for that image. */
+int vk_patch_embed_views_u8(vk_runtime* rt, const vk_tensor* images,
+                            size_t views, size_t h, size_t w, size_t patch,
+                            const float mean[3], const float std_[3],
+                            const vk_linear* proj, const vk_tensor* cls,
+                            const vk_tensor* registers, size_t n_register,
+                            const vk_tensor* pos_table, vk_tensor* out);
+
 /* ------------------------------------------------------------------ */
 /* backbone capture and head hand-off                                   */
 /* ------------------------------------------------------------------ */

@@ -338,6 +338,44 @@ def test_patch_embed_f16_filter_vitl_matches_oracle(rt, rng):
                       "patch_embed 672x1008 f16 filter")
 
 
+@pytest.mark.parametrize("h,w,embed,views,n_register", [(336, 504, 768, 12, 1),
+                                                        (28, 42, 16, 5, 0)])
+def test_patch_embed_views_match_single_views(rt, rng, h, w, embed, views, n_register):
+    """All views of one processed shape in one launch (the per-view loop of
+    prepare_multi_view, engine.rs:573-626): every view's tokens carry the
+    bits of its own vk_patch_embed_u8 call."""
+    gh, gw = h // 14, w // 14
+    tpv = 1 + n_register + gh * gw
+    imgs = rng.integers(0, 256, (views, h, w, 3), dtype=np.uint8)
+    proj = rt.prepare_linear_oihw_f32(588, embed, normals(rng, embed, 3, 14, 14, scale=0.02),
+                                      normals(rng, embed, scale=0.02))
+    cls = rt.upload_f32(normals(rng, embed, scale=0.02))
+    regs = rt.upload_f32(normals(rng, n_register, embed, scale=0.02)) if n_register else None
+    pos = rt.upload_f32(normals(rng, 1 + gh * gw, embed, scale=0.02))
+    out = rt.alloc_f32(views * tpv * embed)
+    rt.patch_embed_views_u8(rt.upload_u8(imgs), views, h, w, 14, MEAN, STD, proj, cls, regs,
+                            n_register, pos, out)
+    got = out.numpy().reshape(views, tpv, embed)
+    for v in range(views):
+        one = rt.alloc_f32(tpv * embed)
+        rt.patch_embed_u8(rt.upload_u8(imgs[v]), h, w, 14, MEAN, STD, proj, cls, regs,
+                          n_register, pos, one)
+        assert np.array_equal(got[v], one.numpy().reshape(tpv, embed)), f"view {v}"
+
+
+def test_patch_embed_views_need_aligned_views(rt, rng):
+    # 14 x 14 x 3 = 588 bytes per view: the second view starts 4-byte aligned
+    imgs = rt.upload_u8(rng.integers(0, 256, (2, 14, 14, 3), dtype=np.uint8))
+    proj = rt.prepare_linear_oihw_f32(588, 16, normals(rng, 16, 3, 14, 14), normals(rng, 16))
+    cls, pos = rt.upload_f32(normals(rng, 16)), rt.upload_f32(normals(rng, 2, 16))
+    with pytest.raises(vh.UnsupportedShape):
+        rt.patch_embed_views_u8(imgs, 2, 14, 14, 14, MEAN, STD, proj, cls, None, 0, pos,
+                                rt.alloc_f32(2 * 2 * 16))
+    with pytest.raises(vh.VestraError):  # image count
+        rt.patch_embed_views_u8(imgs, 3, 14, 14, 14, MEAN, STD, proj, cls, None, 0, pos,
+                                rt.alloc_f32(3 * 2 * 16))
+
+
 def test_patch_embed_rejects_unqualified_patch(rt, rng):
     img = rt.upload_u8(rng.integers(0, 256, (32, 32, 3), dtype=np.uint8))
     proj = rt.prepare_linear_oihw_f32(3 * 16 * 16, 8, normals(rng, 8, 3, 16, 16), normals(rng, 8))

@@ -248,14 +248,15 @@ static_assert(kPeRowsA <= kThreads && kPeRowsA % 64 == 0 && kPeRowsB > kPeStager
 static_assert(kPePitch % 4 == 0 && (kPePitch / 4) % 2 == 1 && kPePitch >= kPeKp, "pitch 4 x odd");
 
 struct PatchArgs {
-  const uint8_t* img;  // [H, W, 3], 8-byte aligned
+  const uint8_t* img;  // [views, H, W, 3], 8-byte aligned views
   const float* wpk;    // [N, 592], k = ky*42 + kx*3 + c, zero beyond 588
   const float* bias;   // [N]
   const float* pos;    // [(1 + M), N]
   const float* cls;    // [N]
   const float* regs;   // [n_register, N] or null
-  float* out;          // [(1 + n_register + M), N]
-  uint32_t img_bytes;  // H*W*3, a multiple of 4
+  float* out;          // [views, (1 + n_register + M), N]
+  uint32_t img_bytes;  // H*W*3 of one view, a multiple of 4
+  int tiles;           // output tiles of one view
   int W, gw, M, N, n_register;
   vkd::FastDivU32 fgw;  // division by gw
   float mean[3], sd[3];
@@ -318,7 +319,12 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
   const bool stager = tid >= kThreads;
   const int strip = wave & 3, half = (wave >> 2) & 1;
   const int gmt = (p.M + BM - 1) / BM;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  // views one after another: workgroup -> (view, tile of the view)
+  const int tile_all = xcd_tile(blockIdx.x, gridDim.x);
+  const int view = tile_all / p.tiles;
+  const int tile = tile_all - view * p.tiles;
+  const uint8_t* const img = p.img + static_cast<size_t>(view) * p.img_bytes;
+  float* const out = p.out + static_cast<size_t>(view) * (1 + p.n_register + p.M) * p.N;
   const int mt = tile % gmt;
   const int m0 = mt * BM, n0 = (tile / gmt) * BN;
 
@@ -351,10 +357,10 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
   const int rb0 = kPeRowsA + (tb >= 0 ? tb : 0);
   const int rb1 = kPeRowsA + kPeStagers +
                   (tb >= 0 && tb < kPeRowsB - kPeStagers ? tb : kPeRowsB - kPeStagers - 1);
-  if (tid < kPeRowsA) row_a.load(p.img, row_start(tid), p.img_bytes);
+  if (tid < kPeRowsA) row_a.load(img, row_start(tid), p.img_bytes);
   if (stager) {
-    row_b0.load(p.img, row_start(rb0), p.img_bytes);
-    row_b1.load(p.img, row_start(rb1), p.img_bytes);
+    row_b0.load(img, row_start(rb0), p.img_bytes);
+    row_b1.load(img, row_start(rb1), p.img_bytes);
   }
 
   // 2. B fragments (compute waves).  Block sequence: waves 0-3 run blocks
@@ -487,7 +493,7 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
         if (row < p.M)
-          p.out[static_cast<size_t>(1 + p.n_register + row) * p.N + col] =
+          out[static_cast<size_t>(1 + p.n_register + row) * p.N + col] =
               (acc[t][r] + bias) + addend[t][r];
       }
   }
@@ -497,7 +503,7 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
     for (int r0 = 0; r0 <= p.n_register; r0 += 4) {
       const int r = r0 + (lane >> 4);
       if (r <= p.n_register && col < p.N)
-        p.out[static_cast<size_t>(r) * p.N + col] =
+        out[static_cast<size_t>(r) * p.N + col] =
             r == 0 ? p.cls[col] + p.pos[col] : p.regs[static_cast<size_t>(r - 1) * p.N + col];
     }
   }
@@ -1315,18 +1321,21 @@ int vk_pos_embed_bicubic_f32(vk_runtime* rt, const vk_tensor* pos_embed, size_t 
   return VK_OK;
 }
 
-int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t w,
-                      size_t patch, const float mean[3], const float std_[3],
-                      const vk_linear* proj, const vk_tensor* cls, const vk_tensor* registers,
-                      size_t n_register, const vk_tensor* pos_table, vk_tensor* out) {
+int vk_patch_embed_views_u8(vk_runtime* rt, const vk_tensor* images, size_t views, size_t h,
+                            size_t w, size_t patch, const float mean[3], const float std_[3],
+                            const vk_linear* proj, const vk_tensor* cls,
+                            const vk_tensor* registers, size_t n_register,
+                            const vk_tensor* pos_table, vk_tensor* out) {
   VK_TRY(vk::bind(rt));
-  VK_REQUIRE(img_hwc && mean && std_ && proj && cls && pos_table && out, "null argument");
+  VK_REQUIRE(images && mean && std_ && proj && cls && pos_table && out, "null argument");
+  VK_REQUIRE(views > 0, "patch_embed: no views");
   VK_UNSUPPORTED_IF(patch != static_cast<size_t>(kPatch),
                     "patch_embed_u8: patch=%zu (qualified: 14)", patch);
   VK_REQUIRE(h > 0 && w > 0 && h % patch == 0 && w % patch == 0,
              "h=%zu and w=%zu must be positive multiples of patch=%zu", h, w, patch);
-  VK_REQUIRE(img_hwc->dtype == VK_U8 && img_hwc->len == h * w * 3,
-             "image must be u8 HWC with h*w*3=%zu bytes (got %zu)", h * w * 3, img_hwc->len);
+  VK_REQUIRE(images->dtype == VK_U8 && images->len == views * h * w * 3,
+             "images must be u8 [views, h, w, 3] with %zu bytes (got %zu)", views * h * w * 3,
+             images->len);
   const size_t gh = h / patch, gw = w / patch, np = gh * gw;
   const size_t embed = proj->out_features;
   VK_REQUIRE(proj->in_features == 3 * patch * patch, "projection in_features=%zu, expected %zu",
@@ -1339,16 +1348,18 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t
   VK_REQUIRE(pos_table->dtype == VK_F32 && pos_table->len == (1 + np) * embed,
              "pos_table must be f32 [(1+gh*gw)*embed=%zu] (got %zu)", (1 + np) * embed,
              pos_table->len);
-  VK_REQUIRE(out->dtype == VK_F32 && out->len == (1 + n_register + np) * embed,
-             "out must be f32 [(1+n_register+gh*gw)*embed=%zu] (got %zu)",
-             (1 + n_register + np) * embed, out->len);
+  VK_REQUIRE(out->dtype == VK_F32 && out->len == views * (1 + n_register + np) * embed,
+             "out must be f32 [views*(1+n_register+gh*gw)*embed=%zu] (got %zu)",
+             views * (1 + n_register + np) * embed, out->len);
   VK_UNSUPPORTED_IF(h * w * 3 > 0x7fffffffULL || np > 0x7fffffffULL, "image too large");
   for (int c = 0; c < 3; ++c) VK_REQUIRE(std_[c] != 0.0f, "std[%d] is zero", c);
   VK_REQUIRE(proj->weight_patch != nullptr, "projection has no patch-order filter");
-  VK_UNSUPPORTED_IF(reinterpret_cast<uintptr_t>(img_hwc->ptr) % 8 != 0,
-                    "patch_embed_u8: image must be 8-byte aligned");
+  // every view's rows are read as aligned 8-byte words
+  VK_UNSUPPORTED_IF(reinterpret_cast<uintptr_t>(images->ptr) % 8 != 0 ||
+                        (views > 1 && (h * w * 3) % 8 != 0),
+                    "patch_embed_u8: every image must start 8-byte aligned");
   PatchArgs a{};
-  a.img = static_cast<const uint8_t*>(img_hwc->ptr);
+  a.img = static_cast<const uint8_t*>(images->ptr);
   a.img_bytes = static_cast<uint32_t>(h * w * 3);
   a.wpk = proj->weight_patch;
   a.bias = proj->bias;
@@ -1367,10 +1378,20 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t
     a.sd[c] = std_[c];
   }
   const long long tiles = static_cast<long long>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "patch_embed_u8: %lld tiles", tiles);
-  hipLaunchKernelGGL(patch_embed_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kPeThreads), 0,
-                     rt->stream, a);
+  VK_UNSUPPORTED_IF(tiles * static_cast<long long>(views) > 0x7fffffffLL,
+                    "patch_embed_u8: %lld tiles", tiles * static_cast<long long>(views));
+  a.tiles = static_cast<int>(tiles);
+  hipLaunchKernelGGL(patch_embed_kernel, dim3(static_cast<unsigned>(tiles * views)),
+                     dim3(kPeThreads), 0, rt->stream, a);
   return vk::check_launch("patch_embed_kernel");
+}
+
+int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t w,
+                      size_t patch, const float mean[3], const float std_[3],
+                      const vk_linear* proj, const vk_tensor* cls, const vk_tensor* registers,
+                      size_t n_register, const vk_tensor* pos_table, vk_tensor* out) {
+  return vk_patch_embed_views_u8(rt, img_hwc, 1, h, w, patch, mean, std_, proj, cls, registers,
+                                 n_register, pos_table, out);
 }
 
 }  // extern "C"

@@ -189,6 +189,8 @@ _SIGS = {
     "vk_prepend_cls_add_pos_f32": ([_vp, _vp, _vp, _vp, _sz, _sz, _pp], _i),
     "vk_pos_embed_bicubic_f32": ([_vp, _vp, _sz, _sz, _sz, _sz, _f, _pp], _i),
     "vk_patch_embed_u8": ([_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp], _i),
+    "vk_patch_embed_views_u8": (
+        [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp], _i),
     "vk_vit_block_fused_ops": (
         [_vp, C.POINTER(VitConfig), _sz, C.POINTER(VitLayer), C.POINTER(VitLayer),
          C.POINTER(VitActivations), _sz, _sz, _sz, _vp, C.c_uint], _i),
@@ -246,12 +248,14 @@ class Tensor:
         return int(lib.vk_tensor_device_ptr(self.handle) or 0)
 
     def view(self, offset: int, length: int) -> "Tensor":
-        """Non-owning f32 view of elements [offset, offset + length); keeps
-        this tensor alive while the view lives."""
+        """Non-owning view of elements [offset, offset + length), of this
+        tensor's dtype; keeps this tensor alive while the view lives."""
         if offset < 0 or length < 0 or offset + length > len(self):
             raise VestraError(VK_ERR_INVALID, "view out of range")
+        dt = self.dtype
+        size = {VK_F32: 4, VK_F16: 2, VK_U8: 1, VK_I32: 4, VK_I64: 8}[dt]
         out = C.c_void_p()
-        _check(lib.vk_tensor_wrap(self.rt.handle, 0, self.device_ptr + 4 * offset, length,
+        _check(lib.vk_tensor_wrap(self.rt.handle, dt, self.device_ptr + size * offset, length,
                                   C.byref(out)))
         t = Tensor(self.rt, out)
         t._base = self
@@ -757,6 +761,19 @@ class Runtime:
                                      C.cast(m, C.c_void_p), C.cast(s, C.c_void_p),
                                      proj.handle, cls.handle, _h(registers), n_register,
                                      pos_table.handle, out.handle))
+
+    def patch_embed_views_u8(self, images: Tensor, views: int, h: int, w: int, patch: int,
+                             mean: Sequence[float], std: Sequence[float], proj: Linear,
+                             cls: Tensor, registers: Optional[Tensor], n_register: int,
+                             pos_table: Tensor, out: Tensor) -> None:
+        """patch_embed_u8 of `views` images [views, h, w, 3] in one launch,
+        into the view-major token buffer."""
+        m = (C.c_float * 3)(*mean)
+        s = (C.c_float * 3)(*std)
+        _check(lib.vk_patch_embed_views_u8(self.handle, images.handle, views, h, w, patch,
+                                           C.cast(m, C.c_void_p), C.cast(s, C.c_void_p),
+                                           proj.handle, cls.handle, _h(registers), n_register,
+                                           pos_table.handle, out.handle))
 
     # -- block sequence ------------------------------------------------------
     def vit_block_fused_ops(self, cfg: VitConfig, layer_idx: int, layer: VitLayer,
