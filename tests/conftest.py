@@ -24,7 +24,9 @@ def pytest_configure(config):
 
 def parity_report(got, ref, atol, rtol):
     """da-parity compare semantics (da-parity/src/lib.rs:64-129): pass iff
-    |got - ref| <= atol + rtol*|ref| element-wise; empty or size mismatch fail."""
+    |got - ref| <= atol + rtol*|ref| element-wise; empty or size mismatch fail.
+    One deliberate difference: a NaN on either side fails here, where the
+    reference's `d > tol` test lets it pass."""
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     ref = np.asarray(ref, dtype=np.float64).reshape(-1)
     if got.size != ref.size or got.size == 0:

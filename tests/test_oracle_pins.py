@@ -40,6 +40,13 @@ def test_compare_semantics_match_reference(kats):
             assert abs(max_abs - case["max_abs"]) < 1e-9
 
 
+def test_compare_rejects_nan_and_size_mismatch():
+    # stricter than the reference on NaN (its `d > tol` lets one pass)
+    assert not parity_report([1.0, float("nan")], [1.0, 1.0], 1.0, 1.0)[0]
+    assert not parity_report([1.0, 1.0], [1.0, float("nan")], 1.0, 1.0)[0]
+    assert not parity_report([1.0, 2.0], [1.0], 1.0, 1.0)[0]
+
+
 # ---------------------------------------------------------------- f16
 def test_f16_widening_is_exact_for_every_bit_pattern():
     bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
