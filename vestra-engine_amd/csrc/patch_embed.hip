@@ -41,6 +41,10 @@ using namespace vk::linear_epilogue;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+#ifndef VK_PE_PIPELINED
+#define VK_PE_PIPELINED 1  // multi-view launches: the pipelined kernel
+#endif
+
 constexpr int BM = 48;
 constexpr int BN = 64;
 constexpr int kThreads = 512;
@@ -257,6 +261,7 @@ struct PatchArgs {
   float* out;          // [views, (1 + n_register + M), N]
   uint32_t img_bytes;  // H*W*3 of one view, a multiple of 4
   int tiles;           // output tiles of one view
+  int views;
   int W, gw, M, N, n_register;
   vkd::FastDivU32 fgw;  // division by gw
   float mean[3], sd[3];
@@ -506,6 +511,242 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
         out[static_cast<size_t>(r) * p.N + col] =
             r == 0 ? p.cls[col] + p.pos[col] : p.regs[static_cast<size_t>(r - 1) * p.N + col];
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined patch embedding, for launches of many tiles (the views of a
+// multi-view batch).  A persistent workgroup runs tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ... of 32 patches x 64 outputs.  Two A buffers
+// (32 x 596 floats each; 156 KB of LDS with the table) let the staging
+// waves gather and normalise the next tile while the MFMA waves run the
+// current one, so after the first tile no MFMA waits for staging.  Every
+// output element takes patch_embed_kernel's block sequence, k-half split and
+// epilogue order: the same bits.  Per tile: the stagers fill the other
+// buffer and the MFMA waves finish (barrier 1); waves 4-7 hand their k-half
+// sums over through the finished buffer (barrier 2); waves 0-3 add them
+// (barrier 3: the buffer is free for the stagers again) and store.
+// ---------------------------------------------------------------------------
+constexpr int kPp = 32;                  // patches per tile
+constexpr int kPpRows = kPp * kPatch;    // 448 patch rows
+constexpr int kPpBuf = kPp * kPePitch;   // floats per A buffer
+constexpr int kPpAhead = 4;              // B prefetch distance in blocks (8 spills here)
+static_assert(kPpRows <= kPeThreads && kPpRows > kPeStagers && kPpRows <= 2 * kPeStagers &&
+                  2 * kPp * 4 <= kPeThreads && 4 * 8 * 64 <= kPpBuf,
+              "prologue: a row per thread; stagers: at most two rows each; padding zeroed by "
+              "one pass; k-half sums fit in a buffer");
+
+__global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(PatchArgs p) {
+  __shared__ float lut[3 * 256];
+  __shared__ __align__(16) float As[2 * kPpBuf];
+
+  const int tid = threadIdx.x;
+  __builtin_assume(tid < kPeThreads);
+  const int wave = tid >> 6, lane = tid & 63;
+  const bool stager = tid >= kThreads;
+  const int strip = wave & 3, half = (wave >> 2) & 1;
+  const int gmt = (p.M + kPp - 1) / kPp;
+  const int total = p.tiles * p.views;
+  const int first = static_cast<int>(blockIdx.x), step = static_cast<int>(gridDim.x);
+  const int count = (total - first + step - 1) / step;  // >= 1: the grid is at most `total`
+
+  // Patch row R of a tile (0..447): groups of 32 rows are 16 patches x 2
+  // pixel rows (the staging writes' bank pattern of patch_embed_kernel):
+  // m = 16 ((R / 32) % 2) + R % 16, ky = 2 (R / 64) + (R / 16) % 2.
+  auto row_m = [](int r) { return 16 * ((r >> 5) & 1) + (r & 15); };
+  auto row_ky = [](int r) { return 2 * (r >> 6) + ((r >> 4) & 1); };
+  struct Tile {
+    const uint8_t* img;
+    float* out;
+    int m0, n0, mt;
+  };
+  auto tile_at = [&](int t) {
+    const int view = t / p.tiles;
+    const int tt = t - view * p.tiles;
+    Tile a;
+    a.img = p.img + static_cast<size_t>(view) * p.img_bytes;
+    a.out = p.out + static_cast<size_t>(view) * (1 + p.n_register + p.M) * p.N;
+    a.mt = tt % gmt;
+    a.m0 = a.mt * kPp;
+    a.n0 = (tt / gmt) * BN;
+    return a;
+  };
+  auto row_start = [&](const Tile& a, int r) {
+    const int gm = a.m0 + row_m(r);
+    const int cm = gm < p.M ? gm : p.M - 1;
+    const uint32_t py = vkd::fdiv(static_cast<uint32_t>(cm), p.fgw);
+    const uint32_t px = static_cast<uint32_t>(cm) - py * static_cast<uint32_t>(p.gw);
+    return ((py * kPatch + row_ky(r)) * static_cast<uint32_t>(p.W) + px * kPatch) * 3u;
+  };
+  auto row_dst = [&](int buf, int r) {
+    return reinterpret_cast<float2*>(As + buf * kPpBuf + row_m(r) * kPePitch +
+                                     row_ky(r) * kPeRowBytes);
+  };
+
+  // prologue: the first tile's rows (one per thread of the first seven
+  // waves), the table, the K padding of both buffers, then the first tile
+  Tile cur = tile_at(first);
+  {
+    PatchRow r0;
+    if (tid < kPpRows) r0.load(cur.img, row_start(cur, tid), p.img_bytes);
+    const int c = tid / 256, v = tid % 256;
+    const float u = static_cast<float>(v) / 255.0f;
+    lut[tid] = (u - p.mean[c]) / p.sd[c];
+    if (tid < 2 * kPp * 4)
+      As[(tid >> 7) * kPpBuf + ((tid >> 2) & 31) * kPePitch + kPeK + (tid & 3)] = 0.0f;
+    __syncthreads();  // table visible
+    if (tid < kPpRows) {
+      r0.align();
+      r0.store(row_dst(0, tid), lut, 0, kPeRowBytes / 2);
+    }
+  }
+
+  // the compute waves' B fragments: column strip of the tile, block
+  // sequence of patch_embed_kernel (waves 0-3: blocks 0-9, 21-28, 10; waves
+  // 4-7: 11-20, 29-36), kPpAhead blocks ahead of the MFMAs
+  const int first1 = half ? kPePhase1 + 1 : 0;
+  const int first2 = kPeBlocksA + half * kPePhase2;
+  auto seq_block = [&](int s) {
+    return s < kPePhase1 ? first1 + s
+                         : (s < kPePhase1 + kPePhase2 ? first2 + s - kPePhase1 : kPePhase1);
+  };
+  f32x4 bf[kPeSeq];
+  const float* wrow = nullptr;
+  auto set_col = [&](const Tile& a) {
+    const int col = a.n0 + strip * 16 + (lane & 15);
+    const int ccol = col < p.N ? col : p.N - 1;
+    wrow = p.wpk + static_cast<size_t>(ccol) * kPeKp + 4 * (lane >> 4);
+  };
+  auto load_b = [&](int s) {
+    if (s < kPeSeq) bf[s] = *reinterpret_cast<const f32x4*>(wrow + 16 * seq_block(s));
+  };
+  if (!stager) {
+    set_col(cur);
+#pragma unroll
+    for (int s = 0; s < kPpAhead; ++s) load_b(s);
+  }
+  __syncthreads();  // the first tile is staged
+
+  struct AFrag {
+    f32x4 a[2];
+  };
+  for (int k = 0; k < count; ++k) {
+    const int b = k & 1;
+    const bool more = k + 1 < count;
+    const Tile nxt = tile_at(more ? first + (k + 1) * step : first);
+    f32x4 acc[2];
+    float bias = 0.0f, addend[2][4];
+    if (stager) {
+      // the next tile into the other buffer: rows s and s + 256 (s < 192)
+      if (more) {
+        const int s = tid - kThreads;
+        const bool two = s + kPeStagers < kPpRows;
+        PatchRow r0, r1;
+        r0.load(nxt.img, row_start(nxt, s), p.img_bytes);
+        if (two) r1.load(nxt.img, row_start(nxt, s + kPeStagers), p.img_bytes);
+        r0.align();
+        r0.store(row_dst(b ^ 1, s), lut, 0, kPeRowBytes / 2);
+        if (two) {
+          r1.align();
+          r1.store(row_dst(b ^ 1, s + kPeStagers), lut, 0, kPeRowBytes / 2);
+        }
+      }
+    } else {
+      // epilogue operands first: their latency hides behind the MFMAs
+      const int col = cur.n0 + strip * 16 + (lane & 15);
+      const int ccol = col < p.N ? col : p.N - 1;
+      if (half == 0) {
+        bias = p.bias[ccol];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = cur.m0 + t * 16 + 4 * (lane >> 4) + r;
+            const int crow = row < p.M ? row : p.M - 1;
+            addend[t][r] = p.pos[static_cast<size_t>(1 + crow) * p.N + ccol];
+          }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const float* arow = As + b * kPpBuf + (lane & 15) * kPePitch + 4 * (lane >> 4);
+      auto load_a = [&](int s, AFrag& f) {
+        const float* q = arow + 16 * seq_block(s);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) f.a[t] = *reinterpret_cast<const f32x4*>(q + t * 16 * kPePitch);
+      };
+      auto mma = [&](const AFrag& f, const f32x4& bb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[t][j], bb[j], acc[t], 0, 0, 0);
+      };
+      constexpr int kRun = kPePhase1 + kPePhase2;  // positions of both halves
+      AFrag f0, f1, f2;
+      load_a(0, f0);
+      load_a(1, f1);
+#pragma unroll
+      for (int s = 0; s < kRun; ++s) {
+        if (s + 2 < kRun) load_a(s + 2, f2);
+        load_b(s + kPpAhead);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0, bf[s]);
+        f0 = f1;
+        f1 = f2;
+      }
+      if (half == 0) {  // waves 0-3's last block, 10
+        AFrag f;
+        load_a(kPeSeq - 1, f);
+        mma(f, bf[kPeSeq - 1]);
+      }
+      // the next tile's first B fragments load during the hand-over below
+      if (more) {
+        set_col(nxt);
+#pragma unroll
+        for (int s = 0; s < kPpAhead; ++s) load_b(s);
+      }
+    }
+    __syncthreads();  // 1: next tile staged; every read of buffer b done
+    float* red = As + b * kPpBuf;
+    if (!stager && half == 1) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(strip * 8 + t * 4 + r) * 64 + lane] = acc[t][r];
+    }
+    __syncthreads();  // 2
+    if (!stager && half == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] += red[(strip * 8 + t * 4 + r) * 64 + lane];
+    }
+    __syncthreads();  // 3: buffer b free again
+    if (!stager && half == 0) {
+      // lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile
+      const int col = cur.n0 + strip * 16 + (lane & 15);
+      if (col < p.N) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = cur.m0 + t * 16 + 4 * (lane >> 4) + r;
+            if (row < p.M)
+              cur.out[static_cast<size_t>(1 + p.n_register + row) * p.N + col] =
+                  (acc[t][r] + bias) + addend[t][r];
+          }
+      }
+      if (cur.mt == 0) {
+        for (int r0 = 0; r0 <= p.n_register; r0 += 4) {
+          const int r = r0 + (lane >> 4);
+          if (r <= p.n_register && col < p.N)
+            cur.out[static_cast<size_t>(r) * p.N + col] =
+                r == 0 ? p.cls[col] + p.pos[col]
+                       : p.regs[static_cast<size_t>(r - 1) * p.N + col];
+        }
+      }
+    }
+    cur = nxt;
   }
 }
 
@@ -1380,6 +1621,18 @@ int vk_patch_embed_views_u8(vk_runtime* rt, const vk_tensor* images, size_t view
   const long long tiles = static_cast<long long>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   VK_UNSUPPORTED_IF(tiles * static_cast<long long>(views) > 0x7fffffffLL,
                     "patch_embed_u8: %lld tiles", tiles * static_cast<long long>(views));
+  a.views = static_cast<int>(views);
+#if VK_PE_PIPELINED
+  const long long tiles32 =
+      static_cast<long long>((a.M + kPp - 1) / kPp) * ((a.N + BN - 1) / BN);
+  const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
+  if (views > 1 && tiles32 * static_cast<long long>(views) > cus) {
+    a.tiles = static_cast<int>(tiles32);
+    hipLaunchKernelGGL(patch_embed_pipelined_kernel, dim3(static_cast<unsigned>(cus)),
+                       dim3(kPeThreads), 0, rt->stream, a);
+    return vk::check_launch("patch_embed_pipelined_kernel");
+  }
+#endif
   a.tiles = static_cast<int>(tiles);
   hipLaunchKernelGGL(patch_embed_kernel, dim3(static_cast<unsigned>(tiles * views)),
                      dim3(kPeThreads), 0, rt->stream, a);
