@@ -516,29 +516,35 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
 
 // ---------------------------------------------------------------------------
 // Pipelined patch embedding, for launches of many tiles (the views of a
-// multi-view batch).  A persistent workgroup runs tiles blockIdx.x,
-// blockIdx.x + gridDim.x, ... of 32 patches x 64 outputs.  Two A buffers
-// (32 x 596 floats each; 156 KB of LDS with the table) let the staging
-// waves gather and normalise the next tile while the MFMA waves run the
-// current one, so after the first tile no MFMA waits for staging.  Every
-// output element takes patch_embed_kernel's block sequence, k-half split and
-// epilogue order: the same bits.  Per tile: the stagers fill the other
-// buffer and the MFMA waves finish (barrier 1); waves 4-7 hand their k-half
-// sums over through the finished buffer (barrier 2); waves 0-3 add them
-// (barrier 3: the buffer is free for the stagers again) and store.
+// multi-view batch).  Tiles are 32 patches x 64 outputs, numbered with the
+// output columns fastest, t = (view * gmt + mt) * gnt + nt, and each
+// persistent workgroup runs one contiguous range of them, so consecutive
+// tiles share their A tile (the 32 normalised patches): it is staged once
+// per M tile of the range instead of once per tile.  Two A buffers (32 x
+// 596 floats each): M tile j of the range lives in buffer j % 2.  The
+// prologue stages the first two M tiles with every thread; while M tile j
+// (j >= 1) runs, the staging waves stage M tile j + 1 into the other buffer,
+// a slice of its rows per tile (that buffer's last reader, M tile j - 1,
+// finished before M tile j began).  The two k halves' sums meet in a small
+// LDS buffer; the half that adds and stores alternates from tile to tile,
+// so one barrier per tile suffices (a wave that writes the buffer in one
+// tile read it in the previous one).  Every output element takes
+// patch_embed_kernel's block sequence, k-half split and epilogue order: the
+// same bits.
 // ---------------------------------------------------------------------------
 constexpr int kPp = 32;                  // patches per tile
 constexpr int kPpRows = kPp * kPatch;    // 448 patch rows
 constexpr int kPpBuf = kPp * kPePitch;   // floats per A buffer
 constexpr int kPpAhead = 4;              // B prefetch distance in blocks (8 spills here)
-static_assert(kPpRows <= kPeThreads && kPpRows > kPeStagers && kPpRows <= 2 * kPeStagers &&
-                  2 * kPp * 4 <= kPeThreads && 4 * 8 * 64 <= kPpBuf,
-              "prologue: a row per thread; stagers: at most two rows each; padding zeroed by "
-              "one pass; k-half sums fit in a buffer");
+static_assert(kPpRows <= kPeThreads && 2 * kPpRows <= 2 * kPeThreads &&
+                  kPpRows <= 2 * kPeStagers && 2 * kPp * 4 <= kPeThreads,
+              "prologue: at most two rows per thread; stagers: at most two rows each; the "
+              "padding zeroed by one pass");
 
 __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(PatchArgs p) {
   __shared__ float lut[3 * 256];
   __shared__ __align__(16) float As[2 * kPpBuf];
+  __shared__ __align__(16) float red[4 * 8 * 64];  // one k half's sums (160 KiB in all)
 
   const int tid = threadIdx.x;
   __builtin_assume(tid < kPeThreads);
@@ -546,32 +552,33 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
   const bool stager = tid >= kThreads;
   const int strip = wave & 3, half = (wave >> 2) & 1;
   const int gmt = (p.M + kPp - 1) / kPp;
-  const int total = p.tiles * p.views;
-  const int first = static_cast<int>(blockIdx.x), step = static_cast<int>(gridDim.x);
-  const int count = (total - first + step - 1) / step;  // >= 1: the grid is at most `total`
+  const int gnt = (p.N + BN - 1) / BN;
+  const long long total = static_cast<long long>(p.tiles) * p.views;
+  const int t0 = static_cast<int>(total * blockIdx.x / gridDim.x);
+  const int t1 = static_cast<int>(total * (blockIdx.x + 1) / gridDim.x);  // > t0: grid <= total
+  const int vm0 = t0 / gnt;                   // the range's first M tile (view * gmt + mt)
+  const int nvm = (t1 - 1) / gnt - vm0 + 1;   // M tiles in the range
 
-  // Patch row R of a tile (0..447): groups of 32 rows are 16 patches x 2
+  // Patch row R of an M tile (0..447): groups of 32 rows are 16 patches x 2
   // pixel rows (the staging writes' bank pattern of patch_embed_kernel):
   // m = 16 ((R / 32) % 2) + R % 16, ky = 2 (R / 64) + (R / 16) % 2.
   auto row_m = [](int r) { return 16 * ((r >> 5) & 1) + (r & 15); };
   auto row_ky = [](int r) { return 2 * (r >> 6) + ((r >> 4) & 1); };
-  struct Tile {
+  struct MTile {
     const uint8_t* img;
     float* out;
-    int m0, n0, mt;
+    int m0, mt;
   };
-  auto tile_at = [&](int t) {
-    const int view = t / p.tiles;
-    const int tt = t - view * p.tiles;
-    Tile a;
+  auto mtile = [&](int vm) {
+    const int view = vm / gmt;
+    MTile a;
+    a.mt = vm - view * gmt;
+    a.m0 = a.mt * kPp;
     a.img = p.img + static_cast<size_t>(view) * p.img_bytes;
     a.out = p.out + static_cast<size_t>(view) * (1 + p.n_register + p.M) * p.N;
-    a.mt = tt % gmt;
-    a.m0 = a.mt * kPp;
-    a.n0 = (tt / gmt) * BN;
     return a;
   };
-  auto row_start = [&](const Tile& a, int r) {
+  auto row_start = [&](const MTile& a, int r) {
     const int gm = a.m0 + row_m(r);
     const int cm = gm < p.M ? gm : p.M - 1;
     const uint32_t py = vkd::fdiv(static_cast<uint32_t>(cm), p.fgw);
@@ -583,21 +590,31 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
                                      row_ky(r) * kPeRowBytes);
   };
 
-  // prologue: the first tile's rows (one per thread of the first seven
-  // waves), the table, the K padding of both buffers, then the first tile
-  Tile cur = tile_at(first);
+  // prologue: rows R = tid and tid + 768 of the first two M tiles' 896
+  // (R / 448 = the M tile), the table, the K padding of both buffers
   {
-    PatchRow r0;
-    if (tid < kPpRows) r0.load(cur.img, row_start(cur, tid), p.img_bytes);
+    const MTile a0 = mtile(vm0), a1 = mtile(nvm > 1 ? vm0 + 1 : vm0);
+    const int R0 = tid, R1 = tid + kPeThreads;
+    const bool s0 = R0 < kPpRows || nvm > 1;
+    const bool s1 = R1 < 2 * kPpRows && nvm > 1;
+    const bool lo0 = R0 < kPpRows;
+    PatchRow r0, r1;
+    if (s0) r0.load(lo0 ? a0.img : a1.img, row_start(lo0 ? a0 : a1, lo0 ? R0 : R0 - kPpRows),
+                    p.img_bytes);
+    if (s1) r1.load(a1.img, row_start(a1, R1 - kPpRows), p.img_bytes);
     const int c = tid / 256, v = tid % 256;
     const float u = static_cast<float>(v) / 255.0f;
     lut[tid] = (u - p.mean[c]) / p.sd[c];
     if (tid < 2 * kPp * 4)
       As[(tid >> 7) * kPpBuf + ((tid >> 2) & 31) * kPePitch + kPeK + (tid & 3)] = 0.0f;
     __syncthreads();  // table visible
-    if (tid < kPpRows) {
+    if (s0) {
       r0.align();
-      r0.store(row_dst(0, tid), lut, 0, kPeRowBytes / 2);
+      r0.store(row_dst(lo0 ? 0 : 1, lo0 ? R0 : R0 - kPpRows), lut, 0, kPeRowBytes / 2);
+    }
+    if (s1) {
+      r1.align();
+      r1.store(row_dst(1, R1 - kPpRows), lut, 0, kPeRowBytes / 2);
     }
   }
 
@@ -612,8 +629,8 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
   };
   f32x4 bf[kPeSeq];
   const float* wrow = nullptr;
-  auto set_col = [&](const Tile& a) {
-    const int col = a.n0 + strip * 16 + (lane & 15);
+  auto set_col = [&](int n0) {
+    const int col = n0 + strip * 16 + (lane & 15);
     const int ccol = col < p.N ? col : p.N - 1;
     wrow = p.wpk + static_cast<size_t>(ccol) * kPeKp + 4 * (lane >> 4);
   };
@@ -621,65 +638,75 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
     if (s < kPeSeq) bf[s] = *reinterpret_cast<const f32x4*>(wrow + 16 * seq_block(s));
   };
   if (!stager) {
-    set_col(cur);
+    set_col((t0 % gnt) * BN);
 #pragma unroll
     for (int s = 0; s < kPpAhead; ++s) load_b(s);
   }
-  __syncthreads();  // the first tile is staged
+  __syncthreads();  // the first two M tiles are staged
 
   struct AFrag {
     f32x4 a[2];
   };
-  for (int k = 0; k < count; ++k) {
-    const int b = k & 1;
-    const bool more = k + 1 < count;
-    const Tile nxt = tile_at(more ? first + (k + 1) * step : first);
+  for (int t = t0; t < t1; ++t) {
+    const int vm = t / gnt;
+    const int n0 = (t - vm * gnt) * BN;
+    const int j = vm - vm0;
+    const int b = j & 1;
+    const MTile cur = mtile(vm);
+    // the half that adds the two sums and stores alternates per tile
+    const bool fin = half == ((t - t0) & 1);
     f32x4 acc[2];
     float bias = 0.0f, addend[2][4];
     if (stager) {
-      // the next tile into the other buffer: rows s and s + 256 (s < 192)
-      if (more) {
-        const int s = tid - kThreads;
-        const bool two = s + kPeStagers < kPpRows;
-        PatchRow r0, r1;
-        r0.load(nxt.img, row_start(nxt, s), p.img_bytes);
-        if (two) r1.load(nxt.img, row_start(nxt, s + kPeStagers), p.img_bytes);
-        r0.align();
-        r0.store(row_dst(b ^ 1, s), lut, 0, kPeRowBytes / 2);
-        if (two) {
-          r1.align();
-          r1.store(row_dst(b ^ 1, s + kPeStagers), lut, 0, kPeRowBytes / 2);
+      // during M tile j >= 1 (whole: it started inside the range and is not
+      // its last), M tile j + 1 into the other buffer, rows [lo, hi) now
+      if (j >= 1 && j + 1 < nvm) {
+        const int i = t - vm * gnt;
+        const int lo = i * kPpRows / gnt, hi = (i + 1) * kPpRows / gnt;
+        const int ra = lo + (tid - kThreads), rb = ra + kPeStagers;
+        const MTile nm = mtile(vm + 1);
+        PatchRow x0, x1;
+        if (ra < hi) x0.load(nm.img, row_start(nm, ra), p.img_bytes);
+        if (rb < hi) x1.load(nm.img, row_start(nm, rb), p.img_bytes);
+        if (ra < hi) {
+          x0.align();
+          x0.store(row_dst(b ^ 1, ra), lut, 0, kPeRowBytes / 2);
+        }
+        if (rb < hi) {
+          x1.align();
+          x1.store(row_dst(b ^ 1, rb), lut, 0, kPeRowBytes / 2);
         }
       }
     } else {
       // epilogue operands first: their latency hides behind the MFMAs
-      const int col = cur.n0 + strip * 16 + (lane & 15);
+      const int col = n0 + strip * 16 + (lane & 15);
       const int ccol = col < p.N ? col : p.N - 1;
-      if (half == 0) {
+      if (fin) {
         bias = p.bias[ccol];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int row = cur.m0 + t * 16 + 4 * (lane >> 4) + r;
+            const int row = cur.m0 + tt * 16 + 4 * (lane >> 4) + r;
             const int crow = row < p.M ? row : p.M - 1;
-            addend[t][r] = p.pos[static_cast<size_t>(1 + crow) * p.N + ccol];
+            addend[tt][r] = p.pos[static_cast<size_t>(1 + crow) * p.N + ccol];
           }
       }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int tt = 0; tt < 2; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       const float* arow = As + b * kPpBuf + (lane & 15) * kPePitch + 4 * (lane >> 4);
       auto load_a = [&](int s, AFrag& f) {
         const float* q = arow + 16 * seq_block(s);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) f.a[t] = *reinterpret_cast<const f32x4*>(q + t * 16 * kPePitch);
+        for (int tt = 0; tt < 2; ++tt)
+          f.a[tt] = *reinterpret_cast<const f32x4*>(q + tt * 16 * kPePitch);
       };
       auto mma = [&](const AFrag& f, const f32x4& bb) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[t][j], bb[j], acc[t], 0, 0, 0);
+          for (int tt = 0; tt < 2; ++tt)
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[tt][jj], bb[jj], acc[tt], 0, 0, 0);
       };
       constexpr int kRun = kPePhase1 + kPePhase2;  // positions of both halves
       AFrag f0, f1, f2;
@@ -700,40 +727,37 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
         mma(f, bf[kPeSeq - 1]);
       }
       // the next tile's first B fragments load during the hand-over below
-      if (more) {
-        set_col(nxt);
+      if (t + 1 < t1) {
+        set_col(((t + 1) % gnt) * BN);
 #pragma unroll
         for (int s = 0; s < kPpAhead; ++s) load_b(s);
       }
+      if (!fin) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[(strip * 8 + tt * 4 + r) * 64 + lane] = acc[tt][r];
+      }
     }
-    __syncthreads();  // 1: next tile staged; every read of buffer b done
-    float* red = As + b * kPpBuf;
-    if (!stager && half == 1) {
+    // the other half's sums in `red`; this tile's rows of the next M tile
+    // staged; every read of the buffer a later tile's staging overwrites done
+    __syncthreads();
+    if (!stager && fin) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[(strip * 8 + t * 4 + r) * 64 + lane] = acc[t][r];
-    }
-    __syncthreads();  // 2
-    if (!stager && half == 0) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] += red[(strip * 8 + t * 4 + r) * 64 + lane];
-    }
-    __syncthreads();  // 3: buffer b free again
-    if (!stager && half == 0) {
+        for (int r = 0; r < 4; ++r) acc[tt][r] += red[(strip * 8 + tt * 4 + r) * 64 + lane];
       // lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile
-      const int col = cur.n0 + strip * 16 + (lane & 15);
+      const int col = n0 + strip * 16 + (lane & 15);
       if (col < p.N) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int row = cur.m0 + t * 16 + 4 * (lane >> 4) + r;
+            const int row = cur.m0 + tt * 16 + 4 * (lane >> 4) + r;
             if (row < p.M)
               cur.out[static_cast<size_t>(1 + p.n_register + row) * p.N + col] =
-                  (acc[t][r] + bias) + addend[t][r];
+                  (acc[tt][r] + bias) + addend[tt][r];
           }
       }
       if (cur.mt == 0) {
@@ -746,7 +770,6 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
         }
       }
     }
-    cur = nxt;
   }
 }
 
