@@ -451,6 +451,32 @@ def full_block_timing(rt, rng, reps=3):
         out[name] = {"rows": rows, "us_per_block": round(ms * 1e3 / DEPTH, 2),
                      "ms_12_blocks": round(ms, 3), "TFLOP_s": round(flop / ms / 1e9, 2),
                      "frac_of_f32_mfma_peak": round(flop / ms / 1e9 / MFMA_F32_PEAK_TFLOPS, 4)}
+        if views == 1:
+            # what the per-token operations cost inside the block at one
+            # image, where they ride in the projections' epilogues and sum
+            # passes: the same projections (Q/K/V still stored head-major,
+            # the projection still reading them so) and attention with plain
+            # stores and no per-token operation, as a timing reference only
+            tmp = rt.alloc_f32(rows * D)
+            t = ws.tensors
+
+            def plain():
+                for i, (_, lin) in enumerate(keep):
+                    glob = i >= ALT and i % 2 == 1
+                    lin["qkv"].run_qkv_hnd(tokens, rows, H, t["q"], t["k"], t["v"])
+                    rt.attention_into_f32(t["q"], t["k"], t["v"], H if glob else H * views,
+                                          rows if glob else TPV, HD, t["attn"])
+                    lin["proj"].run_hnd_into(t["attn"], rows, H, t["ln"])
+                    lin["fc1"].run_into(t["ln"], rows, t["hidden"])
+                    lin["fc2"].run_into(t["hidden"], rows, tmp)
+
+            plain()
+            g2 = capture(rt, plain)
+            g2.launch()
+            ms2 = statistics.median(time_loop(rt, g2.launch, 1) for _ in range(reps))
+            out[name]["projections_attention_plain_us_per_block"] = round(ms2 * 1e3 / DEPTH, 2)
+            out[name]["fused_ops_in_block_us"] = round((ms - ms2) * 1e3 / DEPTH, 2)
+            del g2
         del graph, ws, tokens
     return out
 
