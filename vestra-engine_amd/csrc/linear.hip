@@ -347,26 +347,54 @@ __global__ __launch_bounds__(threads_for(TM) * KG,
     mma_chunk();
   }
 
-  // k groups: group 1's sums through LDS (As, free after the last chunk) to
-  // group 0, one f32x4 per lane and MFMA tile, lane-contiguous
+  // k groups: the two groups' sums meet through LDS (As, free after the
+  // last chunk), one f32x4 per lane and MFMA tile, lane-contiguous.  For the
+  // plain epilogue each group finishes one of the strip's two 16-row halves
+  // (half kh: it hands the other half's sums over and takes this half's),
+  // so all eight waves run the epilogue; the Q/K epilogue and split-K take
+  // the whole sums in group 0.  Either way a sum is group 0's + group 1's.
+  const bool half_epi = KG == 2 && QKN == 0 && g.splits == 1;
   if constexpr (KG == 2) {
     static_assert(kGroupWaves * 2 * NU * 256 <= TM * PITCH, "k-group sums fit in As");
     float* red = As + wl * (2 * NU * 256) + 4 * lane;
     __syncthreads();  // every wave is done reading the last chunk's operands
-    if (!lead) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-          *reinterpret_cast<f32x4*>(red + (t * NU + u) * 256) = acc[t][u];
-    }
-    __syncthreads();
-    if (lead) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
+    if (half_epi) {
+      // constant indices in both branches (kh is uniform over the wave): a
+      // register array indexed by a run-time value would live in scratch
+      if (lead) {
 #pragma unroll
         for (int u = 0; u < NU; ++u)
-          acc[t][u] = acc[t][u] + *reinterpret_cast<const f32x4*>(red + (t * NU + u) * 256);
+          *reinterpret_cast<f32x4*>(red + (NU + u) * 256) = acc[1][u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) *reinterpret_cast<f32x4*>(red + u * 256) = acc[0][u];
+      }
+      __syncthreads();
+      if (lead) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          acc[0][u] = acc[0][u] + *reinterpret_cast<const f32x4*>(red + u * 256);
+      } else {
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          acc[1][u] = *reinterpret_cast<const f32x4*>(red + (NU + u) * 256) + acc[1][u];
+      }
+    } else {
+      if (!lead) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+            *reinterpret_cast<f32x4*>(red + (t * NU + u) * 256) = acc[t][u];
+      }
+      __syncthreads();
+      if (lead) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+            acc[t][u] = acc[t][u] + *reinterpret_cast<const f32x4*>(red + (t * NU + u) * 256);
+      }
     }
   }
 
@@ -438,7 +466,7 @@ __global__ __launch_bounds__(threads_for(TM) * KG,
       return;
     }
   }
-  if (!lead) return;
+  if (!lead && !half_epi) return;
   // Per 16-column strip u: bias, LayerScale and the address of the column
   // at row 0 (row r adds r x the row stride), computed once; a tile inside
   // the matrix stores without bounds checks.
@@ -461,6 +489,7 @@ __global__ __launch_bounds__(threads_for(TM) * KG,
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        if (half_epi && t != kh) continue;
         const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
         const size_t cr = static_cast<size_t>(row < g.M ? row : g.M - 1);
 #pragma unroll
@@ -471,6 +500,7 @@ __global__ __launch_bounds__(threads_for(TM) * KG,
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      if (half_epi && t != kh) continue;
       const int row = m0 + wm * 32 + t * 16 + 4 * (lane >> 4) + r;
       const bool rok = row < g.M;
 #pragma unroll
