@@ -31,19 +31,27 @@ struct QkShape {
 };
 
 // cos/sin of the frequencies j0..j0+NF-1 for a coordinate outside the
-// table: angle rounded in f32, trig in double, as the host table does.  Only
-// the explicit-position forms can meet such a coordinate (grid forms size
-// the table on the host); kept out of line so its double-precision trig does
-// not inflate the register footprint of the streaming path.
+// table (positions past 1023, or negative): the same f32 angle as the table,
+// its cosine and sine from the device's single-precision sincosf (within 2
+// ulp of the table's double-rounded values).  Only the explicit-position
+// forms can meet such a coordinate (grid forms size the table on the host).
+// Double-precision trig here, out of line or inline, took the streaming
+// kernel's register footprint from ~45 to ~100 VGPRs and every launch with
+// explicit positions 12% longer, whether or not a coordinate left the table.
+struct RopeCs {
+  float4 c, s;  // components 0..NF-1
+};
 template <int NF>
-__device__ __noinline__ void rope_cs_slow(const float* __restrict__ table, int table_max, int p,
-                                          int j0, float* cv, float* sv) {
+__device__ __forceinline__ RopeCs rope_cs_slow(const float* __restrict__ table, int table_max,
+                                               int p, int j0) {
+  float cv[4] = {0.f, 0.f, 0.f, 0.f}, sv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
   for (int u = 0; u < NF; ++u) {
     const float inv_freq = table[static_cast<size_t>(table_max + 1) * 32 + j0 + u];
     const float angle = static_cast<float>(p) * inv_freq;
-    cv[u] = static_cast<float>(cos(static_cast<double>(angle)));
-    sv[u] = static_cast<float>(sin(static_cast<double>(angle)));
+    sincosf(angle, &sv[u], &cv[u]);
   }
+  return RopeCs{make_float4(cv[0], cv[1], cv[2], cv[3]), make_float4(sv[0], sv[1], sv[2], sv[3])};
 }
 
 __device__ __forceinline__ float4 swizzle_xor4(float4 v) {
@@ -143,10 +151,9 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
       o.c = *reinterpret_cast<const float4*>(e + j0);
       o.s = *reinterpret_cast<const float4*>(e + 16 + j0);
     } else {
-      float cv[4], sv[4];
-      rope_cs_slow<4>(table, table_max, coord, j0, cv, sv);
-      o.c = make_float4(cv[0], cv[1], cv[2], cv[3]);
-      o.s = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      const RopeCs cs = rope_cs_slow<4>(table, table_max, coord, j0);
+      o.c = cs.c;
+      o.s = cs.s;
     }
   } else {
     const int j0 = (l & 7) * 2;  // frequencies j0, j0+1
@@ -155,10 +162,9 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
       c = *reinterpret_cast<const float2*>(e + j0);
       sn = *reinterpret_cast<const float2*>(e + 16 + j0);
     } else {
-      float cv[2], sv[2];
-      rope_cs_slow<2>(table, table_max, coord, j0, cv, sv);
-      c = make_float2(cv[0], cv[1]);
-      sn = make_float2(sv[0], sv[1]);
+      const RopeCs cs = rope_cs_slow<2>(table, table_max, coord, j0);
+      c = make_float2(cs.c.x, cs.c.y);
+      sn = make_float2(cs.s.x, cs.s.y);
     }
     o.c = make_float4(c.x, c.y, 0.0f, 0.0f);
     o.s = make_float4(sn.x, sn.y, 0.0f, 0.0f);
