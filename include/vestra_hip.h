@@ -221,8 +221,9 @@ int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
  * device encoding, truncated toward zero), i32 or i64 (the CPU kernel's
  * `&[i64]`, qk_norm_rope_f32_da3_base at vit_block.rs:911-924; values must
  * fit in 32 bits).  Positions outside the runtime's cos/sin table (negative
- * or above 1023 and every grid coordinate seen so far) take the same
- * f32 angle and double-precision trig on the device. */
+ * or above 1023 and every grid coordinate seen so far) take the same f32
+ * angle and the device's single-precision sincosf (within 2 ulp of the
+ * table's double-rounded values). */
 int vk_qk_norm_rope_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
                              const vk_tensor* q_gamma, const vk_tensor* q_beta,
                              const vk_tensor* k_gamma, const vk_tensor* k_beta,
