@@ -1004,7 +1004,7 @@ def main():
     tau0 = dispatch_overhead(rt)
     log("patch embedding")
     patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
-             patch_embed_timing(rt, rng, 336, 504, D, max(8, args.op_iters // 4), views=12),
+             patch_embed_timing(rt, rng, 336, 504, D, args.op_iters, views=12),
              patch_embed_timing(rt, rng, 672, 1008, 1024, args.op_iters)]
     gelu = ops12["gelu"]
     log("fused linear epilogues")
