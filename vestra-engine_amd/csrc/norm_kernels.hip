@@ -137,9 +137,11 @@ __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
 // ---------------------------------------------------------------------------
 using namespace vkq;
 
-// Each 16-lane group owns kQkRowsPerGroup consecutive rows of the flattened
-// [Q rows | K rows] index space; both rows' loads are issued before either
-// row's reductions, doubling the bytes in flight per wave.
+// With Q and K, each 16-lane group owns the Q row and the K row of one
+// (head, token): one position and one cos/sin lookup serve both, and both
+// rows' loads are issued before either row's reductions, doubling the bytes
+// in flight per wave.  A single tensor (the rotation alone) gives each group
+// kQkRowsPerGroup consecutive rows.
 #ifndef VK_QK_ROWS_PER_GROUP
 #define VK_QK_ROWS_PER_GROUP 2
 #endif
@@ -159,6 +161,32 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
   // arithmetic: one memory round trip per wave
   float4 v[kQkRowsPerGroup];
   QkRowOperands op[kQkRowsPerGroup];
+  if (kQkRowsPerGroup == 2 && sh.tensors == 2) {
+    // the Q row and the K row of one (head, token): one position, one
+    // cos/sin lookup for both
+    const uint32_t r = grp < sh.rows_per_tensor ? grp : sh.rows_per_tensor - 1;
+    int py, px;
+    qk_row_position<POS>(r, sh, pos_yx, &py, &px);
+    v[0] = vkd::ld_stream(reinterpret_cast<const float4*>(q + static_cast<size_t>(r) * 64) + l);
+    v[kQkRowsPerGroup - 1] =
+        vkd::ld_stream(reinterpret_cast<const float4*>(k + static_cast<size_t>(r) * 64) + l);
+    op[0] = qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, qg, qb, py, px, table, sh.table_max);
+    op[kQkRowsPerGroup - 1] = op[0];
+    if (HAS_NORM) {
+      op[kQkRowsPerGroup - 1].g = vkd::Param<PT>::load4(kg, l);
+      op[kQkRowsPerGroup - 1].b = vkd::Param<PT>::load4(kb, l);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kQkRowsPerGroup; ++j)
+      v[j] = qk_row_apply<HAS_NORM, PAIR>(v[j], l, op[j], eps);
+    if (grp < sh.rows_per_tensor) {
+      vkd::st_stream(reinterpret_cast<float4*>(q + static_cast<size_t>(r) * 64) + l, v[0]);
+      vkd::st_stream(reinterpret_cast<float4*>(k + static_cast<size_t>(r) * 64) + l,
+                     v[kQkRowsPerGroup - 1]);
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < kQkRowsPerGroup; ++j) {
     const uint32_t gr = grp * kQkRowsPerGroup + j;
