@@ -137,10 +137,11 @@ __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
 // ---------------------------------------------------------------------------
 using namespace vkq;
 
-// With Q and K, each 16-lane group owns the Q row and the K row of one
-// (head, token): one position and one cos/sin lookup serve both, and both
-// rows' loads are issued before either row's reductions, doubling the bytes
-// in flight per wave.  A single tensor (the rotation alone) gives each group
+// With Q and K, each 16-lane group owns kQkRowsPerGroup / 2 (head, token)
+// pairs of a Q row and a K row: one position and one cos/sin lookup serve
+// both rows of a pair, and every row's loads are issued before any row's
+// reductions, doubling the bytes in flight per wave.  A single tensor (the
+// rotation alone), or an odd kQkRowsPerGroup, gives each group
 // kQkRowsPerGroup consecutive rows.
 #ifndef VK_QK_ROWS_PER_GROUP
 #define VK_QK_ROWS_PER_GROUP 2
@@ -161,29 +162,38 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
   // arithmetic: one memory round trip per wave
   float4 v[kQkRowsPerGroup];
   QkRowOperands op[kQkRowsPerGroup];
-  if (kQkRowsPerGroup == 2 && sh.tensors == 2) {
-    // the Q row and the K row of one (head, token): one position, one
-    // cos/sin lookup for both
-    const uint32_t r = grp < sh.rows_per_tensor ? grp : sh.rows_per_tensor - 1;
-    int py, px;
-    qk_row_position<POS>(r, sh, pos_yx, &py, &px);
-    v[0] = vkd::ld_stream(reinterpret_cast<const float4*>(q + static_cast<size_t>(r) * 64) + l);
-    v[kQkRowsPerGroup - 1] =
-        vkd::ld_stream(reinterpret_cast<const float4*>(k + static_cast<size_t>(r) * 64) + l);
-    op[0] = qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, qg, qb, py, px, table, sh.table_max);
-    op[kQkRowsPerGroup - 1] = op[0];
-    if (HAS_NORM) {
-      op[kQkRowsPerGroup - 1].g = vkd::Param<PT>::load4(kg, l);
-      op[kQkRowsPerGroup - 1].b = vkd::Param<PT>::load4(kb, l);
+  if (kQkRowsPerGroup % 2 == 0 && sh.tensors == 2) {
+    // Q row and K row pairs of one (head, token) each: one position and one
+    // cos/sin lookup per pair
+    constexpr int NP = kQkRowsPerGroup / 2;
+    uint32_t rr[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint32_t r = grp * NP + p;
+      rr[p] = r < sh.rows_per_tensor ? r : sh.rows_per_tensor - 1;
+      int py, px;
+      qk_row_position<POS>(rr[p], sh, pos_yx, &py, &px);
+      v[2 * p] = vkd::ld_stream(reinterpret_cast<const float4*>(q + static_cast<size_t>(rr[p]) * 64) + l);
+      v[2 * p + 1] =
+          vkd::ld_stream(reinterpret_cast<const float4*>(k + static_cast<size_t>(rr[p]) * 64) + l);
+      op[2 * p] = qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, qg, qb, py, px, table, sh.table_max);
+      op[2 * p + 1] = op[2 * p];
+      if (HAS_NORM) {
+        op[2 * p + 1].g = vkd::Param<PT>::load4(kg, l);
+        op[2 * p + 1].b = vkd::Param<PT>::load4(kb, l);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kQkRowsPerGroup; ++j)
       v[j] = qk_row_apply<HAS_NORM, PAIR>(v[j], l, op[j], eps);
-    if (grp < sh.rows_per_tensor) {
-      vkd::st_stream(reinterpret_cast<float4*>(q + static_cast<size_t>(r) * 64) + l, v[0]);
-      vkd::st_stream(reinterpret_cast<float4*>(k + static_cast<size_t>(r) * 64) + l,
-                     v[kQkRowsPerGroup - 1]);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if (grp * NP + p < sh.rows_per_tensor) {
+        vkd::st_stream(reinterpret_cast<float4*>(q + static_cast<size_t>(rr[p]) * 64) + l, v[2 * p]);
+        vkd::st_stream(reinterpret_cast<float4*>(k + static_cast<size_t>(rr[p]) * 64) + l,
+                       v[2 * p + 1]);
+      }
     }
     return;
   }
