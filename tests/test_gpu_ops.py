@@ -172,6 +172,28 @@ def test_qk_norm_rope_reference_form(rt, rng, n_special, gh, gw, glob):
     assert_parity(tk.numpy(), rk, F32_ATOL, F32_RTOL, "k")
 
 
+@pytest.mark.parametrize("heads,n_special,gh,gw", [(3, 1, 2, 3), (1, 2, 1, 3), (5, 2, 1, 1)])
+def test_qk_norm_rope_odd_row_counts(rt, rng, heads, n_special, gh, gw):
+    # an odd heads * tokens leaves the last (Q row, K row) pair group and
+    # the grid's tail groups past the end: only real rows may be written
+    n = n_special + gh * gw
+    assert heads * n % 2 == 1
+    q, k = normals(rng, heads, n, 64), normals(rng, heads, n, 64)
+    qg, qb, kg, kb = qk_params(rng)
+    pos = oracle.rope_positions(n_special, gh, gw, 1, False)
+    pad = normals(rng, 64)
+    tq = rt.upload_f32(np.concatenate([q.reshape(-1), pad]))
+    tk = rt.upload_f32(np.concatenate([k.reshape(-1), pad]))
+    rt.qk_norm_rope_f32_da3_base(tq.view(0, heads * n * 64), tk.view(0, heads * n * 64),
+                                 rt.upload_f32(qg), rt.upload_f32(qb), rt.upload_f32(kg),
+                                 rt.upload_f32(kb), rt.upload_f32(pos), heads, n, 100.0, 1e-5)
+    rq, rk = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n)
+    got_q, got_k = tq.numpy(), tk.numpy()
+    assert_parity(got_q[:heads * n * 64], rq, F32_ATOL, F32_RTOL, "q")
+    assert_parity(got_k[:heads * n * 64], rk, F32_ATOL, F32_RTOL, "k")
+    assert np.array_equal(got_q[heads * n * 64:], pad) and np.array_equal(got_k[heads * n * 64:], pad)
+
+
 def test_rope_alone_is_bit_exact(rt, rng):
     # without the LayerNorm the rotation itself has no reduction: the GPU
     # must equal the oracle bit for bit (shared cos/sin rounding, no FMA)
