@@ -131,6 +131,28 @@ def step_bytes(rows, views, plan, shape=VITB, w=4):
     return total
 
 
+def step_launches(plan, shape=VITB):
+    """Launches of each per-operation-table entry in one pass of the fused-op
+    sequence (the fused LayerScale + residual + LayerNorm counts its
+    camera-slot form too), following the same flags as step_bytes."""
+    import vestra_hip as vh
+    n = {"layernorm": 0, "qk_norm_rope": 0, "layerscale_residual_layernorm": 0, "gelu": 0,
+         "layerscale_residual": 0, "camera_copy": 0}
+    for i, flags in enumerate(plan):
+        camera_here = i == shape.alt and not (flags & vh.VK_BLOCK_CAMERA_WRITTEN)
+        n["camera_copy"] += int(camera_here)
+        if not (flags & vh.VK_BLOCK_SKIP_LN1) or camera_here:
+            n["layernorm"] += 1
+        n["qk_norm_rope"] += 1
+        n["layerscale_residual_layernorm"] += 1
+        n["gelu"] += 1
+        if flags & vh.VK_BLOCK_FUSE_NEXT_LN1:
+            n["layerscale_residual_layernorm"] += 1
+        else:
+            n["layerscale_residual"] += 1
+    return n
+
+
 # ---------------------------------------------------------------- GPU setup
 class Model:
     """The fused-op sequence of every block of `shape` over `views` views
@@ -339,6 +361,11 @@ def cpu_model():
     info["logical_cpus"] = logical
     info["physical_cores"] = len(cores) or None
     info["granted_cpus"] = GRANTED_CPUS
+    # AMD family numbers of the Zen generations (the model name of a
+    # virtualised host may carry no generation)
+    zen = {"23": "Zen / Zen 2", "25": "Zen 3 / Zen 4", "26": "Zen 5"}
+    if info.get("vendor_id") == "AuthenticAMD" and info.get("cpu family") in zen:
+        info["core_generation"] = zen[info["cpu family"]]
     return info
 
 
@@ -803,16 +830,14 @@ def cpu_baseline(model, seconds, threads):
         out = line(med, runs, threads, "AVX-512 + OpenMP restatement (oracle/cpu_simd.c, "
                                        "x86-64-v4, -O3 -ffp-contract=off)")
         out["kind"] = "port"
-        if physical > threads:
-            out["all_physical_cores"] = {
-                "cores": physical,
-                "not_taken": f"the host has {physical} physical cores; a one-GPU run's share "
-                             f"of them is {threads} threads"}
-        elif physical < threads:
+        if physical != threads:
             simd.set_threads(physical)
             med_all, runs_all = timed(simd_block, seconds / 2)
-            out["all_physical_cores"] = line(med_all, runs_all, physical,
-                                             "same, one thread per physical core")
+            what = "same, one thread per physical core"
+            if GRANTED_CPUS and physical > GRANTED_CPUS:
+                what += (f" (this process may run on {GRANTED_CPUS} CPUs: the threads share "
+                         f"them)")
+            out["all_physical_cores"] = line(med_all, runs_all, physical, what)
             simd.set_threads(threads)
         else:
             out["all_physical_cores"] = {"cores": physical, "same_as_value": True}
@@ -846,14 +871,44 @@ def measured_traffic(op, algorithmic_bytes):
     return entry["traffic_bytes"]
 
 
-def roofline_entry(gelu):
-    """The benchmark line's roofline object: the 12-view GELU launch, the
-    step's dominant per-token kernel, against the HBM peak."""
-    return {"kernel": "gelu_kernel (12-view, 10392x3072, in place, HBM-streaming)",
-            "bound": "hbm", "achieved": gelu["GB_s"], "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(gelu["GB_s"] / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": gelu["bytes"], "avg_launch_us": gelu["us"],
-            "traffic": measured_traffic("gelu", gelu["bytes"])}
+# the kernel behind each per-operation-table entry at the 12-view shape
+# (D 768: three float4 per lane; f32 parameters; grid positions, views outer)
+OP_KERNELS = {
+    "layerscale_residual_layernorm": "ls_residual_layernorm_rows<3, float, true, true, false>",
+    "gelu": "gelu_kernel<0>",
+    "qk_norm_rope": "qk_norm_rope_rows<float, true, 1, 0>",
+    "layernorm": "layernorm_rows<3, float, true>",
+    "layerscale_residual": "layerscale_residual_kernel<float>",
+}
+
+
+def _roofline_of(op, entry):
+    return {"kernel": f"{OP_KERNELS[op]} (12-view, {TPV * 12} rows, HBM-streaming)",
+            "bound": "hbm", "achieved": entry["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(entry["GB_s"] / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": entry["bytes"], "avg_launch_us": entry["us"],
+            "traffic": measured_traffic(op, entry["bytes"])}
+
+
+def roofline_entry(ops, plan):
+    """The benchmark line's roofline object: the step's dominant kernel --
+    the per-operation-table entry with the largest launches-per-step x
+    per-launch time -- against the HBM peak, with the share of the step's
+    kernel time each operation takes and, under "next", the runner-up."""
+    launches = step_launches(plan)
+    per_step = {op: launches[op] * ops[op]["us"] for op in OP_KERNELS if op in ops}
+    ranked = sorted(per_step, key=per_step.get, reverse=True)
+    total = sum(per_step.values())
+    out = _roofline_of(ranked[0], ops[ranked[0]])
+    out["launches_per_step"] = launches[ranked[0]]
+    out["us_per_step"] = round(per_step[ranked[0]], 1)
+    out["share_of_op_time"] = {op: round(per_step[op] / total, 3) for op in ranked}
+    if len(ranked) > 1:
+        nxt = _roofline_of(ranked[1], ops[ranked[1]])
+        nxt["launches_per_step"] = launches[ranked[1]]
+        nxt["us_per_step"] = round(per_step[ranked[1]], 1)
+        out["next"] = nxt
+    return out
 
 
 # ---------------------------------------------------------------- main
@@ -894,7 +949,7 @@ def main():
                     help="attention mode: the attention core at the local, global and ViT-L "
                          "shapes")
     ap.add_argument("--headline", action="store_true",
-                    help="headline mode: only the timed 12-view step and the GELU launch "
+                    help="headline mode: only the timed 12-view step and the per-operation "
                          "timing behind the roofline object, without the other sections")
     ap.add_argument("--sweep", type=str, default=None, metavar="VIEWS",
                     help="size-sweep mode: the per-operation table at each comma-separated "
@@ -972,13 +1027,13 @@ def main():
     log(f"{ms_per_step:.3f} ms/step, {value:.1f} GB/s")
     if args.headline:
         del step_graph
-        gelu = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters,
-                            only="gelu")["gelu"]
+        ops = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters)
         print(json.dumps({"headline": {"value": round(value, 1), "unit": "GB/s",
                                        "ms_per_step": round(ms_per_step, 4),
                                        "steps": args.steps, "warmup": args.warmup,
-                                       "bytes_per_step": int(nbytes),
-                                       "roofline": roofline_entry(gelu)}}), flush=True)
+                                       "bytes_per_step": int(nbytes), "ops_12view": ops,
+                                       "roofline": roofline_entry(ops, model.plan)}}),
+              flush=True)
         return
 
     # single-image block: 866 rows, 12 blocks captured in one HIP graph
@@ -1006,7 +1061,6 @@ def main():
     patch = [patch_embed_timing(rt, rng, 336, 504, D, args.op_iters),
              patch_embed_timing(rt, rng, 336, 504, D, args.op_iters, views=12),
              patch_embed_timing(rt, rng, 672, 1008, 1024, args.op_iters)]
-    gelu = ops12["gelu"]
     log("fused linear epilogues")
     linear = linear_epilogue_timing(rt, rng, model.rows, 10)
     log("attention and whole blocks")
@@ -1059,7 +1113,7 @@ def main():
         "full_block": full_block,
         "vitl_1008x672": vitl,
         "pipeline": pipeline,
-        "roofline": roofline_entry(gelu),
+        "roofline": roofline_entry(ops12, model.plan),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -98,6 +98,31 @@ void* vk_runtime_stream(vk_runtime* rt);
 /* Number of compute units of the runtime's device (0 on error). */
 int vk_runtime_cu_count(vk_runtime* rt);
 
+/* Summation order of the LayerNorm mean and variance, for every LayerNorm
+ * the runtime enqueues after the call: vk_layernorm_f32 / _into, the fused
+ * LayerScale + residual + LayerNorm (and the block's camera-slot form), the
+ * capture and the token -> CHW hand-off, the LayerNorm the residual
+ * projections write for the next block, and the per-(head, token) Q/K
+ * LayerNorm (standalone, in the block sequences and in the QKV projection's
+ * epilogue).
+ *   VK_LN_ORDER_TREE (default): a wave-level tree; results match the CPU
+ *     within rtol 1e-5 (every fused form gives the bits of the separate
+ *     calls).
+ *   VK_LN_ORDER_SEQUENTIAL: the CPU kernel's order, what the reference's
+ *     layernorm_f32_cpu_order names (vit_block.rs:528-537; the sums of
+ *     dpt_head.rs:272-296): mean = (x0 + x1 + ... ) / cols and the biased
+ *     two-pass variance summed left to right, inv = 1/sqrtf(var + eps)
+ *     correctly rounded, y = (x - mean) * inv * gamma + beta -- every
+ *     LayerNorm then gives the CPU's bits.  Slower: a sum in that order is
+ *     one chain of dependent adds per row.
+ * The order of captured graphs is the order at capture.  Returns
+ * VK_ERR_INVALID for other values. */
+#define VK_LN_ORDER_TREE 0
+#define VK_LN_ORDER_SEQUENTIAL 1
+int vk_runtime_set_layernorm_order(vk_runtime* rt, int order);
+/* The runtime's current LayerNorm order (negative status on error). */
+int vk_runtime_layernorm_order(vk_runtime* rt);
+
 /* ------------------------------------------------------------------ */
 /* tensors and transfers                                                */
 /* ------------------------------------------------------------------ */
@@ -148,8 +173,10 @@ int vk_overwrite_prefix_f32(vk_runtime* rt, vk_tensor* tokens,
 /* CudaRuntime::layernorm_f32_cpu_order(x, gamma, beta, rows, cols, eps)
  * (vit_block.rs:528-537, 567-576, 627-636): row LayerNorm, biased two-pass
  * variance, y = (x-mean)*inv*gamma + beta.  Returns a new tensor.  The
- * reduction is a wave-level tree (not the CPU's sequential order); results
- * match the CPU within rtol 1e-5.  cols % 4 == 0, cols <= 8192. */
+ * mean and variance sum in the runtime's LayerNorm order
+ * (vk_runtime_set_layernorm_order): a wave-level tree by default, matching
+ * the CPU within rtol 1e-5; with VK_LN_ORDER_SEQUENTIAL the CPU's own
+ * left-to-right order and its bits.  cols % 4 == 0, cols <= 8192. */
 int vk_layernorm_f32(vk_runtime* rt, const vk_tensor* x, const vk_tensor* gamma,
                      const vk_tensor* beta, size_t rows, size_t cols, float eps,
                      vk_tensor** out);
@@ -218,12 +245,15 @@ int vk_qk_norm_rope_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
                         float freq, float eps);
 /* The same with an explicit RoPE convention (VK_ROPE_* flags; 0 gives
  * vk_qk_norm_rope_f32) and positions of dtype f32 (the CUDA runtime's
- * device encoding, truncated toward zero), i32 or i64 (the CPU kernel's
- * `&[i64]`, qk_norm_rope_f32_da3_base at vit_block.rs:911-924; values must
- * fit in 32 bits).  Positions outside the runtime's cos/sin table (negative
- * or above 1023 and every grid coordinate seen so far) take the same f32
- * angle and the device's single-precision sincosf (within 2 ulp of the
- * table's double-rounded values). */
+ * device encoding, truncated toward zero as `value as i64` reads it: NaN
+ * gives 0, +-inf saturates), i32 or i64 (the CPU kernel's `&[i64]`,
+ * qk_norm_rope_f32_da3_base at vit_block.rs:911-924).  Every position p of
+ * any dtype and range turns by the angle (float)p * inv_freq_j, the CPU
+ * kernel's conversion (an i64 of 2^32 + 5 rotates by (float)(2^32 + 5)).
+ * Positions outside the runtime's cos/sin table (negative or above 1023
+ * and every grid coordinate seen so far) take that f32 angle and the
+ * device's single-precision sincosf (within 2 ulp of the table's
+ * double-rounded values). */
 int vk_qk_norm_rope_mode_f32(vk_runtime* rt, vk_tensor* q, vk_tensor* k,
                              const vk_tensor* q_gamma, const vk_tensor* q_beta,
                              const vk_tensor* k_gamma, const vk_tensor* k_beta,
@@ -632,7 +662,12 @@ typedef struct vk_vit_activations {
                                        overwrite is fused too              */
 #define VK_BLOCK_CAMERA_WRITTEN 8u  /* at alt_start: the previous block's
                                        fused LS2+res+LN1 already wrote the
-                                       camera slot (and LN1)               */
+                                       camera slot (and LN1).  Valid only
+                                       with VK_BLOCK_SKIP_LN1, only at layer
+                                       alt_start, and only after a
+                                       VK_BLOCK_FUSE_NEXT_LN1 call at
+                                       alt_start-1 that was given the camera
+                                       token; other uses: VK_ERR_INVALID   */
 
 /* One DA3 ViT block's fused per-token operations, in the reference order of
  * run_tail_device (vit_block.rs:489-582) and vit_block_with_views

@@ -7,6 +7,7 @@ summed over the launches the block plan issues: 12 ViT-B blocks over 12
 views of 866 tokens, LayerScale + residual fused with the following
 LayerNorm, the camera slot written inside the pass before alt_start.
 """
+import numpy as np
 import pytest
 
 vh = pytest.importorskip("vestra_hip")
@@ -68,3 +69,43 @@ def test_step_bytes_without_the_camera_fusion():
     unfused = bench.step_bytes(n, 12, plan)
     assert unfused - fused == (ls_res(n) + 2 * 12 * D * 4 + ln(n)) - (ls_res_ln(n) + 12 * D * 4)
     assert unfused == 7725969408   # the headline's bytes per step before the fusion
+
+
+def test_step_launches_and_the_dominant_kernel():
+    plan = bench.block_plan(12, 4)
+    n = bench.step_launches(plan)
+    # LN1 of block 0; LS1+res+LN2 in every block and LS2+res+LN1 (next) in
+    # all but the last, whose LS2+res stands alone; the camera slot inside
+    # the fused pass before alt_start
+    assert n == {"layernorm": 1, "qk_norm_rope": 12, "layerscale_residual_layernorm": 23,
+                 "gelu": 12, "layerscale_residual": 1, "camera_copy": 0}
+
+    def entry(us, nbytes):
+        return {"us": us, "bytes": nbytes, "GB_s": nbytes / us / 1e3}
+
+    # per-launch times of the committed headline profile: the fused
+    # LayerScale + LayerNorm dominates (23 x 23.2 us against 12 x 39.7 us)
+    ops = {"layernorm": entry(12.9, ln(10392)), "qk_norm_rope": entry(22.1, qk(10392)),
+           "layerscale_residual_layernorm": entry(23.2, ls_res_ln(10392)),
+           "gelu": entry(39.7, gelu(10392)), "layerscale_residual": entry(16.8, ls_res(10392))}
+    r = bench.roofline_entry(ops, plan)
+    assert r["kernel"].startswith("ls_residual_layernorm_rows")
+    assert r["launches_per_step"] == 23
+    assert r["frac"] == round(ls_res_ln(10392) / 23.2e-6 / 8e12, 4)
+    assert r["next"]["kernel"].startswith("gelu_kernel")
+    assert abs(sum(r["share_of_op_time"].values()) - 1) < 1e-2
+    # a slower GELU takes the roofline over
+    ops["gelu"] = entry(50.0, gelu(10392))
+    assert bench.roofline_entry(ops, plan)["kernel"].startswith("gelu_kernel")
+
+
+def test_record_margin_shapes():
+    from conftest import _MARGINS, record_margin
+    got = np.ones((3, 4))
+    ref = got + 1e-7
+    r = record_margin("_selftest", got, ref, tol=np.full((3, 4), 2e-7))
+    assert abs(r["bound_used"] - 0.5) < 1e-6 and r["max_abs"] > 0
+    r = record_margin("_selftest", got.ravel(), ref, atol=1e-6, rtol=0.0)
+    assert abs(r["bound_used"] - 0.1) < 1e-6
+    assert abs(r["max_rel_ref_ge_1e-3"] - 1e-7) < 1e-9
+    _MARGINS.pop("_selftest")

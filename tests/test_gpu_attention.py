@@ -21,6 +21,7 @@ import numpy as np
 import pytest
 
 import oracle
+from conftest import record_margin
 from test_gpu_patch_block import normals
 
 pytestmark = pytest.mark.gpu
@@ -50,6 +51,7 @@ def _reference_and_bound(q, k, v, rows=None):
 
 def _assert_attention(got, want, bound, label):
     tol = 1e-6 + 1e-5 * np.abs(want) + bound
+    record_margin("attention", got, want, tol=tol, label=label)
     d = np.abs(got.astype(np.float64) - want.astype(np.float64))
     worst = np.unravel_index(np.argmax(d / tol), d.shape)
     assert np.all(d <= tol), (f"[{label}] |d|={d[worst]:.3e} > tol={tol[worst]:.3e} at {worst} "

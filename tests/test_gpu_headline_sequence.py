@@ -141,3 +141,22 @@ def test_camera_write_fused_into_the_previous_pass(rt, rng, views):
                                                           "hidden")})
     for n in outs[0]:
         assert np.array_equal(outs[0][n], outs[1][n]), n
+
+
+@pytest.mark.parametrize("layer,flags", [
+    (bench.ALT, vh.VK_BLOCK_CAMERA_WRITTEN),                          # without SKIP_LN1
+    (bench.ALT, vh.VK_BLOCK_CAMERA_WRITTEN | vh.VK_BLOCK_FUSE_LS_LN),
+    (bench.ALT + 1, vh.VK_BLOCK_CAMERA_WRITTEN | vh.VK_BLOCK_SKIP_LN1),  # not at alt_start
+    (0, vh.VK_BLOCK_CAMERA_WRITTEN | vh.VK_BLOCK_SKIP_LN1),
+])
+def test_camera_written_flag_rejected_out_of_place(rt, rng, layer, flags):
+    """VK_BLOCK_CAMERA_WRITTEN is taken only together with VK_BLOCK_SKIP_LN1
+    at layer alt_start; any other use is an argument error raised before
+    anything is enqueued (the tokens stay as they were)."""
+    model = bench.Model(rt, rng, views=1)
+    before = model.act["tokens"].numpy()
+    with pytest.raises(vh.VestraError, match="CAMERA_WRITTEN"):
+        model.rt.vit_block_fused_ops(model.cfg, layer, model.structs[layer],
+                                     model.structs[layer + 1], model.act_struct,
+                                     model.shape.gh, model.shape.gw, 1, model.camera, flags)
+    assert np.array_equal(model.act["tokens"].numpy(), before)

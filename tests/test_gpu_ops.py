@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import F32_ATOL, F32_RTOL, W16_ATOL, W16_RTOL, assert_parity
+from conftest import F32_ATOL, F32_RTOL, W16_ATOL, W16_RTOL, assert_parity, record_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -34,7 +34,10 @@ def test_layernorm_matches_oracle(rt, rng, rows, cols):
     b = normals(rng, cols, scale=0.02)
     out = rt.layernorm_f32_cpu_order(rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b),
                                      rows, cols, 1e-6).numpy()
-    assert_parity(out, oracle.layernorm(x, g, b, 1e-6), F32_ATOL, F32_RTOL, f"ln {rows}x{cols}")
+    ref = oracle.layernorm(x, g, b, 1e-6)
+    assert_parity(out, ref, F32_ATOL, F32_RTOL, f"ln {rows}x{cols}")
+    record_margin("layernorm (tree order)", out, ref, atol=F32_ATOL, rtol=F32_RTOL,
+                  label=f"{rows}x{cols}")
 
 
 def test_layernorm_in_place_and_f16_params(rt, rng):
@@ -74,6 +77,8 @@ def test_gelu_matches_oracle(rt, rng, n):
     t = rt.upload_f32(x)
     rt.gelu_f32_in_place(t)
     assert_parity(t.numpy(), oracle.gelu(x), F32_ATOL, F32_RTOL, f"gelu n={n}")
+    record_margin("gelu (A&S erf, v_rcp/v_exp)", t.numpy(), oracle.gelu(x), atol=F32_ATOL,
+                  rtol=F32_RTOL, label=f"n={n}")
 
 
 def test_gelu_erf_variant_matches_oracle(rt, rng):
@@ -170,6 +175,9 @@ def test_qk_norm_rope_reference_form(rt, rng, n_special, gh, gw, glob):
     rq, rk = oracle.qk_norm_rope(q, k, qg, qb, kg, kb, pos, heads, n)
     assert_parity(tq.numpy(), rq, F32_ATOL, F32_RTOL, "q")
     assert_parity(tk.numpy(), rk, F32_ATOL, F32_RTOL, "k")
+    for name, got, ref in (("q", tq.numpy(), rq), ("k", tk.numpy(), rk)):
+        record_margin("qk_norm_rope (tree order)", got, ref, atol=F32_ATOL, rtol=F32_RTOL,
+                      label=f"{name} {n_special}+{gh}x{gw}{' global' if glob else ''}")
 
 
 @pytest.mark.parametrize("heads,n_special,gh,gw", [(3, 1, 2, 3), (1, 2, 1, 3), (5, 2, 1, 1)])

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import F32_ATOL, F32_RTOL, assert_parity
+from conftest import F32_ATOL, F32_RTOL, assert_parity, record_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -34,6 +34,8 @@ def assert_dot_parity(got, ref, scale, k, label):
     scale = np.asarray(scale, np.float64).reshape(-1)
     bound = F32_ATOL + F32_RTOL * np.abs(ref) + 2.0 * np.sqrt(k) * 2.0 ** -24 * scale
     err = np.abs(got - ref)
+    record_margin("f32 dot products (projections, patch embedding)", got, ref, tol=bound,
+                  label=label)
     worst = int(np.argmax(err / bound))
     assert np.all(err <= bound), (f"[{label}] worst@{worst} got={got[worst]!r} "
                                   f"ref={ref[worst]!r} err={err[worst]:.3e} "

@@ -106,6 +106,33 @@ def test_rope2d_beyond_the_table(rt, rng, mode):
     assert_parity(t.numpy(), ref, F32_ATOL, F32_RTOL, f"rope2d large positions mode {mode}")
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_rope2d_positions_beyond_32_bits(rt, rng, mode):
+    """i64 coordinates past the int32 range, and f32 ones past it or NaN,
+    rotate by (float)p * inv_freq as the CPU kernel converts its i64
+    positions (no narrowing to 32 bits on the way): 2^32 + 5 is the angle
+    of (float)(2^32 + 5), not of 5."""
+    heads, n = 2, 6
+    x = normals(rng, heads, n, 64)
+    pos = np.array([[2 ** 32 + 5, 7], [3, -(2 ** 33) + 1], [2 ** 40 + 3, 2 ** 31],
+                    [2 ** 31 - 1, -(2 ** 31) - 1], [5, 2 ** 32 + 5], [-(2 ** 62), 1]], np.int64)
+    t = rt.upload_f32(x)
+    rt.rope2d_f32(t, rt.upload_i64(pos), heads, n, rope_mode=mode)
+    ref = oracle.rope2d(x, heads, n, 64, pos, 100.0, mode)
+    assert_parity(t.numpy(), ref, F32_ATOL, F32_RTOL, f"rope2d i64 positions mode {mode}")
+    # the same rows with positions narrowed to 32 bits rotate differently
+    narrowed = oracle.rope2d(x, heads, n, 64, pos.astype(np.int32).astype(np.int64), 100.0, mode)
+    assert not np.allclose(t.numpy().reshape(-1), narrowed.reshape(-1), rtol=1e-3, atol=1e-3)
+    # f32 positions: truncated toward zero like `value as i64`, NaN as 0
+    fpos = np.array([[3.0e9, 7.9], [-2.5e10, 1.0], [np.nan, 2.0], [1e12, -0.5], [4.5, 6.0],
+                     [0.0, np.nan]], np.float32)
+    ipos = np.where(np.isnan(fpos), 0, np.trunc(fpos.astype(np.float64))).astype(np.int64)
+    t = rt.upload_f32(x)
+    rt.rope2d_f32(t, rt.upload_f32(fpos), heads, n, rope_mode=mode)
+    ref = oracle.rope2d(x, heads, n, 64, ipos, 100.0, mode)
+    assert_parity(t.numpy(), ref, F32_ATOL, F32_RTOL, f"rope2d f32 positions mode {mode}")
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("glob", [False, True], ids=["local", "global"])
 def test_grid_form_12_views(rt, rng, mode, glob):

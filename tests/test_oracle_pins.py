@@ -211,6 +211,21 @@ def test_rope_identity_at_origin(rng):
     assert np.array_equal(oracle.rope2d(x, 2, 3, 64, pos), x)
 
 
+def test_rope_i64_position_beyond_32_bits():
+    # A coordinate of 2^32 + 5 turns by the angle of its f32 conversion,
+    # (float)(2^32 + 5) = 2^32, as `p as f32 * inv_freq` reads an i64: not by
+    # 5 (its low 32 bits).  Frequency 0 turns by exactly that many radians.
+    theta = float(np.float32(2 ** 32 + 5))
+    assert theta == 2.0 ** 32
+    for half, pos in ((0, [2 ** 32 + 5, 0]), (32, [0, 2 ** 32 + 5])):
+        x = np.zeros((1, 1, 64), np.float32)
+        x[0, 0, half] = 1.0
+        y = oracle.rope2d(x, 1, 1, 64, np.array([pos], np.int64), 100.0, 0)[0, 0]
+        assert abs(float(y[half]) - math.cos(theta)) < 2e-6
+        assert abs(float(y[half + 16]) - math.sin(theta)) < 2e-6
+        assert abs(math.cos(theta) - math.cos(5.0)) > 0.1  # the narrowed angle differs
+
+
 def _pairs(mode):
     """Element pairs (a, b) of one 32-wide half under a RoPE convention:
     rotate-half (j, j+16) or interleaved (2j, 2j+1), in frequency order j."""

@@ -57,6 +57,17 @@ extern "C" int vk_vit_block_fused_ops(vk_runtime* rt, const vk_vit_config* cfg,
   VK_TRY(check_len(act->mlp_out, rows * D, "mlp_out"));
   VK_REQUIRE(!(flags & VK_BLOCK_FUSE_NEXT_LN1) || next_layer,
              "VK_BLOCK_FUSE_NEXT_LN1 needs next_layer");
+  // The camera slot can only have been written by the previous block's fused
+  // LS2 + residual + LN1 pass, which also produced this block's LN1: the flag
+  // is meaningful only with VK_BLOCK_SKIP_LN1 and only at alt_start.
+  if (flags & VK_BLOCK_CAMERA_WRITTEN) {
+    VK_REQUIRE(flags & VK_BLOCK_SKIP_LN1,
+               "VK_BLOCK_CAMERA_WRITTEN needs VK_BLOCK_SKIP_LN1 (the previous block's fused "
+               "LS2+res+LN1 pass writes both)");
+    VK_REQUIRE(cfg->alt_start >= 0 && layer_idx == static_cast<size_t>(cfg->alt_start),
+               "VK_BLOCK_CAMERA_WRITTEN is valid only at layer alt_start=%d (layer %zu)",
+               cfg->alt_start, layer_idx);
+  }
 
   const bool global = layer_uses_global(cfg, layer_idx);
 

@@ -46,6 +46,9 @@ struct vk_runtime {
   // captured earlier may still name them, so they live until the runtime
   // is destroyed.
   std::vector<void*> retired;
+  // Summation order of every LayerNorm the runtime enqueues
+  // (VK_LN_ORDER_TREE or VK_LN_ORDER_SEQUENTIAL), read at enqueue time.
+  int ln_order = VK_LN_ORDER_TREE;
 };
 
 struct vk_tensor {
@@ -144,6 +147,11 @@ int check_rope_mode(unsigned rope_mode);
 // Looks up, once per device and with that device current, the device
 // address of the allocation-free entry point's static scratch array.
 void noalloc_setup(int device);
+// For a linear of in_features 588 (a 3x14x14 patch filter): allocates and
+// fills lin->weight_patch, the rows of lin->weight_nk with the input order
+// (c, ky, kx) -> (ky, kx, c) of an HWC image's patch, zero-padded to 592, on
+// the runtime's stream.  Any other linear: nothing.
+int prepare_patch_filter(vk_runtime* rt, vk_linear* lin);
 // Makes rt->work hold at least `floats` floats (at least 8 Mi once
 // allocated, doubling on growth).  Growth is refused during stream capture:
 // run the sequence once eagerly first.  The buffer it replaces is retired,
@@ -239,10 +247,15 @@ enum LinearEpilogue {
 int launch_linear_wide(vk_runtime* rt, const LinearArgs& g, int epi, float* partial = nullptr,
                        size_t partial_floats = 0);
 
-// LayerNorm of `rows` x `cols` f32 rows (the layernorm_rows kernel) on raw
-// pointers; gamma/beta f16 when `f16`.
+// LayerNorm of `rows` x `cols` f32 rows on raw pointers, in the runtime's
+// LayerNorm order; gamma/beta f16 when `f16`.
 int layernorm_raw(vk_runtime* rt, const float* x, float* y, const void* gamma, const void* beta,
                   bool f16, int rows, int cols, float eps);
+// The statistics of the sequential-order LayerNorm alone: stats[2r] = mean,
+// stats[2r + 1] = 1/std of logical row r, read from stored row
+// (r / np) * n + ns + r % np of x (np 0: row r); cols % 4 == 0, <= 8192.
+int layernorm_stats_sequential(vk_runtime* rt, const float* x, float* stats, int rows, int cols,
+                               float eps, int np, int n, int ns);
 
 // Output projection of the head-major attention output with LayerScale +
 // residual into `residual`, then ln_out = LayerNorm(residual): the calls
@@ -372,6 +385,35 @@ __device__ __forceinline__ void row_mean_inv(const float4 (&v)[NV], int lane, in
   const float var = q / static_cast<float>(cols);
   *mean_out = mean;
   *inv_out = 1.0f / sqrtf(var + eps);
+}
+
+// Broadcast of lane SRC of every 16-lane DPP row to the whole row
+// (row_newbcast, gfx90a and later).
+template <int SRC>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + SRC, 0xF, 0xF, false));
+}
+
+template <int SRC>
+__device__ __forceinline__ void row16_seq_accum(float& s, const float4& v) {
+  if constexpr (SRC < 16) {
+    s += row_bcast<SRC>(v.x);
+    s += row_bcast<SRC>(v.y);
+    s += row_bcast<SRC>(v.z);
+    s += row_bcast<SRC>(v.w);
+    row16_seq_accum<SRC + 1>(s, v);
+  }
+}
+
+// Sum of the 64 values of a 16-lane DPP row (lane l holding elements
+// 4l..4l+3 in v) in the scalar reference's order,
+// (((0 + e0) + e1) + e2) + ... + e63: every lane of the row runs the whole
+// chain on broadcasts of each lane in turn, so all 16 hold the same bits.
+__device__ __forceinline__ float row16_seq_sum(float4 v) {
+  float s = 0.0f;
+  row16_seq_accum<0>(s, v);
+  return s;
 }
 
 // (v - mean) * inv * gamma + beta, each step rounded: the per-element

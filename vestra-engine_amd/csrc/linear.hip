@@ -120,7 +120,7 @@ __device__ __forceinline__ float4 qk_head_row(const LinearArgs& g, float4 v, int
                                               int row) {
   typedef typename QknTraits<QKN>::PT PT;
   const int rowc = row < g.M ? row : g.M - 1;
-  int py, px;
+  float py, px;
   vkq::grid_position(vkd::fmod_(static_cast<uint32_t>(rowc), g.qkn.tpv), g.qkn.n_special,
                      g.qkn.global, g.qkn.gw, &py, &px);
   const PT* gm = static_cast<const PT*>(is_k ? g.qkn.kg : g.qkn.qg);

@@ -19,6 +19,8 @@
 //  * Arithmetic per element follows the scalar reference order with every
 //    product and sum rounded (built with -ffp-contract=off); only the order
 //    of the mean/variance reductions differs (wave tree vs sequential).
+#include <algorithm>
+
 #include "common.h"
 #include "qk_rows.h"
 
@@ -133,6 +135,162 @@ __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
 }
 
 // ---------------------------------------------------------------------------
+// LayerNorm in the scalar reference's summation order (the runtime's
+// VK_LN_ORDER_SEQUENTIAL): mean = ((x0 + x1) + x2 + ...) / cols and the
+// biased two-pass variance summed the same way, left to right, then
+// 1/sqrtf(var + eps) correctly rounded -- the bits of the CPU kernel
+// (dpt_head.rs:272-296).  A sum in that order is one chain of `cols`
+// dependent adds, which no wave reduction reproduces, so a 256-thread
+// workgroup owns `rpw` whole rows: it loads them (coalesced float4, kept in
+// registers) into LDS, lane r of wave 0 walks row r of the LDS copy for the
+// mean, every thread replaces its elements in LDS by their rounded squared
+// deviations, lane r walks those for the variance, and every thread applies
+// the LayerNorm to its registers.  The rows of a workgroup walk in parallel
+// (one lane each); the chains (2 x cols adds per row) are the latency, which
+// the CU's other workgroups overlap with their loads and stores.
+//
+// LSRES: x += ls (.) yb (or + yb) first, written back to x, with the camera
+// slot (row 0 of every view of tpv rows) overwritten when CAM -- the fused
+// LayerScale + residual + LayerNorm's arithmetic, then its LayerNorm in
+// this order.  out null: only the statistics (mean, 1/std) go to `stats`,
+// for logical row r read from stored row (r / np) * n + ns + r % np (np 0:
+// row r) -- the capture's patch rows.
+// ---------------------------------------------------------------------------
+constexpr int kSeqThreads = 256;
+constexpr int kSeqMaxRows = 64;  // one chain lane per row, all in wave 0
+
+struct SeqLnArgs {
+  float* x;
+  const float* yb;
+  const void* ls;
+  const void* gamma;
+  const void* beta;
+  float* out;
+  float2* stats;
+  const float* cam;
+  int tpv;
+  int rows, cols, rpw;
+  float eps;
+  vkd::FastDivU32 c4;  // cols / 4
+  int np, n, ns;
+  vkd::FastDivU32 fnp;
+};
+
+template <int NV, typename PT, bool LSRES, bool HAS_LS, bool CAM>
+__global__ __launch_bounds__(kSeqThreads) void seq_layernorm_rows(SeqLnArgs a) {
+  // rpw rows of c4 + 1 float4 (the pad puts the 16 chain lanes' reads on
+  // distinct 4-bank groups), then the rows' (mean, 1/std)
+  __shared__ float4 rows_lds[NV * kSeqThreads + kSeqMaxRows];
+  __shared__ float2 st[kSeqMaxRows];
+  const int tid = threadIdx.x;
+  const int c4 = static_cast<int>(a.c4.d);
+  const int pitch4 = c4 + 1;
+  const int r0 = blockIdx.x * a.rpw;
+  const int nr = min(a.rpw, a.rows - r0);
+  const int slots = nr * c4;
+  float4 v[NV];
+  size_t off[NV];
+  // load (clamped to a valid slot: no load waits behind a guard)
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + kSeqThreads * i;
+    const int ec = e < slots ? e : slots - 1;
+    const int lr = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(ec), a.c4));
+    const int c = ec - lr * c4;
+    const int r = r0 + lr;
+    size_t row = static_cast<size_t>(r);
+    if (!LSRES && a.np) {
+      const int vw = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(r), a.fnp));
+      row = static_cast<size_t>(vw) * a.n + a.ns + (r - vw * a.np);
+    }
+    off[i] = row * a.cols + 4 * static_cast<size_t>(c);
+    v[i] = vkd::ld_stream(reinterpret_cast<const float4*>(a.x + off[i]));
+    if (LSRES) {
+      const float4 b = vkd::ld_stream(reinterpret_cast<const float4*>(a.yb + off[i]));
+      if (HAS_LS) {
+        const float4 g = Param<PT>::load4(static_cast<const PT*>(a.ls), c);
+        float t;
+        t = b.x * g.x; v[i].x = v[i].x + t;
+        t = b.y * g.y; v[i].y = v[i].y + t;
+        t = b.z * g.z; v[i].z = v[i].z + t;
+        t = b.w * g.w; v[i].w = v[i].w + t;
+      } else {
+        v[i].x = v[i].x + b.x;
+        v[i].y = v[i].y + b.y;
+        v[i].z = v[i].z + b.z;
+        v[i].w = v[i].w + b.w;
+      }
+      if (CAM && r % a.tpv == 0)
+        v[i] = reinterpret_cast<const float4*>(a.cam + (r >= a.tpv ? a.cols : 0))[c];
+      if (e < slots) vkd::st_stream(reinterpret_cast<float4*>(a.x + off[i]), v[i]);
+    }
+    if (e < slots) rows_lds[lr * pitch4 + c] = v[i];
+  }
+  __syncthreads();
+  if (tid < nr) {
+    const float4* rp = rows_lds + tid * pitch4;
+    float s = 0.0f;
+#pragma unroll 8
+    for (int c = 0; c < c4; ++c) {
+      const float4 w = rp[c];
+      s += w.x;
+      s += w.y;
+      s += w.z;
+      s += w.w;
+    }
+    st[tid].x = s / static_cast<float>(a.cols);
+  }
+  __syncthreads();
+  // squared deviations, each rounded, in place of the values
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + kSeqThreads * i;
+    if (e < slots) {
+      const int lr = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(e), a.c4));
+      const float m = st[lr].x;
+      float4 d;
+      d.x = v[i].x - m; d.x = d.x * d.x;
+      d.y = v[i].y - m; d.y = d.y * d.y;
+      d.z = v[i].z - m; d.z = d.z * d.z;
+      d.w = v[i].w - m; d.w = d.w * d.w;
+      rows_lds[lr * pitch4 + (e - lr * c4)] = d;
+    }
+  }
+  __syncthreads();
+  if (tid < nr) {
+    const float4* rp = rows_lds + tid * pitch4;
+    float q = 0.0f;
+#pragma unroll 8
+    for (int c = 0; c < c4; ++c) {
+      const float4 w = rp[c];
+      q += w.x;
+      q += w.y;
+      q += w.z;
+      q += w.w;
+    }
+    const float var = q / static_cast<float>(a.cols);
+    const float inv = 1.0f / sqrtf(var + a.eps);
+    st[tid].y = inv;
+    if (a.stats) a.stats[r0 + tid] = make_float2(st[tid].x, inv);
+  }
+  if (!a.out) return;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + kSeqThreads * i;
+    if (e < slots) {
+      const int lr = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(e), a.c4));
+      const int c = e - lr * c4;
+      const float2 ms = st[lr];
+      vkd::st_stream(reinterpret_cast<float4*>(a.out + off[i]),
+                     vkd::ln_apply4(v[i], ms.x, ms.y,
+                                    Param<PT>::load4(static_cast<const PT*>(a.gamma), c),
+                                    Param<PT>::load4(static_cast<const PT*>(a.beta), c)));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q/K LayerNorm (head_dim 64) + 2D RoPE, in place.
 // ---------------------------------------------------------------------------
 using namespace vkq;
@@ -149,7 +307,7 @@ using namespace vkq;
 constexpr int kQkRowsPerGroup = VK_QK_ROWS_PER_GROUP;
 constexpr int kQkThreads = 256;  // threads per workgroup: kQkThreads / 16 row groups
 
-template <typename PT, bool HAS_NORM, int POS, int PAIR>
+template <typename PT, bool HAS_NORM, int POS, int PAIR, bool SEQ = false>
 __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
     const PT* __restrict__ qb, const PT* __restrict__ kg, const PT* __restrict__ kb,
@@ -171,7 +329,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     for (int p = 0; p < NP; ++p) {
       const uint32_t r = grp * NP + p;
       rr[p] = r < sh.rows_per_tensor ? r : sh.rows_per_tensor - 1;
-      int py, px;
+      float py, px;
       qk_row_position<POS>(rr[p], sh, pos_yx, &py, &px);
       v[2 * p] = vkd::ld_stream(reinterpret_cast<const float4*>(q + static_cast<size_t>(rr[p]) * 64) + l);
       v[2 * p + 1] =
@@ -186,7 +344,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kQkRowsPerGroup; ++j)
-      v[j] = qk_row_apply<HAS_NORM, PAIR>(v[j], l, op[j], eps);
+      v[j] = qk_row_apply<HAS_NORM, PAIR, SEQ>(v[j], l, op[j], eps);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       if (grp * NP + p < sh.rows_per_tensor) {
@@ -204,7 +362,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     const uint32_t gc = gr < total ? gr : total - 1;
     const bool is_k = gc >= sh.rows_per_tensor;
     const uint32_t r = is_k ? gc - sh.rows_per_tensor : gc;
-    int py, px;
+    float py, px;
     qk_row_position<POS>(r, sh, pos_yx, &py, &px);
     v[j] = vkd::ld_stream(reinterpret_cast<const float4*>((is_k ? k : q) + static_cast<size_t>(r) * 64) + l);
     op[j] = qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, is_k ? kg : qg, is_k ? kb : qb, py, px,
@@ -212,7 +370,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int j = 0; j < kQkRowsPerGroup; ++j) v[j] = qk_row_apply<HAS_NORM, PAIR>(v[j], l, op[j], eps);
+  for (int j = 0; j < kQkRowsPerGroup; ++j) v[j] = qk_row_apply<HAS_NORM, PAIR, SEQ>(v[j], l, op[j], eps);
 #pragma unroll
   for (int j = 0; j < kQkRowsPerGroup; ++j) {
     const uint32_t gr = grp * kQkRowsPerGroup + j;
@@ -263,9 +421,54 @@ int ln_instance_cols(int cols) {
   return -1;
 }
 
+// Rows per workgroup of the sequential-order kernel for rows of `cols`
+// floats (at most 12 float4 per thread, one chain lane per row) and the
+// instance (float4 per thread) that holds them.
+SeqLnArgs seq_args(float* x, int rows, int cols, float eps, int* nv) {
+  SeqLnArgs a{};
+  a.x = x;
+  a.rows = rows;
+  a.cols = cols;
+  a.eps = eps;
+  a.rpw = std::max(1, std::min(kSeqMaxRows, 12 * kSeqThreads * 4 / cols));
+  a.c4 = vkd::make_fastdiv(static_cast<uint32_t>(cols / 4));
+  a.tpv = 1;
+  const int need = (a.rpw * (cols / 4) + kSeqThreads - 1) / kSeqThreads;
+  *nv = need <= 4 ? 4 : (need <= 8 ? 8 : 12);
+  return a;
+}
+
+template <typename PT, bool LSRES, bool HAS_LS, bool CAM>
+int launch_seq(vk_runtime* rt, const SeqLnArgs& a, int nv) {
+  const dim3 grid(static_cast<unsigned>((a.rows + a.rpw - 1) / a.rpw)), block(kSeqThreads);
+  switch (nv) {
+    case 4:
+      hipLaunchKernelGGL((seq_layernorm_rows<4, PT, LSRES, HAS_LS, CAM>), grid, block, 0,
+                         rt->stream, a);
+      break;
+    case 8:
+      hipLaunchKernelGGL((seq_layernorm_rows<8, PT, LSRES, HAS_LS, CAM>), grid, block, 0,
+                         rt->stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((seq_layernorm_rows<12, PT, LSRES, HAS_LS, CAM>), grid, block, 0,
+                         rt->stream, a);
+      break;
+  }
+  return vk::check_launch("seq_layernorm_rows");
+}
+
 template <typename PT>
 int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
                      const void* b, int rows, int cols, float eps) {
+  if (rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+    int snv = 0;
+    SeqLnArgs a = seq_args(const_cast<float*>(x), rows, cols, eps, &snv);
+    a.gamma = g;
+    a.beta = b;
+    a.out = y;
+    return launch_seq<PT, false, false, false>(rt, a, snv);
+  }
   const int nv = ln_instance_cols(cols);
   dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
   auto G = static_cast<const PT*>(g);
@@ -292,6 +495,19 @@ template <typename PT, bool HAS_LS>
 int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
                      const void* g, const void* b, float* out, int rows, int cols,
                      float eps, const float* cam = nullptr, int tpv = 1) {
+  if (rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+    int snv = 0;
+    SeqLnArgs a = seq_args(x, rows, cols, eps, &snv);
+    a.yb = yb;
+    a.ls = ls;
+    a.gamma = g;
+    a.beta = b;
+    a.out = out;
+    a.cam = cam;
+    a.tpv = tpv;
+    return cam ? launch_seq<PT, true, HAS_LS, true>(rt, a, snv)
+               : launch_seq<PT, true, HAS_LS, false>(rt, a, snv);
+  }
   const int nv = ln_instance_cols(cols);
   dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
   auto LS = static_cast<const PT*>(ls);
@@ -326,10 +542,18 @@ int launch_qk(vk_runtime* rt, float* q, float* k, const void* qg, const void* qb
   const long long total = static_cast<long long>(sh.tensors) * sh.rows_per_tensor;
   const long long groups = (total + kQkRowsPerGroup - 1) / kQkRowsPerGroup;
   const long long blocks = (groups + kQkThreads / 16 - 1) / (kQkThreads / 16);
-  hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR>),
-                     dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q, k,
-                     static_cast<const PT*>(qg), static_cast<const PT*>(qb),
-                     static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh, eps);
+  if (HAS_NORM && rt->ln_order == VK_LN_ORDER_SEQUENTIAL)
+    hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR, true>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q,
+                       k, static_cast<const PT*>(qg), static_cast<const PT*>(qb),
+                       static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh,
+                       eps);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q,
+                       k, static_cast<const PT*>(qg), static_cast<const PT*>(qb),
+                       static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh,
+                       eps);
   return vk::check_launch("qk_norm_rope_rows");
 }
 
@@ -420,6 +644,19 @@ int layernorm_raw(vk_runtime* rt, const float* x, float* y, const void* gamma, c
   if (rows == 0) return VK_OK;
   return f16 ? launch_layernorm<uint16_t>(rt, x, y, gamma, beta, rows, cols, eps)
              : launch_layernorm<float>(rt, x, y, gamma, beta, rows, cols, eps);
+}
+
+int layernorm_stats_sequential(vk_runtime* rt, const float* x, float* stats, int rows, int cols,
+                               float eps, int np, int n, int ns) {
+  if (rows == 0) return VK_OK;
+  int nv = 0;
+  SeqLnArgs a = seq_args(const_cast<float*>(x), rows, cols, eps, &nv);
+  a.stats = reinterpret_cast<float2*>(stats);
+  a.np = np;
+  a.n = n;
+  a.ns = ns;
+  a.fnp = vkd::make_fastdiv(static_cast<uint32_t>(np > 0 ? np : 1));
+  return launch_seq<float, false, false, false>(rt, a, nv);
 }
 
 }  // namespace vk

@@ -1,212 +1,32 @@
-// Patch embedding and the F32 linear for gfx950: the MFMA contractions of
-// the fused path.
+// Fused patch embedding for gfx950: the 14x14 / stride-14 patch convolution
+// of the u8 image, and the reference-shaped split entries around it
+// (patchify, CLS + position add, the bicubic position table).
 //
-// The 14x14 / stride-14 patch convolution is a GEMM
+// The convolution is a GEMM
 //   tokens[p, e] = sum_k A[p, k] * W[e, k] + b[e]
 // with A the normalised, unfolded image.  patch_embed_kernel does it all in
 // one pass: A is gathered straight from the u8 HWC image and normalised
 // through a 3x256 lookup table in LDS (the table holds exactly
 // (u8/255 - mean)/std, so the normalisation is bit-identical to the scalar
 // path), the filter is read from a copy of its rows reordered at prepare
-// time to the image's byte order, the products run on v_mfma_f32_16x16x4_f32
-// (F32 in, F32 accumulate), and the epilogue adds the bias and the position
-// table and writes the assembled token rows (CLS + pos[0], register rows,
-// patch rows) so nothing round-trips through HBM.
-//
-// Both kernels compute 48 x 64 output tiles with 8 MFMA waves (two per
-// SIMD).  Wave w computes the 48 x 16 strip w%4 (three 16x16 accumulators)
-// over one half of K (split-K inside the workgroup); the two partial sums
-// meet in LDS before the epilogue.  Two waves per SIMD let one wave's MFMAs
-// run while the other waits on memory.
-//
-// Fragment order.  v_mfma_f32_16x16x4_f32 takes, in lane l, A[l%16][k] and
-// B[k][l%16] for the lane's k = one of 4 per step (lane group g = l/16).  K is
-// walked in blocks of 16: in block b, lane group g holds k = 16b + 4g + j in
-// component j of a 128-bit read, and step j of the block multiplies component
-// j, so four steps cover the block's 16 k once and one ds_read_b128 feeds
-// four MFMAs.  With LDS rows k-contiguous and a row pitch of 4 x odd floats,
-// the 16 rows of a fragment read start on 16 distinct 4-bank groups: no bank
-// conflicts.
-#include <cstring>
-#include <type_traits>
-#include <vector>
-
+// time to the image's byte order (prepare_patch_filter below), the products
+// run on v_mfma_f32_16x16x4_f32 (F32 in, F32 accumulate) on the 48 x 64
+// tiles of mfma_f32.h, and the epilogue adds the bias and the position table
+// and writes the assembled token rows (CLS + pos[0], register rows, patch
+// rows) so nothing round-trips through HBM.
 #include "common.h"
+#include "mfma_f32.h"
 
 namespace {
 
-using vk::LinearArgs;
 using vkd::xcd_tile;
-using namespace vk::linear_epilogue;
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using namespace vkm;
 
 #ifndef VK_PE_PIPELINED
 #define VK_PE_PIPELINED 1  // multi-view launches: the pipelined kernel
 #endif
 
-constexpr int BM = 48;
-constexpr int BN = 64;
-constexpr int kThreads = 512;
 constexpr int kPatch = 14;
-constexpr int kKAlign = 16;  // weight rows are zero-padded to a 16-block
-
-__device__ __forceinline__ void mfma_block(const float* arow, int t_pitch, const f32x4& b,
-                                           f32x4 acc[3]) {
-  f32x4 a[3];
-#pragma unroll
-  for (int t = 0; t < 3; ++t) a[t] = *reinterpret_cast<const f32x4*>(arow + t * t_pitch);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][j], b[j], acc[t], 0, 0, 0);
-}
-
-// Split-K reduction: waves 4-7 hand their partial sums to waves 0-3.  Returns
-// false in waves 4-7, which are then done.
-__device__ __forceinline__ bool reduce_halves(float* red, int strip, int half, int lane,
-                                              f32x4 acc[3]) {
-  if (half == 1) {
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[(strip * 12 + t * 4 + r) * 64 + lane] = acc[t][r];
-  }
-  __syncthreads();
-  if (half == 1) return false;
-#pragma unroll
-  for (int t = 0; t < 3; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t][r] += red[(strip * 12 + t * 4 + r) * 64 + lane];
-  return true;
-}
-
-// ---------------------------------------------------------------------------
-// F32 linear: out[m, n] = (sum_k x[m, k] W[n, k] + b[n]) (* ls[n])
-// K is staged through LDS in chunks of 192 (12 blocks); waves 0-3 take blocks
-// 0-5 of a chunk, waves 4-7 blocks 6-11.  While the MFMAs consume one chunk,
-// the next chunk's global loads are in flight into registers.
-// ---------------------------------------------------------------------------
-constexpr int KC = 192;
-constexpr int kLinPitch = 196;  // 4 x 49
-constexpr int kLinBlocks = KC / 16 / 2;  // per half
-constexpr int kA_PER_THREAD = (KC * BM + kThreads - 1) / kThreads;        // 18
-constexpr int kB_VEC_PER_THREAD = (KC * BN / 4 + kThreads - 1) / kThreads;  // 6
-static_assert(kLinPitch % 4 == 0 && (kLinPitch / 4) % 2 == 1, "pitch must be 4 x odd");
-static_assert(KC * BM % kThreads == 0 && KC * BN / 4 % kThreads == 0, "slots divide evenly");
-
-// The loaders never branch around a global load: a load inside a guard
-// makes the compiler wait for it before the next one, serialising the memory
-// latency.  Slots outside the matrix read a clamped (valid) address and are
-// zeroed when stored to LDS.  A slot e = tid + 512 i covers (m, kk) =
-// (e / KC, e % KC): k fastest, so a wave's loads walk along matrix rows and
-// its LDS stores hit consecutive banks.
-struct LinearStage {
-  float a[kA_PER_THREAD];
-  float4 b[kB_VEC_PER_THREAD];
-  uint32_t live_a, live_b;
-
-  __device__ __forceinline__ void fetch(const LinearArgs& g, int m0, int n0, int k0, int tid) {
-    live_a = 0;
-#pragma unroll
-    for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + kThreads * i;
-      const int m = e / KC, kk = e % KC;
-      const int gm = m0 + m, gk = k0 + kk;
-      live_a |= static_cast<uint32_t>(gm < g.M && gk < g.K) << i;
-      const int cm = gm < g.M ? gm : g.M - 1;
-      const int ck = gk < g.K ? gk : g.K - 1;
-      a[i] = g.x[static_cast<size_t>(cm) * g.K + ck];
-    }
-    live_b = 0;
-#pragma unroll
-    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
-      const int f = tid + kThreads * i;
-      const int n = f / (KC / 4), j = f % (KC / 4);
-      const int gn = n0 + n, gk = k0 + 4 * j;
-      // Kp % 4 == 0 and gk % 4 == 0: a vector never straddles the row end
-      live_b |= static_cast<uint32_t>(gn < g.N && gk < g.Kp) << i;
-      const int cn = gn < g.N ? gn : g.N - 1;
-      const int ck = gk < g.Kp ? gk : g.Kp - 4;
-      b[i] = *reinterpret_cast<const float4*>(g.wnk + static_cast<size_t>(cn) * g.Kp + ck);
-    }
-  }
-  __device__ __forceinline__ void store(float* As, float* Bs, int tid) const {
-#pragma unroll
-    for (int i = 0; i < kA_PER_THREAD; ++i) {
-      const int e = tid + kThreads * i;
-      As[(e / KC) * kLinPitch + e % KC] = ((live_a >> i) & 1) ? a[i] : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < kB_VEC_PER_THREAD; ++i) {
-      const int f = tid + kThreads * i;
-      const bool on = (live_b >> i) & 1;
-      const float4 v = make_float4(on ? b[i].x : 0.f, on ? b[i].y : 0.f, on ? b[i].z : 0.f,
-                                   on ? b[i].w : 0.f);
-      *reinterpret_cast<float4*>(Bs + (f / (KC / 4)) * kLinPitch + 4 * (f % (KC / 4))) = v;
-    }
-  }
-};
-
-template <int EPI>
-__global__ __launch_bounds__(kThreads) void linear_kernel(LinearArgs g) {
-  __shared__ __align__(16) float As[BM * kLinPitch];
-  __shared__ __align__(16) float Bs[BN * kLinPitch];
-  __shared__ float red[4 * 12 * 64];
-
-  const int tid = threadIdx.x;
-  __builtin_assume(tid < kThreads);
-  const int wave = tid >> 6, lane = tid & 63;
-  const int strip = wave & 3, half = wave >> 2;
-  const int gm = (g.M + BM - 1) / BM;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int m0 = (tile % gm) * BM, n0 = (tile / gm) * BN;
-
-  LinearStage st;
-  st.fetch(g, m0, n0, 0, tid);
-
-  f32x4 acc[3];
-#pragma unroll
-  for (int t = 0; t < 3; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int kofs = 4 * (lane >> 4) + 16 * kLinBlocks * half;
-  const float* arow = As + (lane & 15) * kLinPitch + kofs;
-  const float* brow = Bs + (strip * 16 + (lane & 15)) * kLinPitch + kofs;
-
-  for (int k0 = 0; k0 < g.K; k0 += KC) {
-    st.store(As, Bs, tid);
-    __syncthreads();
-    if (k0 + KC < g.K) st.fetch(g, m0, n0, k0 + KC, tid);
-#pragma unroll
-    for (int j = 0; j < kLinBlocks; ++j) {
-      const f32x4 b = *reinterpret_cast<const f32x4*>(brow + 16 * j);
-      mfma_block(arow + 16 * j, 16 * kLinPitch, b, acc);
-    }
-    __syncthreads();
-  }
-  if (!reduce_halves(red, strip, half, lane, acc)) return;
-
-  // epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile
-  const int col = n0 + strip * 16 + (lane & 15);
-  if (col >= g.N) return;
-  const float bias = g.bias[col];
-  const float ls = g.ls ? g.ls[col] : 1.0f;
-#pragma unroll
-  for (int t = 0; t < 3; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
-      if (row < g.M) {
-        float v = acc[t][r] + bias;
-        if (g.ls) v = v * ls;
-        float* o = g.out + static_cast<size_t>(row) * g.N + col;
-        if (EPI == kLinStore) *o = v;
-        if (EPI == kLinGelu) *o = vkd::gelu1<0>(v);
-        if (EPI == kLinGeluErf) *o = vkd::gelu1<1>(v);
-        if (EPI == kLinResidual) *o = *o + v;
-      }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Fused patch embedding.  K is taken in the image's own order, k = ky*42 +
@@ -851,190 +671,8 @@ __global__ void pos_embed_bicubic_kernel(const float* __restrict__ src, float* _
   out[i] = acc;
 }
 
-int alloc_copy(const float* host, size_t n, float** dev) {
-  VK_HIP(hipMalloc(dev, n * sizeof(float)));
-  hipError_t e = hipMemcpy(*dev, host, n * sizeof(float), hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    (void)hipFree(*dev);
-    *dev = nullptr;
-    return vk::hip_fail(e, "hipMemcpy(linear weights)");
-  }
-  return VK_OK;
-}
-
-// Weight rows [out][kp] with the input dimension contiguous and zero-padded
-// to kp = in rounded up to a 16-block, so 128-bit loads never straddle rows
-// and a last partial block multiplies zeros.
-int make_linear(vk_runtime* rt, size_t in, size_t out, const std::vector<float>& wnk,
-                const float* bias, const float* ls, vk_linear** res) {
-  auto* lin = new vk_linear;
-  lin->rt = rt;
-  vk::retain(rt);
-  lin->in_features = in;
-  lin->out_features = out;
-  lin->k_pitch = (in + kKAlign - 1) / kKAlign * kKAlign;
-  int s = alloc_copy(wnk.data(), lin->k_pitch * out, &lin->weight_nk);
-  if (s == VK_OK && in == static_cast<size_t>(kPeK)) {
-    // (c, ky, kx) -> (ky, kx, c) for the image-order patch embedding
-    std::vector<float> wp(static_cast<size_t>(kPeKp) * out, 0.0f);
-    for (size_t o = 0; o < out; ++o)
-      for (int c = 0; c < 3; ++c)
-        for (int ky = 0; ky < kPatch; ++ky)
-          for (int kx = 0; kx < kPatch; ++kx)
-            wp[o * kPeKp + ky * kPeRowBytes + kx * 3 + c] =
-                wnk[o * lin->k_pitch + (c * kPatch + ky) * kPatch + kx];
-    s = alloc_copy(wp.data(), wp.size(), &lin->weight_patch);
-  }
-  if (s == VK_OK) s = alloc_copy(bias, out, &lin->bias);
-  if (s == VK_OK && ls) s = alloc_copy(ls, out, &lin->ls_gamma);
-  if (s != VK_OK) {
-    vk_linear_destroy(lin);
-    return s;
-  }
-  *res = lin;
-  return VK_OK;
-}
-
-int check_linear(const vk_linear* lin, const vk_tensor* x, size_t rows) {
-  VK_REQUIRE(x->dtype == VK_F32, "linear input must be f32");
-  VK_REQUIRE(x->len == rows * lin->in_features, "linear: x holds %zu, rows*in=%zu", x->len,
-             rows * lin->in_features);
-  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "linear: rows=%zu too large", rows);
-  const long long tiles = static_cast<long long>((rows + BM - 1) / BM) *
-                          static_cast<long long>((lin->out_features + BN - 1) / BN);
-  VK_UNSUPPORTED_IF(tiles > 0x7fffffffLL, "linear: %lld tiles", tiles);
-  return VK_OK;
-}
-
-// Output (or residual) checks; it must not overlap the input, which other
-// workgroups may still be reading while one writes.
-int check_linear_out(const vk_linear* lin, const vk_tensor* x, const vk_tensor* out, size_t rows,
-                     const char* what) {
-  VK_REQUIRE(out->dtype == VK_F32 && out->len == rows * lin->out_features,
-             "linear: %s must be f32 [rows*out=%zu] (holds %zu)", what, rows * lin->out_features,
-             out->len);
-  const char* xb = static_cast<const char*>(x->ptr);
-  const char* ob = static_cast<const char*>(out->ptr);
-  VK_REQUIRE(ob + out->len * 4 <= xb || xb + x->len * 4 <= ob || rows == 0,
-             "linear: %s overlaps the input", what);
-  return VK_OK;
-}
-
-LinearArgs linear_args(const vk_linear* lin, const vk_tensor* x, size_t rows, vk_tensor* out) {
-  LinearArgs g{};
-  g.x = static_cast<const float*>(x->ptr);
-  g.wnk = lin->weight_nk;
-  g.bias = lin->bias;
-  g.ls = lin->ls_gamma;
-  g.out = out ? static_cast<float*>(out->ptr) : nullptr;
-  g.M = static_cast<int>(rows);
-  g.N = static_cast<int>(lin->out_features);
-  g.K = static_cast<int>(lin->in_features);
-  g.Kp = static_cast<int>(lin->k_pitch);
-  return g;
-}
-
-bool tensors_disjoint(const vk_tensor* a, const vk_tensor* b) {
-  const char* pa = static_cast<const char*>(a->ptr);
-  const char* pb = static_cast<const char*>(b->ptr);
-  return a->len == 0 || b->len == 0 || pa + a->len * 4 <= pb || pb + b->len * 4 <= pa;
-}
-
-// The head-major forms need the wide kernel: K % 4 == 0 and an aligned x.
-int check_head_layout(const vk_linear* lin, const vk_tensor* x, size_t heads, size_t head_dim) {
-  VK_UNSUPPORTED_IF(head_dim != 64, "linear: head_dim=%zu (qualified: 64)", head_dim);
-  VK_REQUIRE(heads > 0, "linear: heads must be positive");
-  VK_UNSUPPORTED_IF(lin->in_features % 4 != 0 || reinterpret_cast<uintptr_t>(x->ptr) % 16 != 0,
-                    "linear: head-major forms need in_features %% 4 == 0 and an aligned input");
-  return VK_OK;
-}
-
-int launch_linear(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
-                  vk_tensor* out, int epi, float* partial = nullptr,
-                  size_t partial_floats = 0) {
-  if (rows == 0) return VK_OK;
-  LinearArgs g{};
-  g.x = static_cast<const float*>(x->ptr);
-  g.wnk = lin->weight_nk;
-  g.bias = lin->bias;
-  g.ls = lin->ls_gamma;
-  g.out = static_cast<float*>(out->ptr);
-  g.M = static_cast<int>(rows);
-  g.N = static_cast<int>(lin->out_features);
-  g.K = static_cast<int>(lin->in_features);
-  g.Kp = static_cast<int>(lin->k_pitch);
-  // 128x128 tiles wherever rows of x can be read as float4; the 48x64 kernel
-  // (scalar loads of x) for the rest
-  if (g.K % 4 == 0 && reinterpret_cast<uintptr_t>(g.x) % 16 == 0)
-    return vk::launch_linear_wide(rt, g, epi, partial, partial_floats);
-  const unsigned tiles = static_cast<unsigned>(((g.M + BM - 1) / BM) * static_cast<long long>((g.N + BN - 1) / BN));
-  const dim3 grid(tiles), block(kThreads);
-  switch (epi) {
-    case kLinStore: hipLaunchKernelGGL(linear_kernel<kLinStore>, grid, block, 0, rt->stream, g); break;
-    case kLinGelu: hipLaunchKernelGGL(linear_kernel<kLinGelu>, grid, block, 0, rt->stream, g); break;
-    case kLinGeluErf: hipLaunchKernelGGL(linear_kernel<kLinGeluErf>, grid, block, 0, rt->stream, g); break;
-    default: hipLaunchKernelGGL(linear_kernel<kLinResidual>, grid, block, 0, rt->stream, g); break;
-  }
-  return vk::check_launch("linear_kernel");
-}
-
-// ---------------------------------------------------------------------------
-// Weights in GGUF storage formats, expanded on the device.
-//
-// The reference widens F16 and dequantises Q8_0 tensors to f32 once, when
-// it reads the model (Gguf::tensor_f32, crates/da-gguf/src/reader.rs:279-349;
-// q8_0.rs:24-33), and its projections run on those f32 values.  Here the
-// stored bytes are uploaded as they are (half or about a quarter of the f32
-// bytes) and expanded by the kernels below straight into the linear's
-// resident [out, kp] f32 layout.  Both conversions are exact (an f16 widens
-// exactly; d*q of an f16 scale and an int8 needs at most 19 significant
-// bits), so the projections give the bits of the f32 preparation of the
-// same widened weights.  The matrix cores stay on the F32 path: keeping
-// F16 / Q8_0 resident and widening inside the GEMM would add conversion
-// work to every tile for no gain in time (the projections are MFMA-bound)
-// nor in fit (288 GB of HBM).
-// ---------------------------------------------------------------------------
-enum WeightSrc { kSrcF16 = 0, kSrcQ8 = 1 };
-constexpr int kQ8Block = 32;       // values per Q8_0 block (q8_0.rs:10)
-constexpr int kQ8BlockBytes = 34;  // f16 scale + 32 int8
-
-// Element f of a GGUF tensor in storage format SRC, as f32.
-template <int SRC>
-__device__ __forceinline__ float stored_value(const uint8_t* __restrict__ src, size_t f) {
-  if (SRC == kSrcF16) return vkd::f16_to_f32(reinterpret_cast<const uint16_t*>(src)[f]);
-  const uint8_t* b = src + (f / kQ8Block) * kQ8BlockBytes;
-  const uint16_t d = static_cast<uint16_t>(b[0] | (b[1] << 8));
-  const int8_t q = static_cast<int8_t>(b[2 + f % kQ8Block]);
-  return vkd::f16_to_f32(d) * static_cast<float>(q);
-}
-
-// Flat tensor conversion: dst[f] = stored_value(src, f).
-template <int SRC>
-__global__ __launch_bounds__(256) void expand_flat_kernel(const uint8_t* __restrict__ src,
-                                                          float* __restrict__ dst, long long n) {
-  const long long f = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
-  if (f < n) dst[f] = stored_value<SRC>(src, static_cast<size_t>(f));
-}
-
-// Linear weight rows: wnk[o*kp + i] = W(i, o) for i < in, 0 for the padding;
-// the stored tensor is [in, out] (IN_OUT, the projection layout of
-// prepare_linear_f32) or [out, in] (an OIHW filter).
-template <int SRC, bool IN_OUT>
-__global__ __launch_bounds__(256) void expand_weight_kernel(const uint8_t* __restrict__ src,
-                                                            float* __restrict__ wnk, int in,
-                                                            int out, int kp) {
-  const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= static_cast<long long>(out) * kp) return;
-  const int o = static_cast<int>(idx / kp), i = static_cast<int>(idx % kp);
-  float v = 0.0f;
-  if (i < in)
-    v = stored_value<SRC>(src, IN_OUT ? static_cast<size_t>(i) * out + o
-                                      : static_cast<size_t>(o) * in + i);
-  wnk[idx] = v;
-}
-
 // The patch kernel's copy of a 3x14x14 filter: input order (c, ky, kx) ->
-// (ky, kx, c), zero beyond 588 (the device form of the reorder in make_linear).
+// (ky, kx, c), zero beyond 588 (made at prepare time by prepare_patch_filter).
 __global__ __launch_bounds__(256) void patch_order_kernel(const float* __restrict__ wnk,
                                                           float* __restrict__ wp, int out, int kp) {
   const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
@@ -1049,459 +687,23 @@ __global__ __launch_bounds__(256) void patch_order_kernel(const float* __restric
   wp[idx] = v;
 }
 
-unsigned grid_for(long long n) { return static_cast<unsigned>((n + 255) / 256); }
-
-// Uploads `nbytes` of stored weights and expands them into a new linear.
-int make_linear_stored(vk_runtime* rt, size_t in, size_t out, int src_kind, bool in_out,
-                       const void* stored, size_t nbytes, const float* bias, const float* ls,
-                       vk_linear** res) {
-  auto* lin = new vk_linear;
-  lin->rt = rt;
-  vk::retain(rt);
-  lin->in_features = in;
-  lin->out_features = out;
-  lin->k_pitch = (in + kKAlign - 1) / kKAlign * kKAlign;
-  uint8_t* raw = nullptr;
-  int s = VK_OK;
-  const long long nw = static_cast<long long>(lin->k_pitch) * static_cast<long long>(out);
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&lin->weight_nk), nw * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&raw), nbytes);
-  if (e == hipSuccess) e = hipMemcpy(raw, stored, nbytes, hipMemcpyHostToDevice);
-  if (e != hipSuccess) s = vk::hip_fail(e, "upload of stored linear weights");
-  if (s == VK_OK) {
-    const int ii = static_cast<int>(in), oo = static_cast<int>(out),
-              kp = static_cast<int>(lin->k_pitch);
-    if (src_kind == kSrcF16 && in_out)
-      hipLaunchKernelGGL((expand_weight_kernel<kSrcF16, true>), grid_for(nw), 256, 0, rt->stream,
-                         raw, lin->weight_nk, ii, oo, kp);
-    else if (src_kind == kSrcF16)
-      hipLaunchKernelGGL((expand_weight_kernel<kSrcF16, false>), grid_for(nw), 256, 0, rt->stream,
-                         raw, lin->weight_nk, ii, oo, kp);
-    else if (in_out)
-      hipLaunchKernelGGL((expand_weight_kernel<kSrcQ8, true>), grid_for(nw), 256, 0, rt->stream,
-                         raw, lin->weight_nk, ii, oo, kp);
-    else
-      hipLaunchKernelGGL((expand_weight_kernel<kSrcQ8, false>), grid_for(nw), 256, 0, rt->stream,
-                         raw, lin->weight_nk, ii, oo, kp);
-    s = vk::check_launch("expand_weight_kernel");
-  }
-  if (s == VK_OK && in == static_cast<size_t>(kPeK)) {
-    const long long np = static_cast<long long>(kPeKp) * static_cast<long long>(out);
-    e = hipMalloc(reinterpret_cast<void**>(&lin->weight_patch), np * sizeof(float));
-    if (e != hipSuccess) {
-      s = vk::hip_fail(e, "hipMalloc(patch filter)");
-    } else {
-      hipLaunchKernelGGL(patch_order_kernel, grid_for(np), 256, 0, rt->stream, lin->weight_nk,
-                         lin->weight_patch, static_cast<int>(out),
-                         static_cast<int>(lin->k_pitch));
-      s = vk::check_launch("patch_order_kernel");
-    }
-  }
-  if (raw) {
-    // the expansion must finish before its source is released
-    const hipError_t se = hipStreamSynchronize(rt->stream);
-    if (s == VK_OK && se != hipSuccess) s = vk::hip_fail(se, "hipStreamSynchronize");
-    (void)hipFree(raw);
-  }
-  if (s == VK_OK) s = alloc_copy(bias, out, &lin->bias);
-  if (s == VK_OK && ls) s = alloc_copy(ls, out, &lin->ls_gamma);
-  if (s != VK_OK) {
-    vk_linear_destroy(lin);
-    return s;
-  }
-  *res = lin;
-  return VK_OK;
-}
-
-int check_prepare(size_t in_features, size_t out_features) {
-  VK_REQUIRE(in_features > 0 && out_features > 0, "empty linear");
-  VK_UNSUPPORTED_IF(out_features % 4 != 0, "linear: out_features=%zu must be a multiple of 4",
-                    out_features);
-  VK_UNSUPPORTED_IF(in_features > 0x7ffffff0 || out_features > 0x7fffffff ||
-                        in_features * out_features > (1ULL << 36),
-                    "linear too large");
-  return VK_OK;
-}
-
-int expand_flat(vk_runtime* rt, int src_kind, const vk_tensor* src, size_t n, vk_tensor* dst) {
-  if (n == 0) return VK_OK;
-  const auto* s = static_cast<const uint8_t*>(src->ptr);
-  auto* d = static_cast<float*>(dst->ptr);
-  const long long nn = static_cast<long long>(n);
-  if (src_kind == kSrcF16)
-    hipLaunchKernelGGL((expand_flat_kernel<kSrcF16>), grid_for(nn), 256, 0, rt->stream, s, d, nn);
-  else
-    hipLaunchKernelGGL((expand_flat_kernel<kSrcQ8>), grid_for(nn), 256, 0, rt->stream, s, d, nn);
-  return vk::check_launch("expand_flat_kernel");
-}
-
 }  // namespace
 
 namespace vk {
 
-namespace {
-
-// The residual projection followed by ln_out = LayerNorm(residual), for a
-// token-major input (heads == 0) or a head-major one.  The wide kernel takes
-// the LayerNorm into its split-K sum pass; an input it cannot read (K % 4 or
-// alignment) runs the two calls.
-int residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
-                       size_t heads, size_t head_dim, vk_tensor* residual,
-                       const vk_tensor* gamma, const vk_tensor* beta, float eps,
-                       vk_tensor* ln_out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && residual && gamma && beta && ln_out, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  if (heads > 0) {
-    VK_TRY(check_head_layout(lin, x, heads, head_dim));
-    VK_REQUIRE(lin->in_features == heads * head_dim,
-               "linear_residual_layernorm: in_features=%zu, expected heads*64=%zu",
-               lin->in_features, heads * head_dim);
-  }
-  VK_TRY(check_linear_out(lin, x, residual, rows, "residual"));
-  const size_t n = lin->out_features;
-  VK_REQUIRE((gamma->dtype == VK_F32 || gamma->dtype == VK_F16) && gamma->dtype == beta->dtype &&
-                 gamma->len == n && beta->len == n,
-             "linear_residual_layernorm: gamma/beta must be f32 or f16 [%zu]", n);
-  VK_UNSUPPORTED_IF(n > 8192, "linear_residual_layernorm: out_features=%zu (LayerNorm rows of "
-                    "at most 8192)", n);
-  VK_REQUIRE(ln_out->dtype == VK_F32 && ln_out->len == rows * n,
-             "linear_residual_layernorm: ln_out must be f32 [%zu]", rows * n);
-  VK_REQUIRE(tensors_disjoint(ln_out, residual) && tensors_disjoint(ln_out, x),
-             "linear_residual_layernorm: ln_out must not overlap the other tensors");
-  for (const vk_tensor* t : {static_cast<const vk_tensor*>(residual), gamma, beta,
-                             static_cast<const vk_tensor*>(ln_out)})
-    VK_REQUIRE(reinterpret_cast<uintptr_t>(t->ptr) % 16 == 0,
-               "linear_residual_layernorm: tensors must be 16-byte aligned");
-  if (rows == 0) return VK_OK;
-  const bool wide = lin->in_features % 4 == 0 && reinterpret_cast<uintptr_t>(x->ptr) % 16 == 0;
-  if (!wide) {
-    VK_TRY(launch_linear(rt, lin, x, rows, residual, kLinResidual));
-    return vk::layernorm_raw(rt, static_cast<const float*>(residual->ptr),
-                             static_cast<float*>(ln_out->ptr), gamma->ptr, beta->ptr,
-                             gamma->dtype == VK_F16, static_cast<int>(rows),
-                             static_cast<int>(n), eps);
-  }
-  LinearArgs g = linear_args(lin, x, rows, residual);
-  g.a_hnd = heads > 0 ? 1 : 0;
-  g.ln_gamma = gamma->ptr;
-  g.ln_beta = beta->ptr;
-  g.ln_f16 = gamma->dtype == VK_F16 ? 1 : 0;
-  g.ln_eps = eps;
-  g.ln_out = static_cast<float*>(ln_out->ptr);
-  return vk::launch_linear_wide(rt, g, kLinResidual);
-}
-
-}  // namespace
-
-int linear_hnd_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
-                                  size_t rows, size_t heads, size_t head_dim,
-                                  vk_tensor* residual, const vk_tensor* gamma,
-                                  const vk_tensor* beta, float eps, vk_tensor* ln_out) {
-  VK_REQUIRE(heads > 0, "linear: heads must be positive");
-  return residual_layernorm(rt, lin, hnd, rows, heads, head_dim, residual, gamma, beta, eps,
-                            ln_out);
-}
-
-int linear_residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
-                              size_t rows, vk_tensor* residual, const vk_tensor* gamma,
-                              const vk_tensor* beta, float eps, vk_tensor* ln_out) {
-  return residual_layernorm(rt, lin, x, rows, 0, 0, residual, gamma, beta, eps, ln_out);
+int prepare_patch_filter(vk_runtime* rt, vk_linear* lin) {
+  if (lin->in_features != static_cast<size_t>(kPeK)) return VK_OK;
+  const long long np = static_cast<long long>(kPeKp) * static_cast<long long>(lin->out_features);
+  VK_HIP(hipMalloc(reinterpret_cast<void**>(&lin->weight_patch), np * sizeof(float)));
+  hipLaunchKernelGGL(patch_order_kernel, dim3(static_cast<unsigned>((np + 255) / 256)), dim3(256),
+                     0, rt->stream, lin->weight_nk, lin->weight_patch,
+                     static_cast<int>(lin->out_features), static_cast<int>(lin->k_pitch));
+  return vk::check_launch("patch_order_kernel");
 }
 
 }  // namespace vk
 
 extern "C" {
-
-int vk_linear_prepare_w16(vk_runtime* rt, size_t in_features, size_t out_features,
-                          const uint16_t* weight_in_out, const float* bias, const float* ls_gamma,
-                          vk_linear** out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(out && weight_in_out && bias, "null argument");
-  VK_TRY(check_prepare(in_features, out_features));
-  return make_linear_stored(rt, in_features, out_features, kSrcF16, true, weight_in_out,
-                            in_features * out_features * 2, bias, ls_gamma, out);
-}
-
-int vk_linear_prepare_q8_0(vk_runtime* rt, size_t in_features, size_t out_features,
-                           const uint8_t* blocks, size_t nbytes, const float* bias,
-                           const float* ls_gamma, vk_linear** out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(out && blocks && bias, "null argument");
-  VK_TRY(check_prepare(in_features, out_features));
-  const size_t n = in_features * out_features;
-  VK_REQUIRE(n % kQ8Block == 0, "q8_0: %zu elements, not a multiple of the block size %d", n,
-             kQ8Block);
-  VK_REQUIRE(nbytes == n / kQ8Block * kQ8BlockBytes, "q8_0: %zu bytes, expected %zu", nbytes,
-             n / kQ8Block * kQ8BlockBytes);
-  return make_linear_stored(rt, in_features, out_features, kSrcQ8, true, blocks, nbytes, bias,
-                            ls_gamma, out);
-}
-
-int vk_linear_prepare_oihw_w16(vk_runtime* rt, size_t in_features, size_t out_features,
-                               const uint16_t* weight_out_in, const float* bias, vk_linear** out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(out && weight_out_in && bias, "null argument");
-  VK_TRY(check_prepare(in_features, out_features));
-  return make_linear_stored(rt, in_features, out_features, kSrcF16, false, weight_out_in,
-                            in_features * out_features * 2, bias, nullptr, out);
-}
-
-int vk_widen_f16_f32(vk_runtime* rt, const vk_tensor* src, vk_tensor* dst) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(src && dst, "null argument");
-  VK_REQUIRE(src->dtype == VK_F16 && dst->dtype == VK_F32 && dst->len == src->len,
-             "widen: src must be f16 and dst f32 of the same length");
-  return expand_flat(rt, kSrcF16, src, src->len, dst);
-}
-
-int vk_dequantize_q8_0_f32(vk_runtime* rt, const vk_tensor* blocks, size_t n, vk_tensor* dst) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(blocks && dst, "null argument");
-  VK_REQUIRE(n % kQ8Block == 0, "q8_0: %zu elements, not a multiple of the block size %d", n,
-             kQ8Block);
-  VK_REQUIRE(blocks->dtype == VK_U8 && blocks->len == n / kQ8Block * kQ8BlockBytes,
-             "q8_0: blocks must be u8 [%zu]", n / kQ8Block * kQ8BlockBytes);
-  VK_REQUIRE(dst->dtype == VK_F32 && dst->len == n, "q8_0: dst must be f32 [%zu]", n);
-  return expand_flat(rt, kSrcQ8, blocks, n, dst);
-}
-
-int vk_linear_prepare_f32(vk_runtime* rt, size_t in_features, size_t out_features,
-                          const float* weight_in_out, const float* bias, const float* ls_gamma,
-                          vk_linear** out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(out && weight_in_out && bias, "null argument");
-  VK_REQUIRE(in_features > 0 && out_features > 0, "empty linear");
-  VK_UNSUPPORTED_IF(out_features % 4 != 0, "linear: out_features=%zu must be a multiple of 4",
-                    out_features);
-  VK_UNSUPPORTED_IF(in_features > 0x7ffffff0 || out_features > 0x7fffffff, "linear too large");
-  const size_t kp = (in_features + kKAlign - 1) / kKAlign * kKAlign;
-  std::vector<float> w(kp * out_features, 0.0f);
-  for (size_t i = 0; i < in_features; ++i)
-    for (size_t o = 0; o < out_features; ++o) w[o * kp + i] = weight_in_out[i * out_features + o];
-  return make_linear(rt, in_features, out_features, w, bias, ls_gamma, out);
-}
-
-int vk_linear_prepare_oihw_f32(vk_runtime* rt, size_t in_features, size_t out_features,
-                               const float* weight_out_in, const float* bias, vk_linear** out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(out && weight_out_in && bias, "null argument");
-  VK_REQUIRE(in_features > 0 && out_features > 0, "empty linear");
-  VK_UNSUPPORTED_IF(out_features % 4 != 0, "linear: out_features=%zu must be a multiple of 4",
-                    out_features);
-  VK_UNSUPPORTED_IF(in_features > 0x7ffffff0 || out_features > 0x7fffffff, "linear too large");
-  const size_t kp = (in_features + kKAlign - 1) / kKAlign * kKAlign;
-  std::vector<float> w(kp * out_features, 0.0f);
-  for (size_t o = 0; o < out_features; ++o)
-    std::memcpy(&w[o * kp], weight_out_in + o * in_features, in_features * sizeof(float));
-  return make_linear(rt, in_features, out_features, w, bias, nullptr, out);
-}
-
-int vk_linear_destroy(vk_linear* lin) {
-  if (!lin) return VK_OK;
-  vk_runtime* rt = lin->rt;
-  if (rt) (void)vk::bind_device(rt);
-  if (rt) (void)hipStreamSynchronize(rt->stream);
-  if (lin->weight_nk) (void)hipFree(lin->weight_nk);
-  if (lin->weight_patch) (void)hipFree(lin->weight_patch);
-  if (lin->bias) (void)hipFree(lin->bias);
-  if (lin->ls_gamma) (void)hipFree(lin->ls_gamma);
-  delete lin;
-  vk::release(rt);
-  return VK_OK;
-}
-
-size_t vk_linear_input_features(const vk_linear* lin) { return lin ? lin->in_features : 0; }
-
-int vk_linear_run_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
-                      vk_tensor** out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && out, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  vk_tensor* t = nullptr;
-  VK_TRY(vk_tensor_alloc(rt, VK_F32, rows * lin->out_features, &t));
-  const int s = launch_linear(rt, lin, x, rows, t, kLinStore);
-  if (s != VK_OK) {
-    vk_tensor_destroy(t);
-    return s;
-  }
-  *out = t;
-  return VK_OK;
-}
-
-int vk_linear_run_into_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
-                           vk_tensor* out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && out, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
-  return launch_linear(rt, lin, x, rows, out, kLinStore);
-}
-
-int vk_linear_run_gelu_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x, size_t rows,
-                           vk_tensor* out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && out, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
-  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_gelu: the linear carries a LayerScale");
-  return launch_linear(rt, lin, x, rows, out, kLinGelu);
-}
-
-int vk_linear_run_gelu_erf_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
-                               size_t rows, vk_tensor* out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && out, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
-  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_gelu_erf: the linear carries a LayerScale");
-  return launch_linear(rt, lin, x, rows, out, kLinGeluErf);
-}
-
-int vk_linear_run_residual_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
-                               size_t rows, vk_tensor* residual) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && residual, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_linear_out(lin, x, residual, rows, "residual"));
-  return launch_linear(rt, lin, x, rows, residual, kLinResidual);
-}
-
-int vk_linear_run_qkv_hnd_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
-                              size_t rows, size_t heads, size_t head_dim, vk_tensor* q,
-                              vk_tensor* k, vk_tensor* v) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && q && k && v, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_head_layout(lin, x, heads, head_dim));
-  VK_REQUIRE(lin->out_features == 3 * heads * head_dim,
-             "linear_run_qkv_hnd: out_features=%zu, expected 3*heads*head_dim=%zu",
-             lin->out_features, 3 * heads * head_dim);
-  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_qkv_hnd: the linear carries a LayerScale");
-  const size_t part = rows * heads * head_dim;
-  for (const vk_tensor* t : {q, k, v})
-    VK_REQUIRE(t->dtype == VK_F32 && t->len == part, "q, k, v must be f32 [rows*heads*64=%zu]",
-               part);
-  VK_REQUIRE(tensors_disjoint(x, q) && tensors_disjoint(x, k) && tensors_disjoint(x, v) &&
-                 tensors_disjoint(q, k) && tensors_disjoint(q, v) && tensors_disjoint(k, v),
-             "linear_run_qkv_hnd: tensors overlap");
-  if (rows == 0) return VK_OK;
-  LinearArgs g = linear_args(lin, x, rows, nullptr);
-  g.q_out = static_cast<float*>(q->ptr);
-  g.k_out = static_cast<float*>(k->ptr);
-  g.v_out = static_cast<float*>(v->ptr);
-  return vk::launch_linear_wide(rt, g, kLinStore);
-}
-
-int vk_linear_run_qkv_hnd_norm_rope_f32(vk_runtime* rt, const vk_linear* lin,
-                                        const vk_tensor* x, size_t rows, size_t heads,
-                                        size_t head_dim, vk_tensor* q, vk_tensor* k,
-                                        vk_tensor* v, const vk_tensor* q_gamma,
-                                        const vk_tensor* q_beta, const vk_tensor* k_gamma,
-                                        const vk_tensor* k_beta, size_t n_special, size_t gh,
-                                        size_t gw, size_t view_count, int global, float freq,
-                                        float eps) {
-  return vk_linear_run_qkv_hnd_norm_rope_mode_f32(rt, lin, x, rows, heads, head_dim, q, k, v,
-                                                  q_gamma, q_beta, k_gamma, k_beta, n_special,
-                                                  gh, gw, view_count, global, freq, eps,
-                                                  VK_ROPE_DEFAULT);
-}
-
-int vk_linear_run_qkv_hnd_norm_rope_mode_f32(vk_runtime* rt, const vk_linear* lin,
-                                             const vk_tensor* x, size_t rows, size_t heads,
-                                             size_t head_dim, vk_tensor* q, vk_tensor* k,
-                                             vk_tensor* v, const vk_tensor* q_gamma,
-                                             const vk_tensor* q_beta, const vk_tensor* k_gamma,
-                                             const vk_tensor* k_beta, size_t n_special,
-                                             size_t gh, size_t gw, size_t view_count,
-                                             int global, float freq, float eps,
-                                             unsigned rope_mode) {
-  VK_TRY(vk::bind(rt));
-  VK_TRY(vk::check_rope_mode(rope_mode));
-  VK_REQUIRE(lin && x && q && k && v, "null argument");
-  VK_UNSUPPORTED_IF(head_dim != 64, "qkv norm_rope: head_dim=%zu (qualified: 64)", head_dim);
-  VK_REQUIRE(view_count > 0 && gw > 0, "view_count and gw must be > 0");
-  VK_REQUIRE(rows == view_count * (n_special + gh * gw),
-             "qkv norm_rope: rows=%zu, expected view_count*(n_special+gh*gw)=%zu", rows,
-             view_count * (n_special + gh * gw));
-  const bool any = q_gamma || q_beta || k_gamma || k_beta;
-  const bool all = q_gamma && q_beta && k_gamma && k_beta;
-  VK_REQUIRE(!any || all, "q/k norm parameters must be all present or all null");
-  if (all) {
-    for (const vk_tensor* t : {q_gamma, q_beta, k_gamma, k_beta})
-      VK_REQUIRE((t->dtype == VK_F32 || t->dtype == VK_F16) && t->dtype == q_gamma->dtype &&
-                     t->len == head_dim,
-                 "q/k norm parameters must be f32 or f16 vectors of 64 sharing one dtype");
-  }
-  VK_UNSUPPORTED_IF(rows > 0x7fffffffULL, "qkv norm_rope: rows=%zu too large", rows);
-  // Q|K|V projection checks (and nothing to do for zero rows)
-  if (rows == 0) return vk_linear_run_qkv_hnd_f32(rt, lin, x, rows, heads, head_dim, q, k, v);
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_head_layout(lin, x, heads, head_dim));
-  VK_REQUIRE(lin->out_features == 3 * heads * head_dim,
-             "linear_run_qkv_hnd: out_features=%zu, expected 3*heads*head_dim=%zu",
-             lin->out_features, 3 * heads * head_dim);
-  VK_REQUIRE(lin->ls_gamma == nullptr, "linear_run_qkv_hnd: the linear carries a LayerScale");
-  const size_t part = rows * heads * head_dim;
-  for (const vk_tensor* t : {q, k, v})
-    VK_REQUIRE(t->dtype == VK_F32 && t->len == part, "q, k, v must be f32 [rows*heads*64=%zu]",
-               part);
-  VK_REQUIRE(tensors_disjoint(x, q) && tensors_disjoint(x, k) && tensors_disjoint(x, v) &&
-                 tensors_disjoint(q, k) && tensors_disjoint(q, v) && tensors_disjoint(k, v),
-             "linear_run_qkv_hnd: tensors overlap");
-  // the grid's largest coordinate is max(gh, gw) + 1: the table covers it
-  const size_t max_coord = (gh > gw ? gh : gw) + 1;
-  VK_UNSUPPORTED_IF(max_coord > (1u << 22), "patch grid %zux%zu too large", gh, gw);
-  const float* table = nullptr;
-  int table_max = 0;
-  VK_TRY(vk::rope_table(rt, freq, 64, rope_mode, static_cast<int>(max_coord), &table,
-                        &table_max));
-  LinearArgs g = linear_args(lin, x, rows, nullptr);
-  g.q_out = static_cast<float*>(q->ptr);
-  g.k_out = static_cast<float*>(k->ptr);
-  g.v_out = static_cast<float*>(v->ptr);
-  g.qkn_mode = !all ? 3 : (q_gamma->dtype == VK_F16 ? 2 : 1);
-  g.qkn.qg = all ? q_gamma->ptr : nullptr;
-  g.qkn.qb = all ? q_beta->ptr : nullptr;
-  g.qkn.kg = all ? k_gamma->ptr : nullptr;
-  g.qkn.kb = all ? k_beta->ptr : nullptr;
-  g.qkn.table = table;
-  g.qkn.table_max = table_max;
-  g.qkn.n_special = static_cast<uint32_t>(n_special);
-  g.qkn.global = global ? 1u : 0u;
-  g.qkn.tpv = vkd::make_fastdiv(static_cast<uint32_t>(n_special + gh * gw));
-  g.qkn.gw = vkd::make_fastdiv(static_cast<uint32_t>(gw));
-  g.qkn.eps = eps;
-  g.qkn.interleaved = (rope_mode & VK_ROPE_INTERLEAVED) ? 1u : 0u;
-  return vk::launch_linear_wide(rt, g, kLinStore);
-}
-
-static int run_hnd(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd, size_t rows,
-                   size_t heads, size_t head_dim, vk_tensor* out, int epi, const char* what) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && hnd && out, "null argument");
-  VK_TRY(check_linear(lin, hnd, rows));
-  VK_TRY(check_head_layout(lin, hnd, heads, head_dim));
-  VK_REQUIRE(lin->in_features == heads * head_dim, "%s: in_features=%zu, expected heads*64=%zu",
-             what, lin->in_features, heads * head_dim);
-  VK_TRY(check_linear_out(lin, hnd, out, rows, epi == kLinResidual ? "residual" : "out"));
-  if (rows == 0) return VK_OK;
-  LinearArgs g = linear_args(lin, hnd, rows, out);
-  g.a_hnd = 1;
-  return vk::launch_linear_wide(rt, g, epi);
-}
-
-int vk_linear_run_hnd_into_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
-                               size_t rows, size_t heads, size_t head_dim, vk_tensor* out) {
-  return run_hnd(rt, lin, hnd, rows, heads, head_dim, out, kLinStore, "linear_run_hnd_into");
-}
-
-int vk_linear_run_hnd_residual_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* hnd,
-                                   size_t rows, size_t heads, size_t head_dim,
-                                   vk_tensor* residual) {
-  return run_hnd(rt, lin, hnd, rows, heads, head_dim, residual, kLinResidual,
-                 "linear_run_hnd_residual");
-}
 
 int vk_patchify_nchw_f32(vk_runtime* rt, const vk_tensor* img, size_t h, size_t w,
                          size_t patch, size_t channels, vk_tensor** out) {
@@ -1668,73 +870,6 @@ int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t
                       size_t n_register, const vk_tensor* pos_table, vk_tensor* out) {
   return vk_patch_embed_views_u8(rt, img_hwc, 1, h, w, patch, mean, std_, proj, cls, registers,
                                  n_register, pos_table, out);
-}
-
-}  // extern "C"
-
-// ---------------------------------------------------------------------------
-// Allocation-free linear: vk_linear_run_into_f32 with the split-K partial
-// sums in a static device array instead of the runtime's work buffer.
-//
-// `scratch` is a file-scope device array: each device holds its own copy
-// from the library's load until the process ends.  Host code never uses its
-// name as an address (on the host it is a stand-in symbol): the device
-// address is looked up once per device, with that device current, when a
-// runtime is created on it (vk_runtime_create -> vk::noalloc_setup), and
-// only that address is handed to kernels.  Every call on one device shares
-// that device's array; each split writes its whole slice before the sum
-// pass reads it, so nothing needs clearing, but calls that overlap on one
-// device (two runtimes' streams at once) race on it.
-// ---------------------------------------------------------------------------
-constexpr size_t kScratchFloats = size_t{8} << 20;  // 32 MiB per device
-
-static __device__ __align__(256) float scratch[kScratchFloats];
-
-namespace {
-
-constexpr int kMaxDevices = 64;
-
-std::mutex g_scratch_mu;
-float* g_scratch_ptr[kMaxDevices] = {};
-hipError_t g_scratch_err[kMaxDevices] = {};
-bool g_scratch_done[kMaxDevices] = {};
-
-}  // namespace
-
-namespace vk {
-
-void noalloc_setup(int device) {
-  if (device < 0 || device >= kMaxDevices) return;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_done[device]) return;
-  void* p = nullptr;
-  // the caller (vk_runtime_create) made `device` current
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-  g_scratch_err[device] = e;
-  g_scratch_ptr[device] = e == hipSuccess ? static_cast<float*>(p) : nullptr;
-  g_scratch_done[device] = true;
-}
-
-}  // namespace vk
-
-extern "C" {
-
-int vk_linear_run_into_noalloc_f32(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
-                                   size_t rows, vk_tensor* out) {
-  VK_TRY(vk::bind(rt));
-  VK_REQUIRE(lin && x && out, "null argument");
-  VK_TRY(check_linear(lin, x, rows));
-  VK_TRY(check_linear_out(lin, x, out, rows, "out"));
-  float* sp = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    VK_REQUIRE(rt->device < kMaxDevices && g_scratch_done[rt->device],
-               "linear_run_into_noalloc: no scratch address for device %d", rt->device);
-    if (g_scratch_err[rt->device] != hipSuccess)
-      return vk::hip_fail(g_scratch_err[rt->device], "hipGetSymbolAddress(scratch)");
-    sp = g_scratch_ptr[rt->device];
-  }
-  return launch_linear(rt, lin, x, rows, out, kLinStore, sp, kScratchFloats);
 }
 
 }  // extern "C"

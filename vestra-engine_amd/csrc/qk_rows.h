@@ -43,12 +43,12 @@ struct RopeCs {
 };
 template <int NF>
 __device__ __forceinline__ RopeCs rope_cs_slow(const float* __restrict__ table, int table_max,
-                                               int p, int j0) {
+                                               float p, int j0) {
   float cv[4] = {0.f, 0.f, 0.f, 0.f}, sv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < NF; ++u) {
     const float inv_freq = table[static_cast<size_t>(table_max + 1) * 32 + j0 + u];
-    const float angle = static_cast<float>(p) * inv_freq;
+    const float angle = p * inv_freq;
     sincosf(angle, &sv[u], &cv[u]);
   }
   return RopeCs{make_float4(cv[0], cv[1], cv[2], cv[3]), make_float4(sv[0], sv[1], sv[2], sv[3])};
@@ -68,28 +68,42 @@ __device__ __forceinline__ float4 swizzle_xor4(float4 v) {
 // Position (y, x) of token lt of a view (vit_block.rs:841-881): specials
 // (0, 0); patch p at (p / gw + 1, p % gw + 1), or (1, 1) in global layers.
 __device__ __forceinline__ void grid_position(uint32_t lt, uint32_t n_special, uint32_t global,
-                                              const vkd::FastDivU32& gw, int* py, int* px) {
-  *py = 0;
-  *px = 0;
+                                              const vkd::FastDivU32& gw, float* py, float* px) {
+  int y = 0, x = 0;
   if (lt >= n_special) {
     if (global) {
-      *py = 1;
-      *px = 1;
+      y = 1;
+      x = 1;
     } else {
       const uint32_t p = lt - n_special;
       const uint32_t row = vkd::fdiv(p, gw);
-      *py = static_cast<int>(row) + 1;
-      *px = static_cast<int>(p - row * gw.d) + 1;
+      y = static_cast<int>(row) + 1;
+      x = static_cast<int>(p - row * gw.d) + 1;
     }
   }
+  *py = static_cast<float>(y);
+  *px = static_cast<float>(x);
 }
 
-// Position (y, x) of Q/K row r (head-major index inside one tensor).  All
-// index math is 32-bit with multiply-shift division by the shape constants.
+// An f32 device position as the reference's `value as i64` reads it, then
+// as the f32 the angle is computed from: truncated toward zero, NaN to 0,
+// saturated at +-2^63 (the f32 nearest i64::MAX / i64::MIN).
+__device__ __forceinline__ float f32_position(float v) {
+  if (v != v) return 0.0f;
+  return fminf(fmaxf(truncf(v), -9223372036854775808.0f), 9223372036854775808.0f);
+}
+
+// Position (y, x) of Q/K row r (head-major index inside one tensor), as the
+// f32 value the rotation angle is computed from: an integer position p
+// gives (float)p exactly as the CPU kernel converts its i64 positions, so a
+// coordinate of any i64 value (2^32 + 5 included) takes the rotation of
+// that f32 value -- through the table when it is an entry of it, through
+// sincosf otherwise.  All index math is 32-bit with multiply-shift division
+// by the shape constants.
 template <int POS>
 __device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
-                                                const void* __restrict__ pos_yx, int* py,
-                                                int* px) {
+                                                const void* __restrict__ pos_yx, float* py,
+                                                float* px) {
   uint32_t t;   // index in the position sequence
   uint32_t lt;  // index inside its view
   if (sh.layout == VK_QK_HEADS_OUTER) {
@@ -100,21 +114,19 @@ __device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
     lt = vkd::fmod_(r, sh.tpv);
     t = v * sh.tpv.d + lt;
   }
-  *py = 0;
-  *px = 0;
   if (POS == kPosExplicit) {
     // the reference's f32 device encoding, truncated like `value as i64`
     const float* p = static_cast<const float*>(pos_yx);
-    *py = static_cast<int>(p[2 * static_cast<size_t>(t)]);
-    *px = static_cast<int>(p[2 * static_cast<size_t>(t) + 1]);
+    *py = f32_position(p[2 * static_cast<size_t>(t)]);
+    *px = f32_position(p[2 * static_cast<size_t>(t) + 1]);
   } else if (POS == kPosExplicitI32) {
     const int2 p = static_cast<const int2*>(pos_yx)[t];
-    *py = p.x;
-    *px = p.y;
+    *py = static_cast<float>(p.x);
+    *px = static_cast<float>(p.y);
   } else if (POS == kPosExplicitI64) {
     const long long* p = static_cast<const long long*>(pos_yx);
-    *py = static_cast<int>(p[2 * static_cast<size_t>(t)]);
-    *px = static_cast<int>(p[2 * static_cast<size_t>(t) + 1]);
+    *py = static_cast<float>(p[2 * static_cast<size_t>(t)]);
+    *px = static_cast<float>(p[2 * static_cast<size_t>(t) + 1]);
   } else {
     grid_position(lt, sh.n_special, sh.global, sh.gw, py, px);
   }
@@ -132,8 +144,8 @@ struct QkRowOperands {
 
 template <typename PT, bool HAS_NORM, int POS, int PAIR>
 __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __restrict__ g,
-                                                         const PT* __restrict__ b, int py,
-                                                         int px,
+                                                         const PT* __restrict__ b, float py,
+                                                         float px,
                                                          const float* __restrict__ table,
                                                          int table_max) {
   QkRowOperands o;
@@ -142,9 +154,12 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
     o.b = vkd::Param<PT>::load4(b, l);
   }
   // lanes 0-7 rotate by the row coordinate, lanes 8-15 by the column
-  const int coord = (l < 8) ? py : px;
-  const bool in_table = POS == kPosGrid || (coord >= 0 && coord <= table_max);
-  const float* e = table + static_cast<size_t>(in_table ? coord : 0) * 32;
+  // the coordinate is an integral f32: an entry of the table when it lies
+  // in 0..table_max (exactly representable, so the comparison is exact)
+  const float coord = (l < 8) ? py : px;
+  const bool in_table =
+      POS == kPosGrid || (coord >= 0.0f && coord <= static_cast<float>(table_max));
+  const float* e = table + static_cast<size_t>(in_table ? static_cast<int>(coord) : 0) * 32;
   if (PAIR == kRotateHalf) {
     const int j0 = (l & 3) * 4;  // frequencies j0..j0+3
     if (in_table) {
@@ -177,10 +192,26 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
 // hold the y half (elements 0..31), lanes 8-15 the x half.  Every rotated
 // pair (a, b) with angle frequency j becomes (a*cos - b*sin, b*cos + a*sin),
 // each product rounded, then the sum.
-template <bool HAS_NORM, int PAIR>
+// SEQ: the mean and variance summed in the scalar reference's order (the
+// runtime's VK_LN_ORDER_SEQUENTIAL) and 1/sqrtf(var + eps) correctly
+// rounded: the bits of the CPU's LayerNorm of the row.
+template <bool HAS_NORM, int PAIR, bool SEQ = false>
 __device__ __forceinline__ float4 qk_row_apply(float4 v, int l, const QkRowOperands& op,
                                                float eps) {
-  if (HAS_NORM) {
+  if (HAS_NORM && SEQ) {
+    const float mean = vkd::row16_seq_sum(v) / 64.0f;
+    float4 d;
+    d.x = v.x - mean; d.x = d.x * d.x;
+    d.y = v.y - mean; d.y = d.y * d.y;
+    d.z = v.z - mean; d.z = d.z * d.z;
+    d.w = v.w - mean; d.w = d.w * d.w;
+    const float var = vkd::row16_seq_sum(d) / 64.0f;
+    const float inv = 1.0f / sqrtf(var + eps);
+    v.x = (v.x - mean) * inv * op.g.x + op.b.x;
+    v.y = (v.y - mean) * inv * op.g.y + op.b.y;
+    v.z = (v.z - mean) * inv * op.g.z + op.b.z;
+    v.w = (v.w - mean) * inv * op.g.w + op.b.w;
+  } else if (HAS_NORM) {
     float s = v.x;
     s += v.y;
     s += v.z;
@@ -233,14 +264,14 @@ __device__ __forceinline__ float4 qk_row_apply(float4 v, int l, const QkRowOpera
 }
 
 // Both stages for one row (the QKV projection's epilogue).
-template <typename PT, bool HAS_NORM, int POS, int PAIR>
+template <typename PT, bool HAS_NORM, int POS, int PAIR, bool SEQ = false>
 __device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
-                                                   const PT* __restrict__ b, int py, int px,
+                                                   const PT* __restrict__ b, float py, float px,
                                                    const float* __restrict__ table,
                                                    int table_max, float eps) {
   const QkRowOperands op =
       qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, g, b, py, px, table, table_max);
-  return qk_row_apply<HAS_NORM, PAIR>(v, l, op, eps);
+  return qk_row_apply<HAS_NORM, PAIR, SEQ>(v, l, op, eps);
 }
 
 }  // namespace vkq

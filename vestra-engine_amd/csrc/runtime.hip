@@ -327,6 +327,20 @@ void* vk_runtime_stream(vk_runtime* rt) { return rt ? static_cast<void*>(rt->str
 
 int vk_runtime_cu_count(vk_runtime* rt) { return rt ? rt->cu_count : 0; }
 
+int vk_runtime_set_layernorm_order(vk_runtime* rt, int order) {
+  VK_REQUIRE(rt != nullptr, "null runtime");
+  VK_REQUIRE(!rt->destroyed, "runtime was destroyed");
+  VK_REQUIRE(order == VK_LN_ORDER_TREE || order == VK_LN_ORDER_SEQUENTIAL,
+             "unknown LayerNorm order %d", order);
+  rt->ln_order = order;
+  return VK_OK;
+}
+
+int vk_runtime_layernorm_order(vk_runtime* rt) {
+  VK_REQUIRE(rt != nullptr, "null runtime");
+  return rt->ln_order;
+}
+
 int vk_tensor_alloc(vk_runtime* rt, vk_dtype dtype, size_t len, vk_tensor** out) {
   return new_tensor(rt, dtype, len, out);
 }

@@ -35,6 +35,8 @@ VK_ROPE_ROTATE_HALF, VK_ROPE_INTERLEAVED = 0, 1
 VK_ROPE_EXP_HALF, VK_ROPE_EXP_HEAD = 0, 2
 VK_ROPE_DEFAULT = 0
 VK_QK_HEADS_OUTER, VK_QK_VIEWS_OUTER = 0, 1
+# LayerNorm summation order of a runtime (vk_runtime_set_layernorm_order)
+VK_LN_ORDER_TREE, VK_LN_ORDER_SEQUENTIAL = 0, 1
 VK_RESIZE_BILINEAR, VK_RESIZE_CUBIC, VK_RESIZE_AREA = 0, 1, 2
 
 VK_BLOCK_FUSE_LS_LN = 1
@@ -109,6 +111,8 @@ _SIGS = {
     "vk_runtime_synchronize": ([_vp], _i),
     "vk_runtime_stream": ([_vp], _vp),
     "vk_runtime_cu_count": ([_vp], _i),
+    "vk_runtime_set_layernorm_order": ([_vp, _i], _i),
+    "vk_runtime_layernorm_order": ([_vp], _i),
     "vk_tensor_alloc": ([_vp, _i, _sz, _pp], _i),
     "vk_tensor_wrap": ([_vp, _i, _vp, _sz, _pp], _i),
     "vk_tensor_destroy": ([_vp], _i),
@@ -418,6 +422,19 @@ class Runtime:
 
     def cu_count(self) -> int:
         return int(lib.vk_runtime_cu_count(self.handle))
+
+    def set_layernorm_order(self, order: int) -> None:
+        """Summation order of every LayerNorm enqueued from now on:
+        VK_LN_ORDER_TREE (default) or VK_LN_ORDER_SEQUENTIAL, the CPU
+        kernel's left-to-right sums and its bits (layernorm_f32_cpu_order,
+        vit_block.rs:528-537)."""
+        _check(lib.vk_runtime_set_layernorm_order(self.handle, order))
+
+    def layernorm_order(self) -> int:
+        r = int(lib.vk_runtime_layernorm_order(self.handle))
+        if r < 0:
+            _check(r)
+        return r
 
     def close(self) -> None:
         if self.handle:
