@@ -292,8 +292,9 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
                         2 * rows * D * 4),
     }
     table = {}
+    wanted = (only,) if isinstance(only, str) else only
     for name, (fn, nbytes) in ops.items():
-        if only and name != only:
+        if wanted and name not in wanted:
             continue
         for _ in range(3):
             fn()
@@ -309,6 +310,22 @@ def per_op_table(rt, rng, rows, rotate, iters, only=None):
 
 
 MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def sequential_order_table(rng, rows, iters):
+    """The LayerNorm-type operations of the per-operation table on a runtime
+    in the sequential LayerNorm order (VK_LN_ORDER_SEQUENTIAL: the CPU's
+    left-to-right sums and its bits), same shape and rotating buffers; the
+    cost of the reference-order bits next to the default tree order."""
+    import vestra_hip as vh
+    srt = vh.Runtime(0)
+    srt.set_layernorm_order(vh.VK_LN_ORDER_SEQUENTIAL)
+    try:
+        return per_op_table(srt, rng, rows, rotate=ROTATE_SETS, iters=iters,
+                            only=("layernorm", "qk_norm_rope", "layerscale_residual_layernorm"))
+    finally:
+        srt.synchronize()
+        srt.close()
 
 
 def dispatch_overhead(rt, launches=100):
@@ -1051,6 +1068,7 @@ def main():
 
     log("per-operation table")
     ops12 = per_op_table(rt, rng, model.rows, rotate=ROTATE_SETS, iters=args.op_iters)
+    ops12_seq = sequential_order_table(rng, model.rows, args.op_iters)
     ops1 = per_op_table(rt, rng, TPV, rotate=1, iters=args.op_iters)
     # the single-image shape again with its inputs in HBM: 64 rotating sets
     # (>= 340 MB per operation) cycle past the 256 MB Infinity Cache
@@ -1101,6 +1119,10 @@ def main():
         "ops_12view": ops12,
         "ops_12view_mode": (f"cold HBM: {ROTATE_SETS} rotating buffer sets, every operation's "
                             f"working set >= 512 MB, beyond the 256 MB Infinity Cache"),
+        "ops_12view_sequential_ln_order": ops12_seq,
+        "ops_12view_sequential_ln_order_mode": ("the same 12-view shape and buffers on a runtime "
+                                                "in the sequential LayerNorm order (the CPU's "
+                                                "sums and bits)"),
         "ops_single_image": ops1,
         "ops_single_image_mode": ("warm (effective GB/s): one buffer set of 5-21 MB, "
                                   "cache-resident between launches"),

@@ -20,21 +20,27 @@
 //
 // Row statistics and the per-element formula are vkd::row_mean_inv and
 // vkd::ln_apply4, shared with the block LayerNorm: a captured or handed-off
-// row has the bits vk_layernorm_into_f32 gives the same row.
+// row has the bits vk_layernorm_into_f32 gives the same row.  In the
+// runtime's sequential LayerNorm order the statistics come from the
+// sequential-order kernel of the block LayerNorm instead (into the work
+// buffer, then read by the same passes), with the same consequence.
 #include "common.h"
 
 namespace {
 
 using vkd::Param;
 
-template <int NV, typename PT, bool EXACT, bool CAT>
+// STATS: the row's mean and 1/std come from stats[r] (the sequential-order
+// statistics of patch row r), not from the wave's own reduction.
+template <int NV, typename PT, bool EXACT, bool CAT, bool STATS>
 __global__ __launch_bounds__(64) void capture_rows(const float* __restrict__ local_x,
                                                    const float* __restrict__ x,
                                                    const PT* __restrict__ gamma,
                                                    const PT* __restrict__ beta,
                                                    float* __restrict__ feat,
                                                    float* __restrict__ cam, int n_patch, int n,
-                                                   int n_special, int views, int D, float eps) {
+                                                   int n_special, int views, int D, float eps,
+                                                   const float2* __restrict__ stats) {
   const int lane = threadIdx.x;
   const int r = blockIdx.x;
   const int nvec = D >> 2;
@@ -66,7 +72,13 @@ __global__ __launch_bounds__(64) void capture_rows(const float* __restrict__ loc
     vv[i] = (EXACT || c < nvec) ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   float mean, inv;
-  vkd::row_mean_inv<NV, EXACT>(vv, lane, D, eps, &mean, &inv);
+  if (STATS) {
+    const float2 ms = stats[r];
+    mean = ms.x;
+    inv = ms.y;
+  } else {
+    vkd::row_mean_inv<NV, EXACT>(vv, lane, D, eps, &mean, &inv);
+  }
   float4* ln_dst = reinterpret_cast<float4*>(dst + (CAT ? D : 0));
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -183,12 +195,22 @@ int launch_capture(vk_runtime* rt, int nv, bool exact, const float* lx, const fl
   const dim3 grid(static_cast<unsigned>(views * n_patch + views)), block(64);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
+  if (rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+    // the patch rows' statistics in the CPU's order first, into the work buffer
+    VK_TRY(vk::ensure_work(rt, 2 * static_cast<size_t>(views) * n_patch, "capture"));
+    VK_TRY(vk::layernorm_stats_sequential(rt, x, rt->work, views * n_patch, D, eps, n_patch, n,
+                                          ns));
+    const float2* st = reinterpret_cast<const float2*>(rt->work);
+    hipLaunchKernelGGL((capture_rows<12, PT, false, CAT, true>), grid, block, 0, rt->stream, lx,
+                       x, G, B, feat, cam, n_patch, n, ns, views, D, eps, st);
+    return vk::check_launch("capture_rows");
+  }
 #define VK_CAP_CASE(N)                                                                         \
   case N:                                                                                      \
     if (exact)                                                                                 \
-      hipLaunchKernelGGL((capture_rows<N, PT, true, CAT>), grid, block, 0, rt->stream, lx, x, G, B, feat, cam, n_patch, n, ns, views, D, eps); \
+      hipLaunchKernelGGL((capture_rows<N, PT, true, CAT, false>), grid, block, 0, rt->stream, lx, x, G, B, feat, cam, n_patch, n, ns, views, D, eps, nullptr); \
     else                                                                                       \
-      hipLaunchKernelGGL((capture_rows<N, PT, false, CAT>), grid, block, 0, rt->stream, lx, x, G, B, feat, cam, n_patch, n, ns, views, D, eps); \
+      hipLaunchKernelGGL((capture_rows<N, PT, false, CAT, false>), grid, block, 0, rt->stream, lx, x, G, B, feat, cam, n_patch, n, ns, views, D, eps, nullptr); \
     break;
   switch (nv) {
     VK_CAP_CASE(1) VK_CAP_CASE(2) VK_CAP_CASE(3) VK_CAP_CASE(4) VK_CAP_CASE(6) VK_CAP_CASE(8)
@@ -207,6 +229,10 @@ int launch_chw(vk_runtime* rt, int nv, bool exact, const float* tok, const void*
   if (NORM) {
     VK_TRY(vk::ensure_work(rt, 2 * static_cast<size_t>(n_tok), "token_to_chw"));
     float* st = rt->work;
+    if (rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+      VK_TRY(vk::layernorm_stats_sequential(rt, tok, st, n_tok, C, eps, 0, 0, 0));
+      stats = st;
+    }
     const dim3 sgrid(static_cast<unsigned>((n_tok + 3) / 4)), sblock(256);
 #define VK_STAT_CASE(N)                                                                        \
   case N:                                                                                      \
@@ -215,15 +241,16 @@ int launch_chw(vk_runtime* rt, int nv, bool exact, const float* tok, const void*
     else                                                                                       \
       hipLaunchKernelGGL((chw_row_stats<N, false>), sgrid, sblock, 0, rt->stream, tok, st, n_tok, C, eps); \
     break;
-    switch (nv) {
-      VK_STAT_CASE(1) VK_STAT_CASE(2) VK_STAT_CASE(3) VK_STAT_CASE(4) VK_STAT_CASE(6)
-      VK_STAT_CASE(8) VK_STAT_CASE(12)
-      default:
-        return vk::set_error(VK_ERR_UNSUPPORTED, "token_to_chw: no instance for c=%d", C);
+    if (!stats) {
+      switch (nv) {
+        VK_STAT_CASE(1) VK_STAT_CASE(2) VK_STAT_CASE(3) VK_STAT_CASE(4) VK_STAT_CASE(6)
+        VK_STAT_CASE(8) VK_STAT_CASE(12)
+        default:
+          return vk::set_error(VK_ERR_UNSUPPORTED, "token_to_chw: no instance for c=%d", C);
+      }
+      VK_TRY(vk::check_launch("chw_row_stats"));
+      stats = st;
     }
-#undef VK_STAT_CASE
-    VK_TRY(vk::check_launch("chw_row_stats"));
-    stats = st;
   }
   const dim3 grid(static_cast<unsigned>((n_tok + kChwTok - 1) / kChwTok),
                   static_cast<unsigned>((C + kChwCh - 1) / kChwCh));

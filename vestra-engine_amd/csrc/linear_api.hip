@@ -267,15 +267,18 @@ int residual_layernorm(vk_runtime* rt, const vk_linear* lin, const vk_tensor* x,
                "linear_residual_layernorm: tensors must be 16-byte aligned");
   if (rows == 0) return VK_OK;
   const bool wide = lin->in_features % 4 == 0 && reinterpret_cast<uintptr_t>(x->ptr) % 16 == 0;
-  if (!wide) {
-    VK_TRY(launch_linear(rt, lin, x, rows, residual, kLinResidual));
+  LinearArgs g = linear_args(lin, x, rows, residual);
+  g.a_hnd = heads > 0 ? 1 : 0;
+  // The sum pass's LayerNorm reduces in the tree order; the sequential order
+  // (and an input the wide kernel cannot read) takes the two calls.
+  if (!wide || rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+    VK_TRY(wide ? vk::launch_linear_wide(rt, g, kLinResidual)
+                : launch_linear(rt, lin, x, rows, residual, kLinResidual));
     return vk::layernorm_raw(rt, static_cast<const float*>(residual->ptr),
                              static_cast<float*>(ln_out->ptr), gamma->ptr, beta->ptr,
                              gamma->dtype == VK_F16, static_cast<int>(rows),
                              static_cast<int>(n), eps);
   }
-  LinearArgs g = linear_args(lin, x, rows, residual);
-  g.a_hnd = heads > 0 ? 1 : 0;
   g.ln_gamma = gamma->ptr;
   g.ln_beta = beta->ptr;
   g.ln_f16 = gamma->dtype == VK_F16 ? 1 : 0;
@@ -452,6 +455,15 @@ int vk_linear_run_qkv_hnd_norm_rope_mode_f32(vk_runtime* rt, const vk_linear* li
   g.q_out = static_cast<float*>(q->ptr);
   g.k_out = static_cast<float*>(k->ptr);
   g.v_out = static_cast<float*>(v->ptr);
+  if (all && rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+    // the epilogue's Q/K LayerNorm reduces in the tree order: the
+    // sequential order stores Q, K, V and runs the Q/K pass over them (rows
+    // in the same head-major order, the same grid positions)
+    VK_TRY(vk::launch_linear_wide(rt, g, kLinStore));
+    return vk_qk_norm_rope_grid_mode_f32(rt, q, k, q_gamma, q_beta, k_gamma, k_beta, heads,
+                                         head_dim, n_special, gh, gw, view_count, global,
+                                         VK_QK_HEADS_OUTER, freq, eps, rope_mode);
+  }
   g.qkn_mode = !all ? 3 : (q_gamma->dtype == VK_F16 ? 2 : 1);
   g.qkn.qg = all ? q_gamma->ptr : nullptr;
   g.qkn.qb = all ? q_beta->ptr : nullptr;

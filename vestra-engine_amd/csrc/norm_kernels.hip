@@ -17,8 +17,11 @@
 //    covered by one launch; each 16-lane group streams two rows (both loads
 //    in flight before the first reduction).
 //  * Arithmetic per element follows the scalar reference order with every
-//    product and sum rounded (built with -ffp-contract=off); only the order
-//    of the mean/variance reductions differs (wave tree vs sequential).
+//    product and sum rounded (built with -ffp-contract=off); by default only
+//    the order of the mean/variance reductions differs (wave tree vs
+//    sequential).  The runtime's sequential LayerNorm order replaces the
+//    trees by the scalar order's chains (seq_layernorm_rows; the Q/K rows
+//    through vkd::row16_seq_sum) and gives the CPU's bits.
 #include <algorithm>
 
 #include "common.h"
@@ -176,6 +179,21 @@ struct SeqLnArgs {
   vkd::FastDivU32 fnp;
 };
 
+// ((0 + e0) + e1) + ... over the n4 float4 of one LDS row: one chain of
+// dependent adds in element order (eight LDS reads in flight per step).
+__device__ __forceinline__ float seq_row_sum(const float4* rp, int n4) {
+  float s = 0.0f;
+#pragma unroll 8
+  for (int c = 0; c < n4; ++c) {
+    const float4 w = rp[c];
+    s += w.x;
+    s += w.y;
+    s += w.z;
+    s += w.w;
+  }
+  return s;
+}
+
 template <int NV, typename PT, bool LSRES, bool HAS_LS, bool CAM>
 __global__ __launch_bounds__(kSeqThreads) void seq_layernorm_rows(SeqLnArgs a) {
   // rpw rows of c4 + 1 float4 (the pad puts the 16 chain lanes' reads on
@@ -189,86 +207,72 @@ __global__ __launch_bounds__(kSeqThreads) void seq_layernorm_rows(SeqLnArgs a) {
   const int nr = min(a.rpw, a.rows - r0);
   const int slots = nr * c4;
   float4 v[NV];
-  size_t off[NV];
-  // load (clamped to a valid slot: no load waits behind a guard)
+  // every load first (clamped to a valid slot: no load waits behind a
+  // guard or a store), then the arithmetic, the stores and the LDS copy
+  float4 b[LSRES ? NV : 1];
+  int lrow[NV], col[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int e = tid + kSeqThreads * i;
     const int ec = e < slots ? e : slots - 1;
-    const int lr = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(ec), a.c4));
-    const int c = ec - lr * c4;
-    const int r = r0 + lr;
+    lrow[i] = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(ec), a.c4));
+    col[i] = ec - lrow[i] * c4;
+    const int r = r0 + lrow[i];
     size_t row = static_cast<size_t>(r);
     if (!LSRES && a.np) {
       const int vw = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(r), a.fnp));
       row = static_cast<size_t>(vw) * a.n + a.ns + (r - vw * a.np);
     }
-    off[i] = row * a.cols + 4 * static_cast<size_t>(c);
-    v[i] = vkd::ld_stream(reinterpret_cast<const float4*>(a.x + off[i]));
+    const size_t off = row * a.cols + 4 * static_cast<size_t>(col[i]);
+    v[i] = vkd::ld_stream(reinterpret_cast<const float4*>(a.x + off));
+    if (LSRES) b[i] = vkd::ld_stream(reinterpret_cast<const float4*>(a.yb + off));
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + kSeqThreads * i;
     if (LSRES) {
-      const float4 b = vkd::ld_stream(reinterpret_cast<const float4*>(a.yb + off[i]));
+      const int c = col[i], r = r0 + lrow[i];
       if (HAS_LS) {
         const float4 g = Param<PT>::load4(static_cast<const PT*>(a.ls), c);
         float t;
-        t = b.x * g.x; v[i].x = v[i].x + t;
-        t = b.y * g.y; v[i].y = v[i].y + t;
-        t = b.z * g.z; v[i].z = v[i].z + t;
-        t = b.w * g.w; v[i].w = v[i].w + t;
+        t = b[i].x * g.x; v[i].x = v[i].x + t;
+        t = b[i].y * g.y; v[i].y = v[i].y + t;
+        t = b[i].z * g.z; v[i].z = v[i].z + t;
+        t = b[i].w * g.w; v[i].w = v[i].w + t;
       } else {
-        v[i].x = v[i].x + b.x;
-        v[i].y = v[i].y + b.y;
-        v[i].z = v[i].z + b.z;
-        v[i].w = v[i].w + b.w;
+        v[i].x = v[i].x + b[i].x;
+        v[i].y = v[i].y + b[i].y;
+        v[i].z = v[i].z + b[i].z;
+        v[i].w = v[i].w + b[i].w;
       }
       if (CAM && r % a.tpv == 0)
         v[i] = reinterpret_cast<const float4*>(a.cam + (r >= a.tpv ? a.cols : 0))[c];
-      if (e < slots) vkd::st_stream(reinterpret_cast<float4*>(a.x + off[i]), v[i]);
+      if (e < slots)
+        vkd::st_stream(reinterpret_cast<float4*>(a.x + static_cast<size_t>(r) * a.cols + 4 * c),
+                       v[i]);
     }
-    if (e < slots) rows_lds[lr * pitch4 + c] = v[i];
+    if (e < slots) rows_lds[lrow[i] * pitch4 + col[i]] = v[i];
   }
   __syncthreads();
-  if (tid < nr) {
-    const float4* rp = rows_lds + tid * pitch4;
-    float s = 0.0f;
-#pragma unroll 8
-    for (int c = 0; c < c4; ++c) {
-      const float4 w = rp[c];
-      s += w.x;
-      s += w.y;
-      s += w.z;
-      s += w.w;
-    }
-    st[tid].x = s / static_cast<float>(a.cols);
-  }
+  if (tid < nr) st[tid].x = seq_row_sum(rows_lds + tid * pitch4, c4) / static_cast<float>(a.cols);
   __syncthreads();
   // squared deviations, each rounded, in place of the values
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int e = tid + kSeqThreads * i;
     if (e < slots) {
-      const int lr = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(e), a.c4));
-      const float m = st[lr].x;
+      const float m = st[lrow[i]].x;
       float4 d;
       d.x = v[i].x - m; d.x = d.x * d.x;
       d.y = v[i].y - m; d.y = d.y * d.y;
       d.z = v[i].z - m; d.z = d.z * d.z;
       d.w = v[i].w - m; d.w = d.w * d.w;
-      rows_lds[lr * pitch4 + (e - lr * c4)] = d;
+      rows_lds[lrow[i] * pitch4 + col[i]] = d;
     }
   }
   __syncthreads();
   if (tid < nr) {
-    const float4* rp = rows_lds + tid * pitch4;
-    float q = 0.0f;
-#pragma unroll 8
-    for (int c = 0; c < c4; ++c) {
-      const float4 w = rp[c];
-      q += w.x;
-      q += w.y;
-      q += w.z;
-      q += w.w;
-    }
-    const float var = q / static_cast<float>(a.cols);
+    const float var = seq_row_sum(rows_lds + tid * pitch4, c4) / static_cast<float>(a.cols);
     const float inv = 1.0f / sqrtf(var + a.eps);
     st[tid].y = inv;
     if (a.stats) a.stats[r0 + tid] = make_float2(st[tid].x, inv);
@@ -279,13 +283,13 @@ __global__ __launch_bounds__(kSeqThreads) void seq_layernorm_rows(SeqLnArgs a) {
   for (int i = 0; i < NV; ++i) {
     const int e = tid + kSeqThreads * i;
     if (e < slots) {
-      const int lr = static_cast<int>(vkd::fdiv(static_cast<uint32_t>(e), a.c4));
-      const int c = e - lr * c4;
-      const float2 ms = st[lr];
-      vkd::st_stream(reinterpret_cast<float4*>(a.out + off[i]),
+      const float2 ms = st[lrow[i]];
+      // the output forms keep the stored row order (no row map)
+      const size_t off = static_cast<size_t>(r0 + lrow[i]) * a.cols + 4 * col[i];
+      vkd::st_stream(reinterpret_cast<float4*>(a.out + off),
                      vkd::ln_apply4(v[i], ms.x, ms.y,
-                                    Param<PT>::load4(static_cast<const PT*>(a.gamma), c),
-                                    Param<PT>::load4(static_cast<const PT*>(a.beta), c)));
+                                    Param<PT>::load4(static_cast<const PT*>(a.gamma), col[i]),
+                                    Param<PT>::load4(static_cast<const PT*>(a.beta), col[i])));
     }
   }
 }
@@ -542,18 +546,20 @@ int launch_qk(vk_runtime* rt, float* q, float* k, const void* qg, const void* qb
   const long long total = static_cast<long long>(sh.tensors) * sh.rows_per_tensor;
   const long long groups = (total + kQkRowsPerGroup - 1) / kQkRowsPerGroup;
   const long long blocks = (groups + kQkThreads / 16 - 1) / (kQkThreads / 16);
-  if (HAS_NORM && rt->ln_order == VK_LN_ORDER_SEQUENTIAL)
-    hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR, true>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q,
-                       k, static_cast<const PT*>(qg), static_cast<const PT*>(qb),
-                       static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh,
-                       eps);
-  else
-    hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q,
-                       k, static_cast<const PT*>(qg), static_cast<const PT*>(qb),
-                       static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh,
-                       eps);
+  if constexpr (HAS_NORM) {
+    if (rt->ln_order == VK_LN_ORDER_SEQUENTIAL) {
+      hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR, true>),
+                         dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q,
+                         k, static_cast<const PT*>(qg), static_cast<const PT*>(qb),
+                         static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh,
+                         eps);
+      return vk::check_launch("qk_norm_rope_rows");
+    }
+  }
+  hipLaunchKernelGGL((qk_norm_rope_rows<PT, HAS_NORM, POS, PAIR>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kQkThreads), 0, rt->stream, q, k,
+                     static_cast<const PT*>(qg), static_cast<const PT*>(qb),
+                     static_cast<const PT*>(kg), static_cast<const PT*>(kb), pos, table, sh, eps);
   return vk::check_launch("qk_norm_rope_rows");
 }
 
