@@ -387,35 +387,6 @@ __device__ __forceinline__ void row_mean_inv(const float4 (&v)[NV], int lane, in
   *inv_out = 1.0f / sqrtf(var + eps);
 }
 
-// Broadcast of lane SRC of every 16-lane DPP row to the whole row
-// (row_newbcast, gfx90a and later).
-template <int SRC>
-__device__ __forceinline__ float row_bcast(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + SRC, 0xF, 0xF, false));
-}
-
-template <int SRC>
-__device__ __forceinline__ void row16_seq_accum(float& s, const float4& v) {
-  if constexpr (SRC < 16) {
-    s += row_bcast<SRC>(v.x);
-    s += row_bcast<SRC>(v.y);
-    s += row_bcast<SRC>(v.z);
-    s += row_bcast<SRC>(v.w);
-    row16_seq_accum<SRC + 1>(s, v);
-  }
-}
-
-// Sum of the 64 values of a 16-lane DPP row (lane l holding elements
-// 4l..4l+3 in v) in the scalar reference's order,
-// (((0 + e0) + e1) + e2) + ... + e63: every lane of the row runs the whole
-// chain on broadcasts of each lane in turn, so all 16 hold the same bits.
-__device__ __forceinline__ float row16_seq_sum(float4 v) {
-  float s = 0.0f;
-  row16_seq_accum<0>(s, v);
-  return s;
-}
-
 // (v - mean) * inv * gamma + beta, each step rounded: the per-element
 // LayerNorm output of the scalar reference order.
 __device__ __forceinline__ float4 ln_apply4(float4 v, float mean, float inv, float4 g, float4 b) {

@@ -21,7 +21,7 @@
 //    the order of the mean/variance reductions differs (wave tree vs
 //    sequential).  The runtime's sequential LayerNorm order replaces the
 //    trees by the scalar order's chains (seq_layernorm_rows; the Q/K rows
-//    through vkd::row16_seq_sum) and gives the CPU's bits.
+//    through qk_apply_rows) and gives the CPU's bits.
 #include <algorithm>
 
 #include "common.h"
@@ -311,6 +311,74 @@ using namespace vkq;
 constexpr int kQkRowsPerGroup = VK_QK_ROWS_PER_GROUP;
 constexpr int kQkThreads = 256;  // threads per workgroup: kQkThreads / 16 row groups
 
+// The rows of every 16-lane group in the sequential LayerNorm order
+// (SEQ): the group's rows go to LDS (row pitch 17 float4, so the chain lanes
+// of a wave read distinct 4-bank groups), lane j of the group walks row j's
+// 64 values left to right for the sum, every lane writes its rounded
+// squared deviations back, lane j walks those for the variance, and every
+// lane then normalises with 1/sqrtf(var + eps) and rotates: the bits of the
+// CPU's LayerNorm and rotation of each row.  One chain lane per row issues
+// a fraction of the VALU work of a chain every lane runs redundantly.
+template <int R, bool HAS_NORM, int PAIR, bool SEQ>
+__device__ __forceinline__ void qk_apply_rows(float4 (&v)[R], int l, const QkRowOperands (&op)[R],
+                                              float eps) {
+  if constexpr (HAS_NORM && SEQ) {
+    __shared__ float4 rows[kQkThreads / 16 * R * 17];
+    __shared__ float stat[kQkThreads / 16 * R];
+    const int grp = threadIdx.x >> 4;
+    float4* gr = rows + grp * R * 17;
+#pragma unroll
+    for (int j = 0; j < R; ++j) gr[j * 17 + l] = v[j];
+    __syncthreads();
+    if (l < R) {
+      const float4* rp = gr + l * 17;
+      float s = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float4 w = rp[c];
+        s += w.x;
+        s += w.y;
+        s += w.z;
+        s += w.w;
+      }
+      stat[grp * R + l] = s / 64.0f;
+    }
+    __syncthreads();
+    float mean[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      mean[j] = stat[grp * R + j];
+      float4 d;
+      d.x = v[j].x - mean[j]; d.x = d.x * d.x;
+      d.y = v[j].y - mean[j]; d.y = d.y * d.y;
+      d.z = v[j].z - mean[j]; d.z = d.z * d.z;
+      d.w = v[j].w - mean[j]; d.w = d.w * d.w;
+      gr[j * 17 + l] = d;
+    }
+    __syncthreads();
+    if (l < R) {
+      const float4* rp = gr + l * 17;
+      float q = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float4 w = rp[c];
+        q += w.x;
+        q += w.y;
+        q += w.z;
+        q += w.w;
+      }
+      stat[grp * R + l] = 1.0f / sqrtf(q / 64.0f + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      v[j] = qk_row_rope<PAIR>(qk_norm_apply(v[j], mean[j], stat[grp * R + j], op[j]), l, op[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < R; ++j) v[j] = qk_row_apply<HAS_NORM, PAIR>(v[j], l, op[j], eps);
+  }
+}
+
 template <typename PT, bool HAS_NORM, int POS, int PAIR, bool SEQ = false>
 __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
     float* __restrict__ q, float* __restrict__ k, const PT* __restrict__ qg,
@@ -346,9 +414,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < kQkRowsPerGroup; ++j)
-      v[j] = qk_row_apply<HAS_NORM, PAIR, SEQ>(v[j], l, op[j], eps);
+    qk_apply_rows<kQkRowsPerGroup, HAS_NORM, PAIR, SEQ>(v, l, op, eps);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       if (grp * NP + p < sh.rows_per_tensor) {
@@ -373,8 +439,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
                                                      table, sh.table_max);
   }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < kQkRowsPerGroup; ++j) v[j] = qk_row_apply<HAS_NORM, PAIR, SEQ>(v[j], l, op[j], eps);
+  qk_apply_rows<kQkRowsPerGroup, HAS_NORM, PAIR, SEQ>(v, l, op, eps);
 #pragma unroll
   for (int j = 0; j < kQkRowsPerGroup; ++j) {
     const uint32_t gr = grp * kQkRowsPerGroup + j;

@@ -187,52 +187,24 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
   return o;
 }
 
-// LayerNorm of one 64-wide row held as one float4 per lane of a 16-lane DPP
-// row, then its 2D rotation, with the operands of qk_row_operands.  Lanes 0-7
-// hold the y half (elements 0..31), lanes 8-15 the x half.  Every rotated
-// pair (a, b) with angle frequency j becomes (a*cos - b*sin, b*cos + a*sin),
+// (v - mean) * inv * gamma + beta for the lane's four elements, each step
+// rounded.
+__device__ __forceinline__ float4 qk_norm_apply(float4 v, float mean, float inv,
+                                                const QkRowOperands& op) {
+  v.x = (v.x - mean) * inv * op.g.x + op.b.x;
+  v.y = (v.y - mean) * inv * op.g.y + op.b.y;
+  v.z = (v.z - mean) * inv * op.g.z + op.b.z;
+  v.w = (v.w - mean) * inv * op.g.w + op.b.w;
+  return v;
+}
+
+// The 2D rotation of one 64-wide row held as one float4 per lane of a
+// 16-lane DPP row, with the cos/sin of qk_row_operands.  Lanes 0-7 hold the
+// y half (elements 0..31), lanes 8-15 the x half.  Every rotated pair
+// (a, b) with angle frequency j becomes (a*cos - b*sin, b*cos + a*sin),
 // each product rounded, then the sum.
-// SEQ: the mean and variance summed in the scalar reference's order (the
-// runtime's VK_LN_ORDER_SEQUENTIAL) and 1/sqrtf(var + eps) correctly
-// rounded: the bits of the CPU's LayerNorm of the row.
-template <bool HAS_NORM, int PAIR, bool SEQ = false>
-__device__ __forceinline__ float4 qk_row_apply(float4 v, int l, const QkRowOperands& op,
-                                               float eps) {
-  if (HAS_NORM && SEQ) {
-    const float mean = vkd::row16_seq_sum(v) / 64.0f;
-    float4 d;
-    d.x = v.x - mean; d.x = d.x * d.x;
-    d.y = v.y - mean; d.y = d.y * d.y;
-    d.z = v.z - mean; d.z = d.z * d.z;
-    d.w = v.w - mean; d.w = d.w * d.w;
-    const float var = vkd::row16_seq_sum(d) / 64.0f;
-    const float inv = 1.0f / sqrtf(var + eps);
-    v.x = (v.x - mean) * inv * op.g.x + op.b.x;
-    v.y = (v.y - mean) * inv * op.g.y + op.b.y;
-    v.z = (v.z - mean) * inv * op.g.z + op.b.z;
-    v.w = (v.w - mean) * inv * op.g.w + op.b.w;
-  } else if (HAS_NORM) {
-    float s = v.x;
-    s += v.y;
-    s += v.z;
-    s += v.w;
-    s = vkd::row16_sum(s);
-    const float mean = s / 64.0f;
-    float d, sq;
-    d = v.x - mean; sq = d * d;
-    d = v.y - mean; sq += d * d;
-    d = v.z - mean; sq += d * d;
-    d = v.w - mean; sq += d * d;
-    sq = vkd::row16_sum(sq);
-    const float var = sq / 64.0f;
-    // hardware reciprocal square root (v_rsq_f32, 1 ulp): the correctly
-    // rounded 1/sqrtf costs ~18 VALU instructions per row
-    const float inv = __builtin_amdgcn_rsqf(var + eps);
-    v.x = (v.x - mean) * inv * op.g.x + op.b.x;
-    v.y = (v.y - mean) * inv * op.g.y + op.b.y;
-    v.z = (v.z - mean) * inv * op.g.z + op.b.z;
-    v.w = (v.w - mean) * inv * op.g.w + op.b.w;
-  }
+template <int PAIR>
+__device__ __forceinline__ float4 qk_row_rope(float4 v, int l, const QkRowOperands& op) {
   const float4 c = op.c, s = op.s;
   float4 o;
   if (PAIR == kRotateHalf) {
@@ -263,15 +235,43 @@ __device__ __forceinline__ float4 qk_row_apply(float4 v, int l, const QkRowOpera
   return o;
 }
 
+// LayerNorm of one 64-wide row (the tree order: each lane's four values,
+// then the 16-lane DPP sum) and then its rotation, with the operands of
+// qk_row_operands.
+template <bool HAS_NORM, int PAIR>
+__device__ __forceinline__ float4 qk_row_apply(float4 v, int l, const QkRowOperands& op,
+                                               float eps) {
+  if (HAS_NORM) {
+    float s = v.x;
+    s += v.y;
+    s += v.z;
+    s += v.w;
+    s = vkd::row16_sum(s);
+    const float mean = s / 64.0f;
+    float d, sq;
+    d = v.x - mean; sq = d * d;
+    d = v.y - mean; sq += d * d;
+    d = v.z - mean; sq += d * d;
+    d = v.w - mean; sq += d * d;
+    sq = vkd::row16_sum(sq);
+    const float var = sq / 64.0f;
+    // hardware reciprocal square root (v_rsq_f32, 1 ulp): the correctly
+    // rounded 1/sqrtf costs ~18 VALU instructions per row
+    const float inv = __builtin_amdgcn_rsqf(var + eps);
+    v = qk_norm_apply(v, mean, inv, op);
+  }
+  return qk_row_rope<PAIR>(v, l, op);
+}
+
 // Both stages for one row (the QKV projection's epilogue).
-template <typename PT, bool HAS_NORM, int POS, int PAIR, bool SEQ = false>
+template <typename PT, bool HAS_NORM, int POS, int PAIR>
 __device__ __forceinline__ float4 qk_row_transform(float4 v, int l, const PT* __restrict__ g,
                                                    const PT* __restrict__ b, float py, float px,
                                                    const float* __restrict__ table,
                                                    int table_max, float eps) {
   const QkRowOperands op =
       qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, g, b, py, px, table, table_max);
-  return qk_row_apply<HAS_NORM, PAIR, SEQ>(v, l, op, eps);
+  return qk_row_apply<HAS_NORM, PAIR>(v, l, op, eps);
 }
 
 }  // namespace vkq
