@@ -893,7 +893,7 @@ def measured_traffic(op, algorithmic_bytes):
 OP_KERNELS = {
     "layerscale_residual_layernorm": "ls_residual_layernorm_rows<3, float, true, true, false>",
     "gelu": "gelu_kernel<0>",
-    "qk_norm_rope": "qk_norm_rope_rows<float, true, 1, 0>",
+    "qk_norm_rope": "qk_norm_rope_rows<float, true, 1, 0, false>",
     "layernorm": "layernorm_rows<3, float, true>",
     "layerscale_residual": "layerscale_residual_kernel<float>",
 }
@@ -943,6 +943,9 @@ def main():
                                      "patch_embed"],
                     help="profile mode: launch only this operation (12-view shape, rotating "
                          "buffers) after one calibration device copy of 256 MiB")
+    ap.add_argument("--ln-order", choices=["tree", "sequential"], default="tree",
+                    help="profile mode: the runtime's LayerNorm summation order (sequential: the "
+                         "CPU kernel's left-to-right sums and bits)")
     ap.add_argument("--op-views", type=int, default=12,
                     help="profile and headline modes: view count of the shape (866 rows each)")
     ap.add_argument("--patch-views", type=int, default=1,
@@ -980,6 +983,12 @@ def main():
     import vestra_hip as vh
     rng = np.random.default_rng(SEED)
     rt = vh.Runtime(0)
+    if args.ln_order == "sequential":
+        if not args.op:
+            print("--ln-order sequential applies to the profile mode (--op) only",
+                  file=sys.stderr)
+            sys.exit(2)
+        rt.set_layernorm_order(vh.VK_LN_ORDER_SEQUENTIAL)
     if args.sweep:
         # per-launch cost vs size: t(rows) ~ fixed ramp/drain + rows * per-row
         # stream time; fewer rotating sets at large sizes keep memory bounded
@@ -1024,7 +1033,8 @@ def main():
         sets = ROTATE_SETS * max(1, 12 // views)  # the working set stays beyond 256 MB
         table = per_op_table(rt, rng, TPV * views, rotate=sets, iters=args.op_iters,
                              only=args.op)
-        print(json.dumps({"op": args.op, "rows": TPV * views, "rotate_sets": sets,
+        print(json.dumps({"op": args.op, "ln_order": args.ln_order, "rows": TPV * views,
+                          "rotate_sets": sets,
                           "calibration_copy_bytes": 2 * (256 << 20), **table[args.op]}),
               flush=True)
         return
