@@ -889,12 +889,13 @@ def measured_traffic(op, algorithmic_bytes):
 
 
 # the kernel behind each per-operation-table entry at the 12-view shape
-# (D 768: three float4 per lane; f32 parameters; grid positions, views outer)
+# (D 768: three float4 per lane; f32 parameters; serialised stores; grid
+# positions, views outer)
 OP_KERNELS = {
-    "layerscale_residual_layernorm": "ls_residual_layernorm_rows<3, float, true, true, false>",
+    "layerscale_residual_layernorm": "ls_residual_layernorm_rows<3, float, true, true, true, false>",
     "gelu": "gelu_kernel<0>",
     "qk_norm_rope": "qk_norm_rope_rows<float, true, 1, 0, false>",
-    "layernorm": "layernorm_rows<3, float, true>",
+    "layernorm": "layernorm_rows<3, float, true, true>",
     "layerscale_residual": "layerscale_residual_kernel<float>",
 }
 

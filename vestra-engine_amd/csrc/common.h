@@ -136,6 +136,22 @@ void retain(vk_runtime* rt);
 void release(vk_runtime* rt);
 // Launch check: turns a failed launch into a status.
 int check_launch(const char* what);
+// Single-wave workgroups of a persistent stream over `units` equal units
+// (rows, 3 KiB chunks): two units per wave when that puts every wave on the
+// chip at once (cap < units <= 2 cap, cap = kStreamWavesPerCU waves per
+// CU), so that a wave, which loads its next unit before it stores the
+// current one, has issued all its reads before its first write; one unit
+// per wave otherwise.  Measured for LayerNorm at 10,392 x 768 (256 CUs):
+// two rows per wave 11.2 us, one 13.0, three 13.4; at 20,784 rows two rows
+// per wave (10,392 waves) 23.9 us, four 24.6, one 23.4.  At least one wave.
+constexpr int kStreamWavesPerCU = 24;
+inline unsigned stream_waves(const vk_runtime* rt, long long units) {
+  if (units <= 0) return 1;
+  const long long cap =
+      static_cast<long long>(rt->cu_count > 0 ? rt->cu_count : 256) * kStreamWavesPerCU;
+  const long long per = units > cap && units <= 2 * cap ? 2 : 1;
+  return static_cast<unsigned>((units + per - 1) / per);
+}
 // Device cos/sin table for the 2D RoPE (layout below) covering at least
 // positions 0..max(min_max_pos, kRopeTableMax); *table_max receives the
 // largest covered position.  Grows (re-allocates) when a larger grid needs
@@ -412,6 +428,13 @@ __device__ __forceinline__ void st_stream(float4* p, float4 v) {
   const f32x4_t t = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(t, reinterpret_cast<f32x4_t*>(p));
 }
+
+// Waits for every earlier vector memory operation of the wave, its
+// previous stores included.  Issued before each store of a stream kernel it
+// keeps one store of the wave in flight: out-of-place row streams and the
+// LayerScale + residual stream measured faster so on MI355X (HBM reads are
+// then not held up behind a backlog of the wave's writes).
+__device__ __forceinline__ void wait_memory() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));

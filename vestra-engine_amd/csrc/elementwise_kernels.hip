@@ -106,43 +106,56 @@ __global__ __launch_bounds__(256) void layerscale_kernel(float* __restrict__ x,
 }
 
 // x[r, c] += y[r, c] * g[c]   (t = y*g rounded, then x + t rounded)
+// The GELU stream's layout: each workgroup takes 512 consecutive float4 of x
+// and y (thread t: t and t + 256), both pairs of loads before either store,
+// and each store issued after the wave's earlier memory operations
+// (vkd::wait_memory).  Measured at 10,392 x 768: 16.7 us against 17.2 for a
+// grid-stride loop over two float4 a grid apart.
 template <typename PT>
 __global__ __launch_bounds__(256) void layerscale_residual_kernel(
     float* __restrict__ x, const float* __restrict__ y, const PT* __restrict__ g,
     long long n4, int cols4) {
-  const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
   float4* x4 = reinterpret_cast<float4*>(x);
   const float4* y4 = reinterpret_cast<const float4*>(y);
-  long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  for (; i + stride < n4; i += 2 * stride) {
-    float4 a = vkd::ld_stream(x4 + i);
-    float4 a2 = vkd::ld_stream(x4 + i + stride);
-    const float4 b = vkd::ld_stream(y4 + i);
-    const float4 b2 = vkd::ld_stream(y4 + i + stride);
-    const float4 gv = Param<PT>::load4(g, i % cols4);
-    const float4 gv2 = Param<PT>::load4(g, (i + stride) % cols4);
-    float t;
-    t = b.x * gv.x; a.x = a.x + t;
-    t = b.y * gv.y; a.y = a.y + t;
-    t = b.z * gv.z; a.z = a.z + t;
-    t = b.w * gv.w; a.w = a.w + t;
-    t = b2.x * gv2.x; a2.x = a2.x + t;
-    t = b2.y * gv2.y; a2.y = a2.y + t;
-    t = b2.z * gv2.z; a2.z = a2.z + t;
-    t = b2.w * gv2.w; a2.w = a2.w + t;
-    vkd::st_stream(x4 + i, a);
-    vkd::st_stream(x4 + i + stride, a2);
-  }
-  if (i < n4) {
-    float4 a = x4[i];
-    const float4 b = y4[i];
-    const float4 gv = Param<PT>::load4(g, i % cols4);
-    float t;
-    t = b.x * gv.x; a.x = a.x + t;
-    t = b.y * gv.y; a.y = a.y + t;
-    t = b.z * gv.z; a.z = a.z + t;
-    t = b.w * gv.w; a.w = a.w + t;
-    x4[i] = a;
+  constexpr long long kSpan = 512;
+  const long long step = static_cast<long long>(gridDim.x) * kSpan;
+  for (long long b = static_cast<long long>(blockIdx.x) * kSpan; b < n4; b += step) {
+    const long long i0 = b + threadIdx.x;
+    if (b + kSpan <= n4) {
+      float4 a[2], v[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        a[j] = vkd::ld_stream(x4 + i0 + 256 * j);
+        v[j] = vkd::ld_stream(y4 + i0 + 256 * j);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float4 gv = Param<PT>::load4(g, (i0 + 256 * j) % cols4);
+        float t;
+        t = v[j].x * gv.x; a[j].x = a[j].x + t;
+        t = v[j].y * gv.y; a[j].y = a[j].y + t;
+        t = v[j].z * gv.z; a[j].z = a[j].z + t;
+        t = v[j].w * gv.w; a[j].w = a[j].w + t;
+        vkd::wait_memory();
+        vkd::st_stream(x4 + i0 + 256 * j, a[j]);
+      }
+    } else {  // the last, partial span
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const long long i = i0 + 256 * j;
+        if (i < n4) {
+          float4 a = x4[i];
+          const float4 v = y4[i];
+          const float4 gv = Param<PT>::load4(g, i % cols4);
+          float t;
+          t = v.x * gv.x; a.x = a.x + t;
+          t = v.y * gv.y; a.y = a.y + t;
+          t = v.z * gv.z; a.z = a.z + t;
+          t = v.w * gv.w; a.w = a.w + t;
+          x4[i] = a;
+        }
+      }
+    }
   }
 }
 
@@ -240,7 +253,8 @@ int vk_layerscale_residual_f32(vk_runtime* rt, vk_tensor* x, const vk_tensor* y,
   if (rows * cols == 0) return VK_OK;
   const long long n4 = static_cast<long long>(rows * cols / 4);
   const int cols4 = static_cast<int>(cols / 4);
-  const unsigned grid = stream_grid(rt, (n4 + 1) / 2);
+  const long long spans = (n4 + 511) / 512;
+  const unsigned grid = static_cast<unsigned>(spans < kGeluMaxGrid ? spans : kGeluMaxGrid);
   if (gamma->dtype == VK_F16)
     hipLaunchKernelGGL((layerscale_residual_kernel<uint16_t>), dim3(grid), dim3(256), 0,
                        rt->stream, static_cast<float*>(x->ptr),

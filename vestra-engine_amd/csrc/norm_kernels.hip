@@ -3,13 +3,21 @@
 // RoPE.
 //
 // Mapping to CDNA4:
-//  * LayerNorm rows (D = 768 / 1024): one wave64 workgroup per row, each lane
-//    holds D/256 float4 in registers (128-bit coalesced loads: a wave reads
-//    one contiguous KiB per instruction), mean and variance reduced with DPP
-//    row reductions plus two cross-row swizzles; the row is read from HBM
-//    once and written once, both with nontemporal (streaming) hints.
-//    Single-wave workgroups measured fastest on MI355X (65.6% of peak at
-//    10392x768 vs 57.8% for four rows per 256-thread workgroup).
+//  * LayerNorm rows (D = 768 / 1024): single-wave workgroups, each lane
+//    holding D/256 float4 of a row in registers (128-bit coalesced loads: a
+//    wave reads one contiguous KiB per instruction), mean and variance
+//    reduced with DPP row reductions plus two cross-row swizzles; every row
+//    read from HBM once and written once, both with nontemporal (streaming)
+//    hints.  The waves are persistent: wave w takes rows w, w + W, ... (W =
+//    vk::stream_waves), loading its next row before it reduces the current
+//    one, so at the 12-view shape (10,392 rows, two per wave) each wave
+//    reads both its rows before it writes either; once the rows are a
+//    bandwidth-bound stream each store is also issued after the wave's
+//    earlier memory operations (vkd::wait_memory: one store of a wave in
+//    flight).  At 10,392 x 768: LayerNorm 11.2 us against 13.0-13.3 for one
+//    row per wave, the fused LayerScale + residual + LayerNorm 22.4 against
+//    23.7.  In-place element-wise streams (GELU, the Q/K rows) measured
+//    slower in this form and keep theirs.
 //  * Q/K rows (head_dim 64): 16 lanes per (head, token) row, one float4 per
 //    lane, so a row's LayerNorm reduces inside one DPP row (4 DPP steps) and
 //    the RoPE partner element (i <-> i+16 inside each 32-wide half) sits
@@ -32,62 +40,113 @@ namespace {
 using vkd::Param;
 
 // ---------------------------------------------------------------------------
-// LayerNorm over rows of `cols` floats, one wave per row.
-// NV = float4 per lane (cols <= 256 * NV).  EXACT: cols == 256 * NV, so no
-// lane is ever out of the row and every load is issued unguarded (a guarded
-// load makes the compiler wait for each one in turn).  x and y may alias.
+// Row streams shared by the LayerNorm kernels: a wave's NV float4 of row
+// `row` (lane l: float4 l + 64 i), unguarded when EXACT (cols == 256 NV, so
+// no lane is out of the row and no load waits behind a guard), zeros past
+// the row otherwise.
 // ---------------------------------------------------------------------------
-// Rows per workgroup (one wave each, no shared memory or barriers).
-#ifndef VK_LN_WAVES
-#define VK_LN_WAVES 1
-#endif
-constexpr int kLnWaves = VK_LN_WAVES;
+template <int NV, bool EXACT>
+__device__ __forceinline__ void load_row(float4 (&v)[NV], const float* base, int row, int cols,
+                                         int lane) {
+  const int nvec = cols >> 2;
+  const float4* r = reinterpret_cast<const float4*>(base + static_cast<size_t>(row) * cols);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * 64;
+    v[i] = (EXACT || c < nvec) ? vkd::ld_stream(r + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
 
-template <int NV, typename PT, bool EXACT>
-__global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows(const float* x, float* y,
+// The next row is prefetched while the current one is reduced up to 8
+// float4 per lane; wider rows walk their rows one at a time (register use).
+template <int NV>
+constexpr bool kRowPrefetch = NV <= 8;
+
+// A copy of a parameter pointer that the compiler cannot see through: loads
+// through it are not loop-invariant, so each row's parameter loads stay
+// beside that row's stores and each store waits for them (an L2 round trip
+// between a wave's stores).  With the parameters held in registers across
+// rows the persistent LayerNorm measured 13.3 us instead of 11.0 at 10,392
+// x 768.  The pointer is offset by an opaque zero, not passed through the
+// asm itself, so it keeps its global address space (global, not flat,
+// loads).
+template <typename T>
+__device__ __forceinline__ const T* per_row(const T* p) {
+  int zero = 0;
+  asm volatile("" : "+s"(zero));
+  return p + zero;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm over rows of `cols` floats.  NV = float4 per lane (cols <= 256
+// NV).  Persistent single-wave workgroups: wave w normalises rows w, w + W,
+// ... (W = gridDim.x, from vk::stream_waves), the next row's loads issued
+// before the current row's reductions, the parameters re-read for each row
+// (per_row) and, with SER, each store issued after the wave's earlier
+// memory operations.  The per-row arithmetic is row_mean_inv + ln_apply4, the same
+// as every other LayerNorm of a full row.  x and y may alias (each row is
+// read and written only by its own wave).
+// ---------------------------------------------------------------------------
+template <int NV, typename PT, bool EXACT, bool SER>
+__global__ __launch_bounds__(64) void layernorm_rows(const float* x, float* y,
                                                      const PT* __restrict__ gamma,
-                                                     const PT* __restrict__ beta,
-                                                     int rows, int cols, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
+                                                     const PT* __restrict__ beta, int rows,
+                                                     int cols, float eps) {
+  const int lane = threadIdx.x;
+  const int stride = static_cast<int>(gridDim.x);
+  int row = blockIdx.x;
   if (row >= rows) return;
   const int nvec = cols >> 2;
-  const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
-  float4 v[NV];
+  float4 cur[NV], nxt[NV];
+  load_row<NV, EXACT>(cur, x, row, cols, lane);
+  for (;;) {
+    const int nrow = row + stride;
+    const bool more = nrow < rows;
+    if (kRowPrefetch<NV> && more) load_row<NV, EXACT>(nxt, x, nrow, cols, lane);
+    float mean, inv;
+    vkd::row_mean_inv<NV, EXACT>(cur, lane, cols, eps, &mean, &inv);
+    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+    const PT* g = per_row(gamma);
+    const PT* b = per_row(beta);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + i * 64;
-    v[i] = (EXACT || c < nvec) ? vkd::ld_stream(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  float mean, inv;
-  vkd::row_mean_inv<NV, EXACT>(v, lane, cols, eps, &mean, &inv);
-  float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + i * 64;
-    if (EXACT || c < nvec) {
-      vkd::st_stream(yr + c, vkd::ln_apply4(v[i], mean, inv, Param<PT>::load4(gamma, c),
-                                            Param<PT>::load4(beta, c)));
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + i * 64;
+      if (EXACT || c < nvec) {
+        const float4 o = vkd::ln_apply4(cur[i], mean, inv, Param<PT>::load4(g, c),
+                                        Param<PT>::load4(b, c));
+        if (SER) vkd::wait_memory();
+        vkd::st_stream(yr + c, o);
+      }
     }
+    if (!more) break;
+    if constexpr (kRowPrefetch<NV>) {
+      for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
+    } else {
+      load_row<NV, EXACT>(cur, x, nrow, cols, lane);
+    }
+    row = nrow;
   }
 }
 
 // ---------------------------------------------------------------------------
 // x += ls (.) yb (t = yb*ls rounded, x = x + t rounded); ln_out = LN(x).
-// HAS_LS false: unscaled residual add.  One wave per row.
+// HAS_LS false: unscaled residual add.  One wave per row, both streams'
+// loads first: the latency-bound sizes (below kSerRowsPerCU rows per CU),
+// where it measured 3.4 us cold at 866 x 768 against 4.0 for the persistent
+// form below.
 // CAM: the camera-token slot, row 0 of every view of tpv rows, then takes
 // the camera token (cam[0..cols) for view 0, cam[cols..2 cols) for the
 // others) in x and in the LayerNorm, as an overwrite between the residual
 // update and the LayerNorm would.
 // ---------------------------------------------------------------------------
-template <int NV, typename PT, bool HAS_LS, bool EXACT, bool CAM = false>
-__global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
+template <int NV, typename PT, bool HAS_LS, bool EXACT, bool CAM>
+__global__ __launch_bounds__(64) void ls_residual_layernorm_row(
     float* __restrict__ x, const float* __restrict__ yb, const PT* __restrict__ ls,
     const PT* __restrict__ gamma, const PT* __restrict__ beta,
     float* __restrict__ ln_out, int rows, int cols, float eps,
     const float* __restrict__ cam, int tpv) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
+  const int row = blockIdx.x;
   if (row >= rows) return;
   const int nvec = cols >> 2;
   const size_t base = static_cast<size_t>(row) * cols;
@@ -134,6 +193,116 @@ __global__ __launch_bounds__(64 * kLnWaves) void ls_residual_layernorm_rows(
       vkd::st_stream(outr + c, vkd::ln_apply4(v[i], mean, inv, Param<PT>::load4(gamma, c),
                                               Param<PT>::load4(beta, c)));
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// x += ls (.) yb (t = yb*ls rounded, x = x + t rounded); ln_out = LN(x).
+// HAS_LS false: unscaled residual add.  Persistent single-wave workgroups
+// over rows w, w + W, ... as layernorm_rows, the next row's x and yb loaded
+// (interleaved float4 by float4) before the current row's arithmetic; SER:
+// every store issued after the wave's earlier memory operations.  The
+// pointers carry no __restrict__: with it the compiler batched the
+// parameter loads ahead of the stores and the stream measured 24.4 us
+// instead of 22.4 at 10,392 x 768 (one row per wave: 23.7).
+// CAM: the camera-token slot, row 0 of every view of tpv rows, then takes
+// the camera token (cam[0..cols) for view 0, cam[cols..2 cols) for the
+// others) in x and in the LayerNorm, as an overwrite between the residual
+// update and the LayerNorm would.
+// ---------------------------------------------------------------------------
+template <int NV, typename PT, bool HAS_LS, bool EXACT, bool SER, bool CAM>
+__global__ __launch_bounds__(64) void ls_residual_layernorm_rows(
+    float* x, const float* yb, const PT* ls, const PT* gamma, const PT* beta, float* ln_out,
+    int rows, int cols, float eps, const float* cam, int tpv) {
+  const int lane = threadIdx.x;
+  const int stride = static_cast<int>(gridDim.x);
+  int row = blockIdx.x;
+  const int nvec = cols >> 2;
+  float4 ca[NV], cb[NV], na[NV], nb[NV];
+  if (row < rows) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      const bool in = EXACT || c < nvec;
+      ca[i] = in ? vkd::ld_stream(reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols) + c)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+      cb[i] = in ? vkd::ld_stream(reinterpret_cast<const float4*>(yb + static_cast<size_t>(row) * cols) + c)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  while (row < rows) {
+    const int nrow = row + stride;
+    if (kRowPrefetch<NV> && nrow < rows) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        const bool in = EXACT || c < nvec;
+        na[i] = in ? vkd::ld_stream(reinterpret_cast<const float4*>(x + static_cast<size_t>(nrow) * cols) + c)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        nb[i] = in ? vkd::ld_stream(reinterpret_cast<const float4*>(yb + static_cast<size_t>(nrow) * cols) + c)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    // uniform over the wave
+    const float4* camr = CAM && row % tpv == 0
+                             ? reinterpret_cast<const float4*>(cam + (row >= tpv ? cols : 0))
+                             : nullptr;
+    float4* xr = reinterpret_cast<float4*>(x + static_cast<size_t>(row) * cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (EXACT || c < nvec) {
+        float4 a = ca[i];
+        const float4 b = cb[i];
+        if (HAS_LS) {
+          const float4 g = Param<PT>::load4(ls, c);
+          float t;
+          t = b.x * g.x; a.x = a.x + t;
+          t = b.y * g.y; a.y = a.y + t;
+          t = b.z * g.z; a.z = a.z + t;
+          t = b.w * g.w; a.w = a.w + t;
+        } else {
+          a.x = a.x + b.x;
+          a.y = a.y + b.y;
+          a.z = a.z + b.z;
+          a.w = a.w + b.w;
+        }
+        if (CAM && camr) a = camr[c];
+        if (SER) vkd::wait_memory();
+        vkd::st_stream(xr + c, a);
+        ca[i] = a;
+      }
+    }
+    float mean, inv;
+    vkd::row_mean_inv<NV, EXACT>(ca, lane, cols, eps, &mean, &inv);
+    float4* outr = reinterpret_cast<float4*>(ln_out + static_cast<size_t>(row) * cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (EXACT || c < nvec) {
+        const float4 o = vkd::ln_apply4(ca[i], mean, inv, Param<PT>::load4(gamma, c),
+                                        Param<PT>::load4(beta, c));
+        if (SER) vkd::wait_memory();
+        vkd::st_stream(outr + c, o);
+      }
+    }
+    if constexpr (kRowPrefetch<NV>) {
+      for (int i = 0; i < NV; ++i) {
+        ca[i] = na[i];
+        cb[i] = nb[i];
+      }
+    } else if (nrow < rows) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        const bool in = EXACT || c < nvec;
+        ca[i] = in ? vkd::ld_stream(reinterpret_cast<const float4*>(x + static_cast<size_t>(nrow) * cols) + c)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        cb[i] = in ? vkd::ld_stream(reinterpret_cast<const float4*>(yb + static_cast<size_t>(nrow) * cols) + c)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    row = nrow;
   }
 }
 
@@ -527,6 +696,16 @@ int launch_seq(vk_runtime* rt, const SeqLnArgs& a, int nv) {
   return vk::check_launch("seq_layernorm_rows");
 }
 
+// Stores serialised per wave (SER) once the rows are a bandwidth-bound
+// stream: at least kSerRowsPerCU rows per CU (2,048 on 256 CUs).  At one
+// image (866 rows) the launch is latency-bound and the waits cost time
+// (LayerNorm 2.9 -> 3.2 us, the fused form 3.4 -> 4.0 us in cold HBM).
+constexpr int kSerRowsPerCU = 8;
+
+bool serialise_stores(const vk_runtime* rt, int rows) {
+  return rows >= (rt->cu_count > 0 ? rt->cu_count : 256) * kSerRowsPerCU;
+}
+
 template <typename PT>
 int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
                      const void* b, int rows, int cols, float eps) {
@@ -539,15 +718,18 @@ int launch_layernorm(vk_runtime* rt, const float* x, float* y, const void* g,
     return launch_seq<PT, false, false, false>(rt, a, snv);
   }
   const int nv = ln_instance_cols(cols);
-  dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
+  const dim3 grid(vk::stream_waves(rt, rows)), block(64);
+  const bool ser = serialise_stores(rt, rows);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
 #define VK_LN_CASE(N)                                                                          \
   case N:                                                                                      \
-    if (cols == N * 256)                                                                       \
-      hipLaunchKernelGGL((layernorm_rows<N, PT, true>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
+    if (cols == N * 256 && ser)                                                                \
+      hipLaunchKernelGGL((layernorm_rows<N, PT, true, true>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
+    else if (cols == N * 256)                                                                  \
+      hipLaunchKernelGGL((layernorm_rows<N, PT, true, false>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
     else                                                                                       \
-      hipLaunchKernelGGL((layernorm_rows<N, PT, false>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
+      hipLaunchKernelGGL((layernorm_rows<N, PT, false, false>), grid, block, 0, rt->stream, x, y, G, B, rows, cols, eps); \
     break;
   switch (nv) {
     VK_LN_CASE(1) VK_LN_CASE(2) VK_LN_CASE(3) VK_LN_CASE(4)
@@ -578,20 +760,28 @@ int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
                : launch_seq<PT, true, HAS_LS, false>(rt, a, snv);
   }
   const int nv = ln_instance_cols(cols);
-  dim3 grid((rows + kLnWaves - 1) / kLnWaves), block(64 * kLnWaves);
+  const dim3 grid(vk::stream_waves(rt, rows)), block(64);
+  const bool ser = serialise_stores(rt, rows);
   auto LS = static_cast<const PT*>(ls);
   auto G = static_cast<const PT*>(g);
   auto B = static_cast<const PT*>(b);
+#define VK_LSLN_LAUNCH(N, EX, SR, CM)                                                          \
+  hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, EX, SR, CM>), grid, block, 0, \
+                     rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv)
+#define VK_LSLN_ROW(N, EX, CM)                                                                 \
+  hipLaunchKernelGGL((ls_residual_layernorm_row<N, PT, HAS_LS, EX, CM>), dim3(rows), block, 0,  \
+                     rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv)
 #define VK_LSLN_CASE(N)                                                                        \
   case N:                                                                                      \
-    if (cam && cols == N * 256)                                                                \
-      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, true, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
-    else if (cam)                                                                              \
-      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, false, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
-    else if (cols == N * 256)                                                                  \
-      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, true>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
-    else                                                                                       \
-      hipLaunchKernelGGL((ls_residual_layernorm_rows<N, PT, HAS_LS, false>), grid, block, 0, rt->stream, x, yb, LS, G, B, out, rows, cols, eps, cam, tpv); \
+    if (cols == N * 256 && ser) {                                                              \
+      if (cam) VK_LSLN_LAUNCH(N, true, true, true); else VK_LSLN_LAUNCH(N, true, true, false); \
+    } else if (cols == N * 256) {                                                              \
+      if (cam) VK_LSLN_ROW(N, true, true); else VK_LSLN_ROW(N, true, false);                   \
+    } else if (cam) {                                                                          \
+      VK_LSLN_ROW(N, false, true);                                                             \
+    } else {                                                                                   \
+      VK_LSLN_ROW(N, false, false);                                                            \
+    }                                                                                          \
     break;
   switch (nv) {
     VK_LSLN_CASE(1) VK_LSLN_CASE(2) VK_LSLN_CASE(3) VK_LSLN_CASE(4)
@@ -601,6 +791,8 @@ int launch_ls_res_ln(vk_runtime* rt, float* x, const float* yb, const void* ls,
       return vk::set_error(VK_ERR_UNSUPPORTED, "ls_residual_layernorm: no instance for cols=%d", cols);
   }
 #undef VK_LSLN_CASE
+#undef VK_LSLN_LAUNCH
+#undef VK_LSLN_ROW
   return vk::check_launch("ls_residual_layernorm_rows");
 }
 
