@@ -63,13 +63,14 @@ template <int NV>
 constexpr bool kRowPrefetch = NV <= 8;
 
 // A copy of a parameter pointer that the compiler cannot see through: loads
-// through it are not loop-invariant, so each row's parameter loads stay
-// beside that row's stores and each store waits for them (an L2 round trip
-// between a wave's stores).  With the parameters held in registers across
-// rows the persistent LayerNorm measured 13.3 us instead of 11.0 at 10,392
-// x 768.  The pointer is offset by an opaque zero, not passed through the
-// asm itself, so it keeps its global address space (global, not flat,
-// loads).
+// through it are not loop-invariant, so each row's parameter loads stay in
+// the row loop, between the wave's stores, where the store waits
+// (vkd::wait_memory) also wait for them.  At 10,392 x 768 the persistent
+// LayerNorm measured 11.0 us so, 12.3 with the parameters held in registers
+// across rows, and 12.6 without the waits (the compiler then issues a
+// row's parameter loads ahead of its stores).  The pointer is offset by an
+// opaque zero, not passed through the asm itself, so it keeps its global
+// address space (global, not flat, loads).
 template <typename T>
 __device__ __forceinline__ const T* per_row(const T* p) {
   int zero = 0;
@@ -83,9 +84,9 @@ __device__ __forceinline__ const T* per_row(const T* p) {
 // ... (W = gridDim.x, from vk::stream_waves), the next row's loads issued
 // before the current row's reductions, the parameters re-read for each row
 // (per_row) and, with SER, each store issued after the wave's earlier
-// memory operations.  The per-row arithmetic is row_mean_inv + ln_apply4, the same
-// as every other LayerNorm of a full row.  x and y may alias (each row is
-// read and written only by its own wave).
+// memory operations.  The per-row arithmetic is row_mean_inv + ln_apply4,
+// the same as every other LayerNorm of a full row.  x and y may alias (each
+// row is read and written only by its own wave).
 // ---------------------------------------------------------------------------
 template <int NV, typename PT, bool EXACT, bool SER>
 __global__ __launch_bounds__(64) void layernorm_rows(const float* x, float* y,
