@@ -153,6 +153,65 @@ def test_fused_layerscale_residual_layernorm(rt, rng, with_ls):
                   "ls+res+ln")
 
 
+# Row counts at the edges of the row kernels' launch regimes, from the CU count
+# as the launchers see it: stores are serialised from 8 rows per CU, and a
+# wave takes two rows when the rows exceed 24 waves per CU but not twice that
+# (an odd count leaves the last wave one row).
+ROW_REGIMES = {
+    "below_serialised": lambda cu: 8 * cu - 1,
+    "first_serialised": lambda cu: 8 * cu,
+    "two_per_wave_first": lambda cu: 24 * cu + 1,
+    "two_per_wave_odd_last": lambda cu: 48 * cu - 1,
+    "one_per_wave_again": lambda cu: 48 * cu + 1,
+}
+
+
+@pytest.mark.parametrize("regime", sorted(ROW_REGIMES))
+def test_layernorm_row_regimes(rt, rng, regime):
+    rows, cols = ROW_REGIMES[regime](rt.cu_count()), 768
+    x = normals(rng, rows, cols, shift=0.5)
+    g = normals(rng, cols, scale=0.02, shift=1.0)
+    b = normals(rng, cols, scale=0.02)
+    out = rt.layernorm_f32_cpu_order(rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b),
+                                     rows, cols, 1e-6).numpy()
+    assert_parity(out, oracle.layernorm(x, g, b, 1e-6), F32_ATOL, F32_RTOL,
+                  f"ln {regime} {rows}x{cols}")
+
+
+def test_layernorm_two_per_wave_ragged_cols(rt, rng):
+    """640 columns (not a multiple of 256) in the two-rows-per-wave regime."""
+    rows, cols = 48 * rt.cu_count() - 1, 640
+    x = normals(rng, rows, cols)
+    g = normals(rng, cols, scale=0.02, shift=1.0)
+    b = normals(rng, cols, scale=0.02)
+    out = rt.layernorm_f32_cpu_order(rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b),
+                                     rows, cols, 1e-6).numpy()
+    assert_parity(out, oracle.layernorm(x, g, b, 1e-6), F32_ATOL, F32_RTOL,
+                  f"ln ragged {rows}x{cols}")
+
+
+@pytest.mark.parametrize("regime", sorted(ROW_REGIMES))
+def test_fused_layerscale_residual_layernorm_row_regimes(rt, rng, regime):
+    """x bit-exact; the LayerNorm output equals the separate LayerNorm of the
+    updated x bit for bit (both reduce a row in the same order)."""
+    rows, cols = ROW_REGIMES[regime](rt.cu_count()), 768
+    x, y = normals(rng, rows, cols), normals(rng, rows, cols)
+    ls = rng.uniform(0, 0.1, cols).astype(np.float32)
+    g = normals(rng, cols, scale=0.02, shift=1.0)
+    b = normals(rng, cols, scale=0.02)
+    tx, tg, tb = rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b)
+    out = rt.alloc_f32(rows * cols)
+    rt.layerscale_residual_layernorm_f32(tx, rt.upload_f32(y), rt.upload_f32(ls), tg, tb,
+                                         rows, cols, 1e-6, out)
+    x_ref = oracle.layerscale_residual(x, y, ls)
+    assert np.array_equal(tx.numpy().reshape(rows, cols), x_ref)
+    fused = out.numpy()
+    assert_parity(fused, oracle.layernorm(x_ref, g, b, 1e-6), F32_ATOL, F32_RTOL,
+                  f"ls+res+ln {regime} {rows}x{cols}")
+    alone = rt.layernorm_f32_cpu_order(tx, tg, tb, rows, cols, 1e-6).numpy()
+    assert np.array_equal(fused, alone)
+
+
 # ---------------------------------------------------------------- Q/K norm + RoPE
 def qk_params(rng, dtype=np.float32):
     return [normals(rng, 64, scale=0.02, shift=1.0 if i % 2 == 0 else 0.0).astype(dtype)

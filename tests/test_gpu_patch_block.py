@@ -62,6 +62,28 @@ def test_runtime_copies(rt, rng):
     assert "outside" in e.value.message
 
 
+# 16-byte copies run in chunks of 192 float4 per wave, two chunks per wave
+# between 24 and 48 waves per CU, and the last workgroup copies what is left
+# after the whole chunks; other alignments take the element loop.
+@pytest.mark.parametrize("float4s", ["short", "one_chunk_plus", "two_per_wave", "one_per_wave"])
+def test_device_copy_sizes(rt, rng, float4s):
+    cu = rt.cu_count()
+    n16 = {"short": 100, "one_chunk_plus": 192 * 5 + 40,
+           "two_per_wave": 192 * (24 * cu + 7) + 37,
+           "one_per_wave": 192 * (48 * cu + 3) + 191}[float4s]
+    x = normals(rng, 4 * n16)
+    t = rt.upload_f32(x)
+    assert np.array_equal(rt.copy_f32(t).numpy(), x)
+    dst = rt.upload_f32(np.full(4 * n16 + 8, -1.0, np.float32))
+    rt.copy_segment_into_f32(dst, 4, t, 0, 4 * n16)          # 16-byte aligned
+    expect = np.full(4 * n16 + 8, -1.0, np.float32)
+    expect[4:4 + 4 * n16] = x
+    assert np.array_equal(dst.numpy(), expect)
+    rt.copy_segment_into_f32(dst, 1, t, 3, 4 * n16 - 5)      # 4-byte aligned
+    expect[1:4 * n16 - 4] = x[3:4 * n16 - 2]
+    assert np.array_equal(dst.numpy(), expect)
+
+
 def test_events_and_graph_replays(rt, rng):
     rows, cols = 866, 768
     x, y = normals(rng, rows, cols), normals(rng, rows, cols)
