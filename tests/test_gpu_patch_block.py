@@ -365,13 +365,18 @@ def test_patch_embed_f16_filter_vitl_matches_oracle(rt, rng):
 @pytest.mark.parametrize("h,w,embed,views,n_register", [(336, 504, 768, 12, 1),
                                                         (336, 504, 768, 2, 1),
                                                         (28, 42, 16, 5, 0),
-                                                        (28, 42, 80, 300, 2)])
+                                                        (28, 42, 80, 300, 2),
+                                                        (112, 168, 768, 2, 1),
+                                                        (672, 1008, 1024, 2, 1)])
 def test_patch_embed_views_match_single_views(rt, rng, h, w, embed, views, n_register):
     """All views of one processed shape in one launch (the per-view loop of
     prepare_multi_view, engine.rs:573-626): every view's tokens carry the
     bits of its own vk_patch_embed_u8 call.  Launches of more 32-patch tiles
     than CUs take the pipelined kernel (persistent workgroups of two to 16
-    tiles here, partial tiles in M and N at 28x42 with 80 outputs)."""
+    tiles here, partial tiles in M and N at 28x42 with 80 outputs); the
+    others and every single view take the gathered kernel, with u32
+    addresses for one round of tiles (two 112x168 views: 48 tiles, view by
+    view) and u16 for several (one 672x1008 view: 1,188 tiles)."""
     gh, gw = h // 14, w // 14
     tpv = 1 + n_register + gh * gw
     imgs = rng.integers(0, 256, (views, h, w, 3), dtype=np.uint8)

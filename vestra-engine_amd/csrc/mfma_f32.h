@@ -1,5 +1,6 @@
-// The 48 x 64 F32-MFMA output tile shared by the fused patch embedding
-// (patch_embed.hip) and the narrow linear (linear_api.hip).
+// The 48 x 64 F32-MFMA output tile of the narrow linear (linear_api.hip);
+// the pipelined patch embedding (patch_embed.hip) keeps its wave layout and
+// fragment order.
 //
 // Eight MFMA waves (two per SIMD) compute a 48 x 64 tile: wave w computes the
 // 48 x 16 strip w%4 (three 16x16 accumulators) over one half of K (split-K

@@ -4,18 +4,23 @@
 //
 // The convolution is a GEMM
 //   tokens[p, e] = sum_k A[p, k] * W[e, k] + b[e]
-// with A the normalised, unfolded image.  patch_embed_kernel does it all in
-// one pass: A is gathered straight from the u8 HWC image and normalised
+// with A the normalised, unfolded image.  Both kernels below do it all in
+// one pass: A is taken straight from the u8 HWC image and normalised
 // through a 3x256 lookup table in LDS (the table holds exactly
 // (u8/255 - mean)/std, so the normalisation is bit-identical to the scalar
 // path), the filter is read from a copy of its rows reordered at prepare
 // time to the image's byte order (prepare_patch_filter below), the products
-// run on v_mfma_f32_16x16x4_f32 (F32 in, F32 accumulate) on the 48 x 64
-// tiles of mfma_f32.h, and the epilogue adds the bias and the position table
-// and writes the assembled token rows (CLS + pos[0], register rows, patch
-// rows) so nothing round-trips through HBM.
+// run on v_mfma_f32_16x16x4_f32 (F32 in, F32 accumulate), and the epilogue
+// adds the bias and the position table and writes the assembled token rows
+// (CLS + pos[0], register rows, patch rows) so nothing round-trips through
+// HBM.  patch_embed_gather_kernel takes one image (or a few views),
+// patch_embed_pipelined_kernel the many tiles of a multi-view batch; both
+// give every output element the same operation order, so a view's tokens
+// have the same bits whichever kernel computes them.
 #include "common.h"
 #include "mfma_f32.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -29,46 +34,32 @@ using namespace vkm;
 constexpr int kPatch = 14;
 
 // ---------------------------------------------------------------------------
-// Fused patch embedding.  K is taken in the image's own order, k = ky*42 +
-// kx*3 + c (the filter is reordered to match at prepare time), so one patch
-// row is 42 contiguous bytes of the HWC image and 42 consecutive k.  The whole
-// A tile (48 patches x 588, 113 KB) lives in LDS, gathered and normalised
-// once; each wave streams its B fragments (16 columns x its half of K)
-// straight from L2 into registers, eight blocks ahead of the MFMAs.
-//
-// The workgroup has 12 waves: waves 0-7 run the MFMAs (two per SIMD, as the
-// linear), waves 8-11 only stage.  Staging overlaps the MFMAs: pixel rows ky
-// 0-7 of every patch (k < 336 = 21 blocks) are normalised into LDS first;
-// then the compute waves run those blocks (waves 0-3 blocks 0-9, waves 4-7
-// blocks 11-20) while the staging waves normalise rows ky 8-13; one barrier
-// later waves 0-3 run blocks 21-28 and then 10, waves 4-7 blocks 29-36.
+// K is taken in the image's own order, k = ky*42 + kx*3 + c (the filter is
+// reordered to match at prepare time), so one patch row is 42 contiguous
+// bytes of the HWC image and 42 consecutive k.  K is padded to 592 = 37
+// blocks of 16.  In block b, lane group g = lane / 16 holds k = 16 b + 4 g + j
+// in component j of one fragment read, and MFMA step j multiplies component
+// j.  The operation order every output element follows: two k halves, each
+// a chain of blocks in one accumulator -- half 0 blocks 0-9, 21-28 and then
+// 10, half 1 blocks 11-20 and 29-36 -- then (half 0 + half 1), + bias,
+// + position.
 // ---------------------------------------------------------------------------
 constexpr int kPeRowBytes = 3 * kPatch;    // 42 bytes per patch row
 constexpr int kPeK = kPatch * kPeRowBytes; // 588
 constexpr int kPeKp = 592;                 // 37 blocks of 16
 constexpr int kPeBlocks = kPeKp / 16;
-constexpr int kPeSplitKy = 8;              // first stage: ky < 8
-constexpr int kPeBlocksA = kPeSplitKy * kPeRowBytes / 16;  // 21 blocks in the first stage
-constexpr int kPeRowsA = kPeSplitKy * BM;                  // 384 patch rows
-constexpr int kPeRowsB = (kPatch - kPeSplitKy) * BM;       // 288 patch rows
-constexpr int kPePhase1 = kPeBlocksA / 2;                  // 10 per wave
-constexpr int kPePhase2 = (kPeBlocks - kPeBlocksA) / 2;    // 8 per wave
-constexpr int kPeSeq = kPePhase1 + kPePhase2 + 1;          // + waves 0-3's stage-A block 10
-constexpr int kPeAhead = 8;                // B prefetch distance in blocks
-constexpr int kPePitch = 596;              // A row pitch in LDS: 4 x 149
-constexpr int kPeStagers = 256;            // waves 8-11
+constexpr int kPeBlocksA = 8 * kPeRowBytes / 16;         // 21: blocks of pixel rows 0-7
+constexpr int kPePhase1 = kPeBlocksA / 2;                // 10: half 0 blocks 0-9, half 1 11-20
+constexpr int kPePhase2 = (kPeBlocks - kPeBlocksA) / 2;  // 8: half 0 21-28, half 1 29-36
+constexpr int kPeSeq = kPePhase1 + kPePhase2 + 1;        // + half 0's last block, 10
+constexpr int kPePitch = 596;              // normalised A row pitch in LDS: 4 x 149
+constexpr int kPeStagers = 256;            // staging waves of the pipelined kernel
 constexpr int kPeThreads = kThreads + kPeStagers;
 static_assert(kPeKp % 16 == 0 && kPeKp >= kPeK && kPeKp == (kPeK + kKAlign - 1) / kKAlign * kKAlign,
               "weight rows padded to a 16-block");
-static_assert(kPeSplitKy * kPeRowBytes % 16 == 0, "stage boundary on a block boundary");
-static_assert(BM == 48 && kPatch % 2 == 0 && kPeSplitKy % 2 == 0,
-              "patch-row groups of 16 patches x 2 pixel rows");
 static_assert(kPeBlocksA == 2 * kPePhase1 + 1 && kPeBlocks - kPeBlocksA == 2 * kPePhase2,
               "block split");
-static_assert(kPeRowsA <= kThreads && kPeRowsA % 64 == 0 && kPeRowsB > kPeStagers &&
-                  kPeRowsB <= 2 * kPeStagers && 3 * 256 == kPeThreads,
-              "stage A: one patch row per thread of the first waves; stage B: at most two per "
-              "staging thread; one table entry per thread");
+static_assert(3 * 256 == kPeThreads, "one table entry per thread of the pipelined kernel");
 static_assert(kPePitch % 4 == 0 && (kPePitch / 4) % 2 == 1 && kPePitch >= kPeKp, "pitch 4 x odd");
 
 struct PatchArgs {
@@ -133,203 +124,310 @@ struct PatchRow {
   }
 };
 
-__global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
-  __shared__ float lut[3 * 256];
-  __shared__ __align__(16) float As[BM * kPePitch];
-  __shared__ float red[4 * 12 * 64];
+// ---------------------------------------------------------------------------
+// Gathered patch embedding, for one image (and launches of few views).
+// Tiles are 32 patches x 96 outputs (a 336 x 504 image: 27 x 8 = 216
+// workgroups, numbered XCD-major, so each XCD's L2 holds one 96-column slice
+// of the filter).  The A tile stays in LDS as the table address of every
+// element (the byte offset 4 v + 1024 c), written straight from the image
+// bytes; the MFMA waves read their fragments' addresses and gather the
+// normalised values from the table themselves.  So the MFMAs start as soon
+// as the address tile and the table are in LDS: there is no normalised tile
+// to build first, and no wave stages while the MFMAs run.  Eight waves, two
+// per SIMD: wave w takes patches 16 (w % 2) .. +16, the three 16-column
+// strips 3 ((w / 2) % 2) .. +3 and k half w / 4 (each SIMD runs one wave of
+// either half: 19 + 18 blocks), and one gathered fragment feeds three
+// strips.  Every output element takes the block sequence, k-half split and
+// epilogue order above.
+//
+// Addresses are held as u32 (91 KB of LDS, one workgroup per CU: a launch
+// of one round of tiles, and four addresses per 128-bit read) or as u16
+// (54 KB, two workgroups per CU for launches of several rounds; four
+// addresses per 64-bit read, split one block after the read).
+// ---------------------------------------------------------------------------
+constexpr int kGm = 32;           // patches per tile
+constexpr int kGn = 96;           // outputs per tile
+constexpr int kGThreads = 512;
+constexpr int kGZero = 3 * 256;   // table entry 768 holds 0: the K padding's address
+constexpr int kGAhead = 3;        // B fragments this many blocks ahead
+constexpr int kGLook = 2;         // gathered values this many blocks ahead, addresses one more
+static_assert(kGm * kPatch <= kGThreads && kGThreads - kGm * kPatch >= 2 * kGm,
+              "one patch row per staging thread; the padding by the others");
+static_assert(kGn == 6 * 16 && kGm == 2 * 16, "waves: 2 patch strips x 2 k halves x 2 column groups");
 
+template <bool U16>
+struct GatherTile {
+  typedef typename std::conditional<U16, uint16_t, uint32_t>::type Addr;
+  static constexpr int kPitch = U16 ? 600 : 596;  // addresses per patch in LDS
+};
+static_assert(GatherTile<false>::kPitch >= kPeKp && GatherTile<false>::kPitch % 4 == 0 &&
+                  (GatherTile<false>::kPitch / 4) % 2 == 1,
+              "u32: 128-bit reads of 16 patches start on 16 distinct 4-bank groups");
+static_assert(GatherTile<true>::kPitch >= kPeKp && GatherTile<true>::kPitch % 4 == 0,
+              "u16: 64-bit reads aligned");
+typedef uint32_t __attribute__((may_alias)) u32_alias;
+
+// Block s of a k half's sequence (the order above): positions
+// 0-9 are blocks first1 + s, positions 10-17 blocks first2 + s - 10, and
+// half 0's position 18 is block 10.  Both halves run the same code (one
+// instruction stream through the instruction cache: two streams measured
+// slower) with two base pointers per operand, so every block offset is an
+// immediate.
+constexpr int kGSeg = kPePhase1;               // positions in the first segment
+constexpr int kGSeg2 = kPePhase1 + kPePhase2;  // end of the second
+
+template <bool U16>
+__global__ __launch_bounds__(kGThreads) void patch_embed_gather_kernel(PatchArgs p) {
+  using Addr = typename GatherTile<U16>::Addr;
+  constexpr int kPitch = GatherTile<U16>::kPitch;
+  // one LDS block with the table first, at offset 0: the gathers' addresses
+  // then fit the LDS instructions' 16-bit offset field (no address adds)
+  __shared__ struct __align__(16) {
+    float lut[3 * 256 + 4];
+    Addr At[kGm * kPitch];
+    float red[4 * 12 * 64];
+  } sm;
+  float* const lut = sm.lut;
+  Addr* const At = sm.At;
+  float* const red = sm.red;
+  // every argument the first addresses and the epilogue need, fetched in
+  // one batch (each fetch otherwise waits for the one before it)
+  asm volatile("" ::"s"(p.img), "s"(p.wpk), "s"(p.bias), "s"(p.pos), "s"(p.out),
+               "s"(p.img_bytes), "s"(p.tiles), "s"(p.W), "s"(p.gw), "s"(p.M), "s"(p.N),
+               "s"(p.n_register), "s"(p.fgw.m), "s"(p.fgw.s1), "s"(p.fgw.s2), "s"(gridDim.x));
   const int tid = threadIdx.x;
-  __builtin_assume(tid < kPeThreads);
   const int wave = tid >> 6, lane = tid & 63;
-  const bool stager = tid >= kThreads;
-  const int strip = wave & 3, half = (wave >> 2) & 1;
-  const int gmt = (p.M + BM - 1) / BM;
-  // views one after another: workgroup -> (view, tile of the view)
+  const int rs = wave & 1, cg = (wave >> 1) & 1, half = wave >> 2;
+  const int first1 = half ? kPePhase1 + 1 : 0;
+  const int first2 = kPeBlocksA + half * kPePhase2;
+  const int len = half ? kPeSeq - 1 : kPeSeq;
+  const int g = lane >> 4;
+  const int gmt = (p.M + kGm - 1) / kGm;
   const int tile_all = xcd_tile(blockIdx.x, gridDim.x);
   const int view = tile_all / p.tiles;
   const int tile = tile_all - view * p.tiles;
   const uint8_t* const img = p.img + static_cast<size_t>(view) * p.img_bytes;
-  float* const out = p.out + static_cast<size_t>(view) * (1 + p.n_register + p.M) * p.N;
-  const int mt = tile % gmt;
-  const int m0 = mt * BM, n0 = (tile / gmt) * BN;
+  float* out = p.out + static_cast<size_t>(view) * (1 + p.n_register + p.M) * p.N;
+  int mt = tile % gmt;
+  int m0 = mt * kGm, n0 = (tile / gmt) * kGn;
+  // computed once: the epilogue would otherwise redo the divisions
+  asm volatile("" : "+s"(out), "+s"(mt), "+s"(m0), "+s"(n0));
 
-  // Patch row R of the tile (0..671): each group of 32 rows is 16 patches x
-  // 2 pixel rows, m = 16 (g % 3) + R % 16 and ky = 2 (g / 3) + (R / 16) % 2
-  // with g = R / 32.  A half-wave then reads two pixel rows of 16 adjacent
-  // patches, and its 8-byte LDS writes (row pitch 596 = 20 mod 64 banks,
-  // the second pixel row 42 = 2 mod 4 banks further) hit all 64 banks once.
-  // Rows with ky < 8 are exactly R < 384.
-  auto row_m = [](int r) { return 16 * ((r >> 5) % 3) + (r & 15); };
-  auto row_ky = [](int r) { return 2 * ((r >> 5) / 3) + ((r >> 4) & 1); };
-  // byte offset of a patch row (patches past the image clamp to the last
-  // one: their rows compute values that are never stored)
-  auto row_start = [&](int r) {
-    const int gm = m0 + row_m(r);
+  // 1. patch row (m, ky) = (tid % 32, tid / 32) for tid < 448 (patches past
+  // the image clamp to the last one: their rows are never stored)
+  const bool stg = tid < kGm * kPatch;
+  PatchRow row;
+  if (stg) {
+    const int gm = m0 + (tid & 31);
     const int cm = gm < p.M ? gm : p.M - 1;
     const uint32_t py = vkd::fdiv(static_cast<uint32_t>(cm), p.fgw);
     const uint32_t px = static_cast<uint32_t>(cm) - py * static_cast<uint32_t>(p.gw);
-    return ((py * kPatch + row_ky(r)) * static_cast<uint32_t>(p.W) + px * kPatch) * 3u;
-  };
-  auto row_dst = [&](int r) {
-    return reinterpret_cast<float2*>(As + row_m(r) * kPePitch + row_ky(r) * kPeRowBytes);
-  };
-
-  // 1. gather.  Stage A (rows 0..383, ky < 8): thread tid holds row tid.
-  // Stage B (rows 384..671): staging thread t = tid - 512 holds rows 384 + t
-  // and, for t < 32, 640 + t.
-  PatchRow row_a, row_b0, row_b1;
-  const int tb = tid - kThreads;
-  const int rb0 = kPeRowsA + (tb >= 0 ? tb : 0);
-  const int rb1 = kPeRowsA + kPeStagers +
-                  (tb >= 0 && tb < kPeRowsB - kPeStagers ? tb : kPeRowsB - kPeStagers - 1);
-  if (tid < kPeRowsA) row_a.load(img, row_start(tid), p.img_bytes);
-  if (stager) {
-    row_b0.load(img, row_start(rb0), p.img_bytes);
-    row_b1.load(img, row_start(rb1), p.img_bytes);
+    row.load(img, ((py * kPatch + (tid >> 5)) * static_cast<uint32_t>(p.W) + px * kPatch) * 3u,
+             p.img_bytes);
   }
 
-  // 2. B fragments (compute waves).  Block sequence: waves 0-3 run blocks
-  // 0-10 then 21-28, waves 4-7 blocks 11-20 then 29-36.
-  // Positions 0-9 run in phase 1 and 10-17 in phase 2 in both halves, so
-  // their code (and the B loads in it) is the same for every wave; waves 0-3
-  // run their 19th block, stage-A block 10, last.
-  const int first1 = half ? kPePhase1 + 1 : 0;
-  const int first2 = kPeBlocksA + half * kPePhase2;
-  auto seq_block = [&](int s) {
-    return s < kPePhase1 ? first1 + s
-                         : (s < kPePhase1 + kPePhase2 ? first2 + s - kPePhase1 : kPePhase1);
-  };
-  const int col = n0 + strip * 16 + (lane & 15);
-  const int ccol = col < p.N ? col : p.N - 1;
-  const float* wrow = p.wpk + static_cast<size_t>(ccol) * kPeKp + 4 * (lane >> 4);
-  f32x4 bf[kPeSeq];
-  auto load_b = [&](int s) {
-    if (s < kPeSeq) bf[s] = *reinterpret_cast<const f32x4*>(wrow + 16 * seq_block(s));
-  };
-
-  // 3. (v/255 - mean[c]) / std[c], exactly as the scalar normalisation (one
-  // entry per thread), and zeros in the K padding 588..591
-  {
-    const int c = tid / 256, v = tid % 256;
+  // 2. the table, exactly (v/255 - mean[c]) / std[c] (mean and std taken
+  // from the scalar arguments: an indexed load of them would wait behind the
+  // image rows), and its zero entry
+  float mean[3], sd[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    mean[c] = p.mean[c];
+    sd[c] = p.sd[c];
+    asm volatile("" : "+s"(mean[c]), "+s"(sd[c]));  // kept in SGPRs, not reloaded
+  }
+  for (int e = tid; e < 3 * 256; e += kGThreads) {
+    const int c = e / 256, v = e % 256;
+    const float mc = c == 0 ? mean[0] : (c == 1 ? mean[1] : mean[2]);
+    const float sc = c == 0 ? sd[0] : (c == 1 ? sd[1] : sd[2]);
     const float u = static_cast<float>(v) / 255.0f;
-    lut[tid] = (u - p.mean[c]) / p.sd[c];
+    lut[e] = (u - mc) / sc;
   }
-  if (tid < BM * 4) As[(tid >> 2) * kPePitch + kPeK + (tid & 3)] = 0.0f;
-  __syncthreads();  // LUT visible
+  if (tid == 0) lut[kGZero] = 0.0f;
 
-  // 4. stage A into LDS; the first B fragments load meanwhile (they are not
-  // needed before phase 1, and issuing them earlier delays the barrier above)
-  if (!stager) {
+  // 3. B fragments of this wave's three column strips, first blocks
+  const float* wrow[3][2];
 #pragma unroll
-    for (int s = 0; s < kPeAhead; ++s) load_b(s);
+  for (int cs = 0; cs < 3; ++cs) {
+    const int col = n0 + 48 * cg + 16 * cs + (lane & 15);
+    const int ccol = col < p.N ? col : p.N - 1;
+    const float* w = p.wpk + static_cast<size_t>(ccol) * kPeKp + 4 * g;
+    wrow[cs][0] = w + 16 * first1;
+    wrow[cs][1] = w + 16 * first2;
   }
-  if (tid < kPeRowsA) {
-    row_a.align();
-    row_a.store(row_dst(tid), lut, 0, kPeRowBytes / 2);
-  }
-  __syncthreads();
-
-  // 5. phase 1: compute waves run stage-A blocks, staging waves stage B
-  f32x4 acc[3];
+  // position s's operand: segment base + immediate offset (position 18 is
+  // block 10 from the first segment's base, which is block 0 in half 0)
+  auto seg = [](int s) { return s < kGSeg ? 0 : (s < kGSeg2 ? 1 : 0); };
+  auto off = [](int s) { return s < kGSeg ? s : (s < kGSeg2 ? s - kGSeg : kPePhase1); };
+  auto valid = [&](int s) { return s < kGSeg2 || (s < kPeSeq && len == kPeSeq); };
+  f32x4 bf[kPeSeq][3];
+  auto load_b = [&](int s) {
+    if (valid(s)) {
 #pragma unroll
-  for (int t = 0; t < 3; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float* arow = As + (lane & 15) * kPePitch + 4 * (lane >> 4);
-  // A fragments run two blocks ahead of their MFMAs and B eight; the
-  // scheduling barrier keeps each block's prefetch loads where they are
-  // written (the scheduler otherwise sinks them next to their use)
-  struct AFrag {
-    f32x4 a[3];
-  };
-  auto load_a = [&](int s, AFrag& f) {
-    const float* q = arow + 16 * seq_block(s);
-#pragma unroll
-    for (int t = 0; t < 3; ++t) f.a[t] = *reinterpret_cast<const f32x4*>(q + t * 16 * kPePitch);
-  };
-  auto mma = [&](const AFrag& f, const f32x4& b) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int t = 0; t < 3; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[t][j], b[j], acc[t], 0, 0, 0);
-  };
-  // positions s0 <= s < s1 of the sequence
-  auto run_blocks = [&](auto s0c, auto s1c) {
-    constexpr int s0 = decltype(s0c)::value, s1 = decltype(s1c)::value;
-    AFrag f0, f1, f2;
-    load_a(s0, f0);
-    if (s0 + 1 < s1) load_a(s0 + 1, f1);
-#pragma unroll
-    for (int s = s0; s < s1; ++s) {
-      if (s + 2 < s1) load_a(s + 2, f2);
-      load_b(s + kPeAhead);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f0, bf[s]);
-      f0 = f1;
-      f1 = f2;
+      for (int cs = 0; cs < 3; ++cs)
+        bf[s][cs] = *reinterpret_cast<const f32x4*>(wrow[cs][seg(s)] + 16 * off(s));
     }
   };
-  if (stager) {
-    row_b0.align();
-    row_b0.store(row_dst(rb0), lut, 0, kPeRowBytes / 2);
-    if (tb < kPeRowsB - kPeStagers) {
-      row_b1.align();
-      row_b1.store(row_dst(rb1), lut, 0, kPeRowBytes / 2);
+#pragma unroll
+  for (int s = 0; s < kGAhead; ++s) load_b(s);
+
+  // 4. the address tile: row (m, ky)'s 42 bytes -> byte offsets 4 v + 1024 c
+  // at element m * pitch + 42 ky (c = byte % 3: k = ky*42 + kx*3 + c); the
+  // other threads point the K padding 588..591 at the zero entry
+  if (stg) {
+    row.align();
+    if constexpr (U16) {
+      u32_alias* dst =
+          reinterpret_cast<u32_alias*>(At + (tid & 31) * kPitch + (tid >> 5) * kPeRowBytes);
+#pragma unroll
+      for (int q = 0; q < kPeRowBytes / 2; ++q) {
+        // bytes 2q, 2q+1 into the two u16 halves (one byte permute), then
+        // times 4 plus both channels' table offsets
+        const int b = 2 * q;
+        const uint32_t v01 =
+            __builtin_amdgcn_perm(0u, row.w[b >> 2], (b & 3) == 0 ? 0x0c010c00u : 0x0c030c02u);
+        dst[q] = (v01 << 2) | ((1024u * (b % 3)) | ((1024u * ((b + 1) % 3)) << 16));
+      }
+    } else {
+      Addr* dst = At + (tid & 31) * kPitch + (tid >> 5) * kPeRowBytes;
+#pragma unroll
+      for (int b = 0; b < kPeRowBytes; ++b)
+        dst[b] = 4u * ((row.w[b >> 2] >> (8 * (b & 3))) & 0xffu) + 1024u * (b % 3);
     }
   } else {
-    run_blocks(std::integral_constant<int, 0>{}, std::integral_constant<int, kPePhase1>{});
+    const int t = tid - kGm * kPatch;
+    if (t < 2 * kGm) {
+      Addr* pad = At + (t & 31) * kPitch + kPeK + 2 * (t >> 5);
+      pad[0] = 4u * kGZero;
+      pad[1] = 4u * kGZero;
+    }
   }
   __syncthreads();
-  if (stager) {
-    __syncthreads();  // the split-K reduction's barrier
-    return;
-  }
 
-  // 6. epilogue operands, loaded now so their latency hides behind the MFMAs
-  float bias = 0.0f;
+  // 5. MFMAs: element k = 16 b + 4 g + j of patch m = lane % 16 has its
+  // address at arow[16 b + j]
+  const Addr* const arow0 = At + (16 * rs + (lane & 15)) * kPitch + 4 * g;
+  const Addr* const arow[2] = {arow0 + 16 * first1, arow0 + 16 * first2};
+  const char* lutb = reinterpret_cast<const char*>(lut);
+  f32x4 acc[3];
+#pragma unroll
+  for (int cs = 0; cs < 3; ++cs) acc[cs] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t ad[kPeSeq][4];
+  float av[kPeSeq][4];
+  uint2 raw[kPeSeq];
+  // u16: four addresses in one 64-bit read, split one block later (so the
+  // split does not wait for the read); u32: one 128-bit read
+  auto load_raw = [&](int s) {
+    if constexpr (U16) {
+      if (valid(s)) raw[s] = *reinterpret_cast<const uint2*>(arow[seg(s)] + 16 * off(s));
+    }
+  };
+  auto load_ad = [&](int s) {
+    if (valid(s)) {
+      if constexpr (U16) {
+        ad[s][0] = raw[s].x & 0xffffu;
+        ad[s][1] = raw[s].x >> 16;
+        ad[s][2] = raw[s].y & 0xffffu;
+        ad[s][3] = raw[s].y >> 16;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ad[s][j] = arow[seg(s)][16 * off(s) + j];
+      }
+    }
+  };
+  auto gather = [&](int s) {
+    if (valid(s)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) av[s][j] = *reinterpret_cast<const float*>(lutb + ad[s][j]);
+    }
+  };
+  float bias[3] = {0.f, 0.f, 0.f};
   float addend[3][4];
-  if (half == 0) {
-    bias = p.bias[ccol];
+  auto load_epilogue = [&]() {
 #pragma unroll
-    for (int t = 0; t < 3; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
-        const int crow = row < p.M ? row : p.M - 1;
-        addend[t][r] = p.pos[static_cast<size_t>(1 + crow) * p.N + ccol];
-      }
-  }
-
-  // 7. phase 2: stage-B blocks, then waves 0-3's last block
-  run_blocks(std::integral_constant<int, kPePhase1>{},
-             std::integral_constant<int, kPePhase1 + kPePhase2>{});
-  if (half == 0) {
-    AFrag f;
-    load_a(kPeSeq - 1, f);
-    mma(f, bf[kPeSeq - 1]);
-  }
-
-  if (!reduce_halves(red, strip, half, lane, acc)) return;
-
-  // 8. epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile
-  if (col < p.N) {
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
+    for (int cs = 0; cs < 3; ++cs) {
+      const int col = n0 + 48 * cg + 16 * cs + (lane & 15);
+      const int ccol = col < p.N ? col : p.N - 1;
+      bias[cs] = p.bias[ccol];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + t * 16 + 4 * (lane >> 4) + r;
-        if (row < p.M)
-          out[static_cast<size_t>(1 + p.n_register + row) * p.N + col] =
-              (acc[t][r] + bias) + addend[t][r];
+        const int rw = m0 + 16 * rs + 4 * g + r;
+        const int crow = rw < p.M ? rw : p.M - 1;
+        addend[cs][r] = p.pos[static_cast<size_t>(1 + crow) * p.N + ccol];
       }
+    }
+  };
+  auto mma = [&](int s) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int cs = 0; cs < 3; ++cs)
+        acc[cs] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s][j], bf[s][cs][j], acc[cs], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Each block's MFMAs come first and the LDS reads of later blocks after
+  // them: LDS reads complete in issue order, so a read issued just before
+  // the MFMAs would hold them up.
+#pragma unroll
+  for (int s = 0; s <= kGLook + 1; ++s) load_raw(s);
+#pragma unroll
+  for (int s = 0; s <= kGLook; ++s) load_ad(s);
+#pragma unroll
+  for (int s = 0; s < kGLook; ++s) gather(s);
+#pragma unroll
+  for (int s = 0; s < kGSeg2; ++s) {
+    mma(s);
+    load_raw(s + kGLook + 2);
+    load_ad(s + kGLook + 1);
+    gather(s + kGLook);
+    load_b(s + kGAhead);
+    if (s == kPeSeq - kGAhead - 1 && half == 0) load_epilogue();
   }
-  if (mt == 0) {
-    // special rows of this column strip, four rows per pass (one per lane
-    // group): row 0 = CLS + pos[0], rows 1.. = registers
+  if (len == kPeSeq) mma(kGSeg2);  // half 0's position 18: block 10
+
+  // 6. the k halves meet: half 1 hands its sums to half 0
+  const int pair = rs + 2 * cg;
+  if (half == 1) {
+#pragma unroll
+    for (int cs = 0; cs < 3; ++cs)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[(pair * 12 + cs * 4 + r) * 64 + lane] = acc[cs][r];
+  }
+  __syncthreads();
+  if (half == 1) return;
+#pragma unroll
+  for (int cs = 0; cs < 3; ++cs)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[cs][r] += red[(pair * 12 + cs * 4 + r) * 64 + lane];
+
+  // 7. epilogue: lane holds D[4 g + r][lane % 16] of each 16x16 tile
+#pragma unroll
+  for (int cs = 0; cs < 3; ++cs) {
+    const int col = n0 + 48 * cg + 16 * cs + (lane & 15);
+    if (col < p.N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rw = m0 + 16 * rs + 4 * g + r;
+        if (rw < p.M)
+          out[static_cast<size_t>(1 + p.n_register + rw) * p.N + col] =
+              (acc[cs][r] + bias[cs]) + addend[cs][r];
+      }
+    }
+  }
+  if (mt == 0 && rs == 0) {
+    // special rows of this wave's 48 columns, four rows per pass (one per
+    // lane group): row 0 = CLS + pos[0], rows 1.. = registers
     for (int r0 = 0; r0 <= p.n_register; r0 += 4) {
-      const int r = r0 + (lane >> 4);
-      if (r <= p.n_register && col < p.N)
-        out[static_cast<size_t>(r) * p.N + col] =
-            r == 0 ? p.cls[col] + p.pos[col] : p.regs[static_cast<size_t>(r - 1) * p.N + col];
+      const int r = r0 + g;
+#pragma unroll
+      for (int cs = 0; cs < 3; ++cs) {
+        const int col = n0 + 48 * cg + 16 * cs + (lane & 15);
+        if (r <= p.n_register && col < p.N)
+          out[static_cast<size_t>(r) * p.N + col] =
+              r == 0 ? p.cls[col] + p.pos[col] : p.regs[static_cast<size_t>(r - 1) * p.N + col];
+      }
     }
   }
 }
@@ -349,8 +447,8 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_kernel(PatchArgs p) {
 // LDS buffer; the half that adds and stores alternates from tile to tile,
 // so one barrier per tile suffices (a wave that writes the buffer in one
 // tile read it in the previous one).  Every output element takes
-// patch_embed_kernel's block sequence, k-half split and epilogue order: the
-// same bits.
+// block sequence, k-half split and epilogue order above: the same bits as
+// the gathered kernel.
 // ---------------------------------------------------------------------------
 constexpr int kPp = 32;                  // patches per tile
 constexpr int kPpRows = kPp * kPatch;    // 448 patch rows
@@ -380,7 +478,7 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
   const int nvm = (t1 - 1) / gnt - vm0 + 1;   // M tiles in the range
 
   // Patch row R of an M tile (0..447): groups of 32 rows are 16 patches x 2
-  // pixel rows (the staging writes' bank pattern of patch_embed_kernel):
+  // pixel rows (so a half-wave's 8-byte LDS writes hit all 64 banks once):
   // m = 16 ((R / 32) % 2) + R % 16, ky = 2 (R / 64) + (R / 16) % 2.
   auto row_m = [](int r) { return 16 * ((r >> 5) & 1) + (r & 15); };
   auto row_ky = [](int r) { return 2 * (r >> 6) + ((r >> 4) & 1); };
@@ -439,7 +537,7 @@ __global__ __launch_bounds__(kPeThreads) void patch_embed_pipelined_kernel(Patch
   }
 
   // the compute waves' B fragments: column strip of the tile, block
-  // sequence of patch_embed_kernel (waves 0-3: blocks 0-9, 21-28, 10; waves
+  // sequence above (waves 0-3: blocks 0-9, 21-28, 10; waves
   // 4-7: 11-20, 29-36), kPpAhead blocks ahead of the MFMAs
   const int first1 = half ? kPePhase1 + 1 : 0;
   const int first2 = kPeBlocksA + half * kPePhase2;
@@ -843,25 +941,32 @@ int vk_patch_embed_views_u8(vk_runtime* rt, const vk_tensor* images, size_t view
     a.mean[c] = mean[c];
     a.sd[c] = std_[c];
   }
-  const long long tiles = static_cast<long long>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  VK_UNSUPPORTED_IF(tiles * static_cast<long long>(views) > 0x7fffffffLL,
-                    "patch_embed_u8: %lld tiles", tiles * static_cast<long long>(views));
   a.views = static_cast<int>(views);
+  const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
 #if VK_PE_PIPELINED
   const long long tiles32 =
       static_cast<long long>((a.M + kPp - 1) / kPp) * ((a.N + BN - 1) / BN);
-  const long long cus = rt->cu_count > 0 ? rt->cu_count : 256;
   if (views > 1 && tiles32 * static_cast<long long>(views) > cus) {
+    VK_UNSUPPORTED_IF(tiles32 * static_cast<long long>(views) > 0x7fffffffLL,
+                      "patch_embed_u8: %lld tiles", tiles32 * static_cast<long long>(views));
     a.tiles = static_cast<int>(tiles32);
     hipLaunchKernelGGL(patch_embed_pipelined_kernel, dim3(static_cast<unsigned>(cus)),
                        dim3(kPeThreads), 0, rt->stream, a);
     return vk::check_launch("patch_embed_pipelined_kernel");
   }
 #endif
-  a.tiles = static_cast<int>(tiles);
-  hipLaunchKernelGGL(patch_embed_kernel, dim3(static_cast<unsigned>(tiles * views)),
-                     dim3(kPeThreads), 0, rt->stream, a);
-  return vk::check_launch("patch_embed_kernel");
+  // one round of tiles: u32 addresses; several rounds: u16 (two workgroups
+  // per CU)
+  const long long gtiles = static_cast<long long>((a.M + kGm - 1) / kGm) * ((a.N + kGn - 1) / kGn);
+  VK_UNSUPPORTED_IF(gtiles * static_cast<long long>(views) > 0x7fffffffLL,
+                    "patch_embed_u8: %lld tiles", gtiles * static_cast<long long>(views));
+  a.tiles = static_cast<int>(gtiles);
+  const dim3 grid(static_cast<unsigned>(gtiles * views));
+  if (gtiles * static_cast<long long>(views) <= cus)
+    hipLaunchKernelGGL(patch_embed_gather_kernel<false>, grid, dim3(kGThreads), 0, rt->stream, a);
+  else
+    hipLaunchKernelGGL(patch_embed_gather_kernel<true>, grid, dim3(kGThreads), 0, rt->stream, a);
+  return vk::check_launch("patch_embed_gather_kernel");
 }
 
 int vk_patch_embed_u8(vk_runtime* rt, const vk_tensor* img_hwc, size_t h, size_t w,
