@@ -245,15 +245,21 @@ __global__ __launch_bounds__(kGThreads) void patch_embed_gather_kernel(PatchArgs
   }
   if (tid == 0) lut[kGZero] = 0.0f;
 
-  // 3. B fragments of this wave's three column strips, first blocks
-  const float* wrow[3][2];
+  // 3. B fragments of this wave's three column strips, first blocks: raw
+  // buffer loads (a lane byte offset per strip and segment, the block's
+  // offset an immediate), which hold up the MFMA issue less than 64-bit
+  // address loads (a microbenchmark of this loop: 34.2 against 36.8 cycles
+  // per MFMA with three fragment loads per 12 MFMAs)
+  const __amdgpu_buffer_rsrc_t wsrc =
+      vkd::buffer_rsrc(p.wpk, static_cast<uint32_t>(p.N) * kPeKp * 4u);
+  uint32_t wrow[3][2];
 #pragma unroll
   for (int cs = 0; cs < 3; ++cs) {
     const int col = n0 + 48 * cg + 16 * cs + (lane & 15);
-    const int ccol = col < p.N ? col : p.N - 1;
-    const float* w = p.wpk + static_cast<size_t>(ccol) * kPeKp + 4 * g;
-    wrow[cs][0] = w + 16 * first1;
-    wrow[cs][1] = w + 16 * first2;
+    const uint32_t ccol = static_cast<uint32_t>(col < p.N ? col : p.N - 1);
+    const uint32_t w = (ccol * kPeKp + 4 * g) * 4u;
+    wrow[cs][0] = w + 64u * first1;
+    wrow[cs][1] = w + 64u * first2;
   }
   // position s's operand: segment base + immediate offset (position 18 is
   // block 10 from the first segment's base, which is block 0 in half 0)
@@ -265,7 +271,7 @@ __global__ __launch_bounds__(kGThreads) void patch_embed_gather_kernel(PatchArgs
     if (valid(s)) {
 #pragma unroll
       for (int cs = 0; cs < 3; ++cs)
-        bf[s][cs] = *reinterpret_cast<const f32x4*>(wrow[cs][seg(s)] + 16 * off(s));
+        bf[s][cs] = __builtin_bit_cast(f32x4, vkd::buffer_load4(wsrc, wrow[cs][seg(s)], 64u * off(s)));
     }
   };
 #pragma unroll
@@ -916,6 +922,8 @@ int vk_patch_embed_views_u8(vk_runtime* rt, const vk_tensor* images, size_t view
              "out must be f32 [views*(1+n_register+gh*gw)*embed=%zu] (got %zu)",
              views * (1 + n_register + np) * embed, out->len);
   VK_UNSUPPORTED_IF(h * w * 3 > 0x7fffffffULL || np > 0x7fffffffULL, "image too large");
+  // the filter is read through a buffer descriptor of 32-bit byte size
+  VK_UNSUPPORTED_IF(embed * kPeKp * 4 > 0x7fffffffULL, "patch_embed_u8: embed=%zu", embed);
   for (int c = 0; c < 3; ++c) VK_REQUIRE(std_[c] != 0.0f, "std[%d] is zero", c);
   VK_REQUIRE(proj->weight_patch != nullptr, "projection has no patch-order filter");
   // every view's rows are read as aligned 8-byte words
