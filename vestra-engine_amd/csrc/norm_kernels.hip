@@ -579,8 +579,8 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_rows(
       op[2 * p] = qk_row_operands<PT, HAS_NORM, POS, PAIR>(l, qg, qb, py, px, table, sh.table_max);
       op[2 * p + 1] = op[2 * p];
       if (HAS_NORM) {
-        op[2 * p + 1].g = vkd::Param<PT>::load4(kg, l);
-        op[2 * p + 1].b = vkd::Param<PT>::load4(kb, l);
+        op[2 * p + 1].g = qk_param4(kg, l);
+        op[2 * p + 1].b = qk_param4(kb, l);
       }
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -137,6 +137,26 @@ __device__ __forceinline__ void qk_row_position(uint32_t r, const QkShape& sh,
 // frequencies with rotate-half pairing, two with interleaved pairing).
 // Loading them is a stage of its own, so a caller holding several rows can
 // issue every row's loads before any row's arithmetic.
+// A lane's four LayerNorm parameters (64 per row, F32 or F16) by a raw
+// buffer load: a buffer load holds up the wave's other instructions less
+// than a 64-bit address load (measured on this kernel: 23.6 against 24.1 us
+// at 12 views of 10,392 rows).
+template <typename PT>
+__device__ __forceinline__ float4 qk_param4(const PT* p, int l) {
+  const __amdgpu_buffer_rsrc_t r = vkd::buffer_rsrc(p, 64 * sizeof(PT));
+  if constexpr (sizeof(PT) == 4) {
+    return vkd::buffer_load4(r, 16u * l, 0);
+  } else {
+    typedef int i32x2_t __attribute__((ext_vector_type(2)));
+    const i32x2_t h = __builtin_amdgcn_raw_buffer_load_b64(r, 8 * l, 0, 0);
+    const uint32_t a = static_cast<uint32_t>(h.x), b = static_cast<uint32_t>(h.y);
+    return make_float4(vkd::f16_to_f32(static_cast<uint16_t>(a & 0xffffu)),
+                       vkd::f16_to_f32(static_cast<uint16_t>(a >> 16)),
+                       vkd::f16_to_f32(static_cast<uint16_t>(b & 0xffffu)),
+                       vkd::f16_to_f32(static_cast<uint16_t>(b >> 16)));
+  }
+}
+
 struct QkRowOperands {
   float4 g, b;  // LayerNorm parameters (unused without the norm)
   float4 c, s;  // cos/sin: components 0..3 (rotate-half) or 0..1 (interleaved)
@@ -150,8 +170,8 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
                                                          int table_max) {
   QkRowOperands o;
   if (HAS_NORM) {
-    o.g = vkd::Param<PT>::load4(g, l);
-    o.b = vkd::Param<PT>::load4(b, l);
+    o.g = qk_param4(g, l);
+    o.b = qk_param4(b, l);
   }
   // lanes 0-7 rotate by the row coordinate, lanes 8-15 by the column
   // the coordinate is an integral f32: an entry of the table when it lies
@@ -159,12 +179,15 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
   const float coord = (l < 8) ? py : px;
   const bool in_table =
       POS == kPosGrid || (coord >= 0.0f && coord <= static_cast<float>(table_max));
-  const float* e = table + static_cast<size_t>(in_table ? static_cast<int>(coord) : 0) * 32;
+  const uint32_t eo = static_cast<uint32_t>(in_table ? static_cast<int>(coord) : 0) * 128u;
   if (PAIR == kRotateHalf) {
     const int j0 = (l & 3) * 4;  // frequencies j0..j0+3
     if (in_table) {
-      o.c = *reinterpret_cast<const float4*>(e + j0);
-      o.s = *reinterpret_cast<const float4*>(e + 16 + j0);
+      // the table row by raw buffer loads, like the parameters
+      const __amdgpu_buffer_rsrc_t tr =
+          vkd::buffer_rsrc(table, static_cast<uint32_t>(table_max + 1) * 32u * 4u);
+      o.c = vkd::buffer_load4(tr, eo + 4u * j0, 0);
+      o.s = vkd::buffer_load4(tr, eo + 4u * j0, 64);
     } else {
       const RopeCs cs = rope_cs_slow<4>(table, table_max, coord, j0);
       o.c = cs.c;
@@ -174,8 +197,12 @@ __device__ __forceinline__ QkRowOperands qk_row_operands(int l, const PT* __rest
     const int j0 = (l & 7) * 2;  // frequencies j0, j0+1
     float2 c, sn;
     if (in_table) {
-      c = *reinterpret_cast<const float2*>(e + j0);
-      sn = *reinterpret_cast<const float2*>(e + 16 + j0);
+      typedef int i32x2_t __attribute__((ext_vector_type(2)));
+      const __amdgpu_buffer_rsrc_t tr =
+          vkd::buffer_rsrc(table, static_cast<uint32_t>(table_max + 1) * 32u * 4u);
+      c = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(tr, eo + 4u * j0, 0, 0));
+      sn = __builtin_bit_cast(float2,
+                              __builtin_amdgcn_raw_buffer_load_b64(tr, eo + 4u * j0, 64, 0));
     } else {
       const RopeCs cs = rope_cs_slow<2>(table, table_max, coord, j0);
       c = make_float2(cs.c.x, cs.c.y);
