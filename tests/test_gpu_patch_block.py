@@ -336,6 +336,33 @@ def test_patch_embed_u8_matches_oracle(rt, rng, h, w, embed, n_register):
                       f"patch_embed {h}x{w}")
 
 
+def test_patch_embed_u8_several_rounds_partial_tiles(rt, rng):
+    """700x840 (3,000 patches: the last 32-patch tile holds 24) with 200
+    outputs (the last 96-column tile holds 8): 94 x 3 = 282 tiles, more
+    than one round of CUs, so the gathered kernel runs with u16 table
+    addresses; rows and columns past the tile edges are computed on clamped
+    data and never stored."""
+    h, w, embed, n_register = 700, 840, 200, 2
+    gh, gw = h // 14, w // 14
+    img = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    wt = normals(rng, embed, 3, 14, 14, scale=0.02)
+    b = normals(rng, embed, scale=0.02)
+    cls = normals(rng, embed, scale=0.02)
+    regs = normals(rng, n_register, embed, scale=0.02)
+    pos = normals(rng, 1 + gh * gw, embed, scale=0.02)
+    proj = rt.prepare_linear_oihw_f32(588, embed, wt, b)
+    out = rt.upload_f32(np.full((1 + n_register + gh * gw) * embed, np.nan, np.float32))
+    rt.patch_embed_u8(rt.upload_u8(img), h, w, 14, MEAN, STD, proj, rt.upload_f32(cls),
+                      rt.upload_f32(regs), n_register, rt.upload_f32(pos), out)
+    ref = oracle.patch_embed_u8(img, 14, MEAN, STD, wt, b, cls, regs, pos)
+    got = out.numpy().reshape(ref.shape)
+    assert np.array_equal(got[:1 + n_register], ref[:1 + n_register])
+    a = np.abs(oracle.patchify_nchw(oracle.normalize_u8_hwc(img, MEAN, STD), 14)).astype(np.float64)
+    scale = a @ np.abs(wt.reshape(embed, -1)).astype(np.float64).T
+    assert_dot_parity(got[1 + n_register:], ref[1 + n_register:], scale, 588,
+                      "patch_embed 700x840, 200 outputs")
+
+
 def test_patch_embed_f16_filter_vitl_matches_oracle(rt, rng):
     """ViT-L at 1008x672 with the patch filter stored as F16 (GGUF F16
     element layout) and widened on the device: the oracle runs on the same
