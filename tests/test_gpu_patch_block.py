@@ -363,6 +363,37 @@ def test_patch_embed_u8_several_rounds_partial_tiles(rt, rng):
                       "patch_embed 700x840, 200 outputs")
 
 
+@pytest.mark.parametrize("h,w,embed", [(336, 504, 768), (672, 1008, 1024)])
+def test_patch_embed_graph_replays(rt, rng, h, w, embed):
+    """The fused patch embedding captured in a HIP graph (one round of tiles:
+    u32 table addresses; several: u16) replays with the eager bits, replay
+    after replay, with eager work on the same stream in between."""
+    gh, gw = h // 14, w // 14
+    rows = 1 + 1 + gh * gw
+    img = rt.upload_u8(rng.integers(0, 256, (h, w, 3), dtype=np.uint8))
+    proj = rt.prepare_linear_oihw_f32(588, embed, normals(rng, embed, 3, 14, 14, scale=0.02),
+                                      normals(rng, embed, scale=0.02))
+    cls = rt.upload_f32(normals(rng, embed, scale=0.02))
+    regs = rt.upload_f32(normals(rng, embed, scale=0.02))
+    pos = rt.upload_f32(normals(rng, 1 + gh * gw, embed, scale=0.02))
+    eager = rt.alloc_f32(rows * embed)
+    rt.patch_embed_u8(img, h, w, 14, MEAN, STD, proj, cls, regs, 1, pos, eager)
+    want = eager.numpy()
+    out = rt.alloc_f32(rows * embed)
+    rt.synchronize()
+    rt.begin_capture()
+    try:
+        rt.patch_embed_u8(img, h, w, 14, MEAN, STD, proj, cls, regs, 1, pos, out)
+    finally:
+        graph = rt.end_capture()
+    junk = rt.upload_f32(np.ones(rows * embed, np.float32))
+    for r in range(3):
+        graph.launch()
+        rt.synchronize()
+        assert np.array_equal(out.numpy(), want), f"replay {r}"
+        rt.add_f32_in_place(out, junk)  # eager work between the replays
+
+
 def test_patch_embed_f16_filter_vitl_matches_oracle(rt, rng):
     """ViT-L at 1008x672 with the patch filter stored as F16 (GGUF F16
     element layout) and widened on the device: the oracle runs on the same
