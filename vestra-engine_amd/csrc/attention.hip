@@ -49,14 +49,40 @@ constexpr float kQScale = 0.125f * 1.44269504088896341f;  // log2(e) / sqrt(64)
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1, "pitch 4 x odd");
 static_assert(PITCH % 16 == 4, "transposed V stores: 16 (l >> 4) + (l & 15) covers 64 banks");
 
+// Max and sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups
+// of one query column).  v_permlane16_swap / v_permlane32_swap with both
+// operands v leave each lane its own value and that of lane l ^ 16 (l ^ 32)
+// in the two results: a VALU exchange, with no LDS round trip.  Both
+// operations are commutative, so the result has the bits of the butterfly
+// v op shfl_xor(v, 16), then op shfl_xor(., 32).
+__device__ __forceinline__ float xor16_pair(float v, float* other) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  *other = __uint_as_float(r[1]);
+  return __uint_as_float(r[0]);
+}
+
+__device__ __forceinline__ float xor32_pair(float v, float* other) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  *other = __uint_as_float(r[1]);
+  return __uint_as_float(r[0]);
+}
+
 __device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  float o;
+  v = xor16_pair(v, &o);
+  v = fmaxf(v, o);
+  v = xor32_pair(v, &o);
+  return fmaxf(v, o);
 }
 
 __device__ __forceinline__ float group_sum(float v) {
-  v = v + __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  float o;
+  v = xor16_pair(v, &o);
+  v = v + o;
+  v = xor32_pair(v, &o);
+  return v + o;
 }
 
 // Four query groups of 16 (one wave each) per workgroup: 64 queries over
@@ -180,17 +206,27 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
     if (!live) continue;
 
     // S^T tiles: s[t][r] = score of query q0 + c16 with key k0 + 16t + 4g + r
-    f32x4 s[4];
+    // (K fragments of tile t + 1 are read while tile t's 16 MFMAs run)
+    f32x4 s[4], ka[2][4];
+#pragma unroll
+    for (int bd = 0; bd < 4; ++bd)
+      ka[0][bd] = *reinterpret_cast<const f32x4*>(karow + 16 * bd);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      if (t < 3) {
+#pragma unroll
+        for (int bd = 0; bd < 4; ++bd)
+          ka[(t + 1) & 1][bd] =
+              *reinterpret_cast<const f32x4*>(karow + (t + 1) * 16 * PITCH + 16 * bd);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int bd = 0; bd < 4; ++bd) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(karow + t * 16 * PITCH + 16 * bd);
+      for (int bd = 0; bd < 4; ++bd)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], qf[bd][j], s[t], 0, 0, 0);
-      }
+          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[t & 1][bd][j], qf[bd][j], s[t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (k0 + KB > n) {  // the last, partial block
 #pragma unroll
@@ -229,15 +265,26 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
       }
     }
     // O += P V: A = the lane's probabilities of key tile t, B = V^T rows
+    // (V^T fragments of column tile dt + 1 are read while dt's MFMAs run)
+    f32x4 vb[2][4];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int t = 0; t < 4; ++t) vb[0][t] = *reinterpret_cast<const f32x4*>(vtrow + 16 * t);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const f32x4 b = *reinterpret_cast<const f32x4*>(vtrow + dt * 16 * PITCH + 16 * t);
+    for (int dt = 0; dt < 4; ++dt) {
+      if (dt < 3) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          vb[(dt + 1) & 1][t] =
+              *reinterpret_cast<const f32x4*>(vtrow + (dt + 1) * 16 * PITCH + 16 * t);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[t][j], b[j], o[dt], 0, 0, 0);
-      }
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[t][j], vb[dt & 1][t][j], o[dt], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   if constexpr (PART) {
@@ -346,13 +393,16 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
   // workgroups per CU (at least two key blocks per split) and a second pass
   // merges the partial results.  Fuller grids split only where the last
   // round of workgroups leaves CUs unevenly loaded and a cost model puts the
-  // split at least 5% below the unsplit launch: the busiest CU runs
+  // split at least 1% below the unsplit launch: the busiest CU runs
   // ceil(tiles * s / CUs) workgroups of up to ceil(key blocks / s) blocks
   // (about 2.2 us per block of one of the four workgroups a CU holds), and a
   // split adds its partial results' traffic (s slices of rows x 66 floats
   // written and read back) and the merge pass (about 3 us).  ViT-L at 3,458
-  // rows (880 tiles of 55 blocks, 3.4 per CU): 2 splits; the 12-view layers
-  // stay unsplit.
+  // rows (880 tiles of 55 blocks, 3.4 per CU): 2 splits (425 us; unsplit
+  // 464); the 12-view global layer (1,956 tiles of 163 blocks, model 1.6%
+  // below unsplit): 3 splits (2,486 us; unsplit 2,582, 4 splits 2,528); the
+  // 12-view local layers (14 blocks per tile) stay unsplit (260 us; 3
+  // splits 288).
   const int cus = rt->cu_count > 0 ? rt->cu_count : 256;
   const long long tiles64 = static_cast<long long>(sequences) * ((n + 63) / 64);
   const int nkb = static_cast<int>((n + KB - 1) / KB);
@@ -371,7 +421,7 @@ int vk_attention_into_f32(vk_runtime* rt, const vk_tensor* q, const vk_tensor* k
       const long long load = (tiles64 * sp + cus - 1) / cus * ((nkb + sp - 1) / sp);
       const double us = kBlockUs * static_cast<double>(load) +
                         2.0 * sp * row_bytes / kBytesPerUs + kMergeUs;
-      if (us < best && us < 0.95 * unsplit) {
+      if (us < best && us < 0.99 * unsplit) {
         best = us;
         splits = sp;
       }
