@@ -104,10 +104,12 @@ def test_attention_large_scores_and_selection(rt, rng):
     assert np.allclose(got[0, 17], v[0, 250], rtol=0, atol=1e-6)
 
 
-@pytest.mark.parametrize("heads,n", [(12, 10392), (16, 3458)])
+@pytest.mark.parametrize("heads,n", [(12, 10392), (16, 3458), (12, 13856), (12, 20784)])
 def test_attention_full_size_sampled_rows(rt, rng, heads, n):
-    """Global layer of the 12-view ViT-B sequence (12 heads over 10,392 rows)
-    and the ViT-L 1008x672 image (16 heads over 3,458 rows): every head, 48
+    """Global layer of the 12-view ViT-B sequence (12 heads over 10,392 rows,
+    each query tile's key blocks in three splits), the ViT-L 1008x672 image
+    (16 heads over 3,458 rows, two splits) and the global layers of 16 and 24
+    views (13,856 and 20,784 rows: five and four splits): every head, 48
     sampled query rows (first, last, the special tokens, view boundaries)
     against float64 with the bound above."""
     q, k, v = (normals(rng, heads, n, 64) for _ in range(3))
