@@ -153,6 +153,9 @@ __device__ __forceinline__ void split_sums(const float* __restrict__ partial, si
 #pragma unroll
     for (int i = 0; i < NV; ++i) p[i][sp] = *reinterpret_cast<const f32x4*>(partial + slice + e[i]);
   }
+  // all loads issued before the first addition (the scheduler would
+  // otherwise roll them behind the additions, one round trip each)
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     acc[i] = p[i][0];
@@ -523,6 +526,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
   const size_t e = static_cast<size_t>(i4) * 4;
   const int row = static_cast<int>(e / g.N), col = static_cast<int>(e % g.N);
   const size_t es[1] = {e};
+  // the epilogue's loads before the partial sums' and every store: a load
+  // after a store to `out` would wait for it (the compiler cannot tell them
+  // apart)
+  const float4 bias = *reinterpret_cast<const float4*>(g.bias + col);
+  const float4 ls = g.ls ? *reinterpret_cast<const float4*>(g.ls + col)
+                         : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+  f32x4 old = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (EPI == kLinResidual) old = *reinterpret_cast<const f32x4*>(g.out + e);
   f32x4 accs[1];
   split_sums<1, SPB>(g.partial, static_cast<size_t>(mn), es, g.splits, accs);
   const f32x4 acc = accs[0];
@@ -533,10 +544,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
     if (which < 2) {
       const int c = col - which * embed;
       float4 v;
-      v.x = acc[0] + g.bias[col];
-      v.y = acc[1] + g.bias[col + 1];
-      v.z = acc[2] + g.bias[col + 2];
-      v.w = acc[3] + g.bias[col + 3];
+      v.x = acc[0] + bias.x;
+      v.y = acc[1] + bias.y;
+      v.z = acc[2] + bias.z;
+      v.w = acc[3] + bias.w;
       const float4 o = qk_head_row<QKN>(g, v, threadIdx.x & 15, which == 1, row);
       float* dst = (which == 0 ? g.q_out : g.k_out) +
                    (static_cast<size_t>(c >> 6) * g.M + row) * 64 + (c & 63);
@@ -544,12 +555,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearArgs g) {
       return;
     }
   }
-  f32x4 old = f32x4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (EPI == kLinResidual) old = *reinterpret_cast<const f32x4*>(g.out + e);
+  const float bj[4] = {bias.x, bias.y, bias.z, bias.w};
+  const float lj[4] = {ls.x, ls.y, ls.z, ls.w};
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    store_out<EPI, LAY>(g, row, col + j, acc[j], g.bias[col + j], g.ls ? g.ls[col + j] : 1.0f,
-                        old[j]);
+  for (int j = 0; j < 4; ++j) store_out<EPI, LAY>(g, row, col + j, acc[j], bj[j], lj[j], old[j]);
 }
 
 // Sum pass of a split-K linear with the residual epilogue, followed by the
@@ -564,40 +573,49 @@ __global__ __launch_bounds__(64) void splitk_residual_ln_kernel(LinearArgs g) {
   const size_t row = blockIdx.x;
   const size_t mn = static_cast<size_t>(g.M) * g.N;
   const size_t rb = row * g.N;
-  float4 vv[NV];
   size_t es[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) es[i] = rb + 4 * static_cast<size_t>(lane + 64 * i);
-  f32x4 accs[NV];
-  split_sums<NV, SPB>(g.partial, mn, es, g.splits, accs);
+  // Every load of the row -- the residual, bias, LayerScale and LayerNorm
+  // parameters, then the partial sums -- is issued before the first store:
+  // the compiler cannot tell the stores to `out` from the parameter
+  // pointers, so a load placed after a store would wait for it (one memory
+  // round trip per float4 column of the lane).
+  const PT* gm = static_cast<const PT*>(g.ln_gamma);
+  const PT* bt = static_cast<const PT*>(g.ln_beta);
+  f32x4 old[NV];
+  float4 bias[NV], lsv[NV], lg[NV], lb[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c4 = lane + 64 * i;
-    const size_t e = es[i];
+    old[i] = *reinterpret_cast<const f32x4*>(g.out + es[i]);
+    bias[i] = *reinterpret_cast<const float4*>(g.bias + 4 * c4);
+    lsv[i] = g.ls ? *reinterpret_cast<const float4*>(g.ls + 4 * c4)
+                  : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    lg[i] = vkd::Param<PT>::load4(gm, c4);
+    lb[i] = vkd::Param<PT>::load4(bt, c4);
+  }
+  f32x4 accs[NV];
+  split_sums<NV, SPB>(g.partial, mn, es, g.splits, accs);
+  float4 vv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
     const f32x4 acc = accs[i];
-    const f32x4 old = *reinterpret_cast<const f32x4*>(g.out + e);
-    const int col = 4 * c4;
     float4 v;
-    v.x = epi_value<kLinResidual>(g, acc[0], g.bias[col], g.ls ? g.ls[col] : 1.0f, old[0]);
-    v.y = epi_value<kLinResidual>(g, acc[1], g.bias[col + 1], g.ls ? g.ls[col + 1] : 1.0f,
-                                  old[1]);
-    v.z = epi_value<kLinResidual>(g, acc[2], g.bias[col + 2], g.ls ? g.ls[col + 2] : 1.0f,
-                                  old[2]);
-    v.w = epi_value<kLinResidual>(g, acc[3], g.bias[col + 3], g.ls ? g.ls[col + 3] : 1.0f,
-                                  old[3]);
-    *reinterpret_cast<float4*>(g.out + e) = v;
+    v.x = epi_value<kLinResidual>(g, acc[0], bias[i].x, lsv[i].x, old[i][0]);
+    v.y = epi_value<kLinResidual>(g, acc[1], bias[i].y, lsv[i].y, old[i][1]);
+    v.z = epi_value<kLinResidual>(g, acc[2], bias[i].z, lsv[i].z, old[i][2]);
+    v.w = epi_value<kLinResidual>(g, acc[3], bias[i].w, lsv[i].w, old[i][3]);
+    *reinterpret_cast<float4*>(g.out + es[i]) = v;
     vv[i] = v;
   }
   float mean, inv;
   vkd::row_mean_inv<NV, true>(vv, lane, g.N, g.ln_eps, &mean, &inv);
-  const PT* gm = static_cast<const PT*>(g.ln_gamma);
-  const PT* bt = static_cast<const PT*>(g.ln_beta);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c4 = lane + 64 * i;
     *reinterpret_cast<float4*>(g.ln_out + rb + 4 * static_cast<size_t>(c4)) =
-        vkd::ln_apply4(vv[i], mean, inv, vkd::Param<PT>::load4(gm, c4),
-                       vkd::Param<PT>::load4(bt, c4));
+        vkd::ln_apply4(vv[i], mean, inv, lg[i], lb[i]);
   }
 }
 
