@@ -49,9 +49,10 @@ constexpr int PITCH = 68;
 constexpr int kSlots = KB * HD / 4;  // float4 of one K (or V) block: 1024
 constexpr float kQScale = 0.125f * 1.44269504088896341f;  // log2(e) / sqrt(64)
 // Unsplit launches over sequences of at most this many rows run 128-query
-// workgroups of eight waves (two per SIMD, as four-wave workgroups four to a
-// CU give): a 12-view local layer (144 x 866) 259.6-265.4 -> 252.8-258.1
-// us, bits unchanged.  The global layer (10,392 rows) measured 1% slower in
+// workgroups of eight waves (two to a CU: four waves per SIMD, as four-wave
+// workgroups four to a CU give, with half the K/V staging per query): a
+// 12-view local layer (144 x 866) 259.6-265.4 -> 252.8-258.1 us, bits
+// unchanged.  The global layer (10,392 rows) measured 1% slower in
 // that form when it ran unsplit.
 constexpr int kWideTileMaxN = 1024;
 static_assert(PITCH % 4 == 0 && (PITCH / 4) % 2 == 1, "pitch 4 x odd");
